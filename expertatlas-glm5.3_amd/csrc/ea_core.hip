@@ -1,0 +1,236 @@
+// Library set-up, status words, trellis dequantisation, the router's top-8 and the shared expert's SwiGLU.
+#include <hip/hip_runtime.h>
+
+#include <mutex>
+#include <vector>
+
+#include "ea_device.hpp"
+#include "ea_host.hpp"
+
+namespace ea {
+
+namespace {
+std::mutex g_mu;
+std::vector<DevCtx> g_ctx;
+}  // namespace
+
+DevCtx* ctx() {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0) return nullptr;
+    std::lock_guard<std::mutex> lk(g_mu);
+    if ((size_t)dev >= g_ctx.size()) return nullptr;
+    return &g_ctx[dev];
+}
+
+// ---- dequantisation -------------------------------------------------------------------------------------------
+// One block a tile, one thread a value: thread (k, n) of the tile finds its stream value p by inverting the
+// placement (decode.cuh:134-136), reads the 16-bit window from two words and writes W[k][n] (coalesced rows).
+template <int CB>
+__global__ void __launch_bounds__(256) unpack_kernel(const uint32_t* __restrict__ T, uint16_t* __restrict__ W, int N,
+                                                     int k2, int64_t stride_k, int64_t stride_nb) {
+    const int nt = blockIdx.x, kt = blockIdx.y;
+    const int k = threadIdx.x >> 4, n = threadIdx.x & 15;
+    const int L = 4 * (n & 7) + ((k & 7) >> 1);
+    const int p = 8 * L + 4 * (n >> 3) + (k & 1) + 2 * (k >> 3);
+    const int TW = 4 * k2, NB = 128 * k2;
+    const int e = (k2 & 1) ? ((p + 1) * k2 - ((p + 1) & 1)) / 2 : (p + 1) * (k2 / 2);
+    const int b = (e - 16 + NB) % NB;
+    const uint32_t* tile = T + kt * stride_k + (nt >> 3) * stride_nb + (nt & 7) * TW;
+    const uint64_t q = ((uint64_t)tile[b >> 5] << 32) | tile[((b >> 5) + 1) % TW];
+    const uint32_t s = (uint32_t)(q >> (48 - (b & 31))) & 0xffffu;
+    W[(size_t)(kt * 16 + k) * N + nt * 16 + n] = __builtin_bit_cast(uint16_t, cb_value<CB>(s));
+}
+
+// ---- router top-8 ----------------------------------------------------------------------------------------------
+// One block a row, a thread an expert (E = 256). Eight rounds of a block arg-max over choice = sigmoid + bias, the
+// lower id winning ties; the winner's choice becomes -inf (native_ops.cu:1015-1068).
+__global__ void __launch_bounds__(256) topk8_kernel(const float* __restrict__ logits, const float* __restrict__ bias,
+                                                    int32_t* __restrict__ pick, float* __restrict__ wts, float scale,
+                                                    uint8_t* __restrict__ log) {
+    __shared__ float s_val[4];
+    __shared__ int s_idx[4];
+    __shared__ float s_wts[8];
+    __shared__ int s_pick[8];
+    const int r = blockIdx.x, t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const float score = 1.0f / (expf_path(0.0f - logits[(size_t)r * 256 + t]) + 1.0f);
+    float choice = score + bias[t];
+    for (int k = 0; k < 8; ++k) {
+        float v = choice;
+        int i = t;
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) {
+            const float ov = __shfl_xor(v, o, 64);
+            const int oi = __shfl_xor(i, o, 64);
+            if (ov > v || (ov == v && oi < i)) {
+                v = ov;
+                i = oi;
+            }
+        }
+        if (lane == 0) {
+            s_val[wave] = v;
+            s_idx[wave] = i;
+        }
+        __syncthreads();
+        float bv = s_val[0];
+        int bi = s_idx[0];
+#pragma unroll
+        for (int w = 1; w < 4; ++w)
+            if (s_val[w] > bv || (s_val[w] == bv && s_idx[w] < bi)) {
+                bv = s_val[w];
+                bi = s_idx[w];
+            }
+        __syncthreads();  // every thread has read the winners before the next round writes them
+        if (t == bi) {
+            s_pick[k] = bi;
+            s_wts[k] = score;
+            choice = -__builtin_inff();
+        }
+    }
+    __syncthreads();
+    if (t < 8) {
+        float total = 0.0f;
+        for (int k = 0; k < 8; ++k) total = total + s_wts[k];
+        pick[(size_t)r * 8 + t] = s_pick[t];
+        wts[(size_t)r * 8 + t] = s_wts[t] / (total + 1e-20f) * scale;
+        if (log) log[(size_t)r * 8 + t] = (uint8_t)s_pick[t];
+    }
+}
+
+// ---- SwiGLU of the shared expert ------------------------------------------------------------------------------
+__global__ void __launch_bounds__(256) swiglu2_kernel(const uint16_t* __restrict__ g, const uint16_t* __restrict__ u,
+                                                      uint16_t* __restrict__ out, size_t n) {
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256) {
+        const float gv = bf2f(g[i]);
+        const float s = bf16r(gv / (expf_path(0.0f - gv) + 1.0f));
+        out[i] = f2bf(s * bf2f(u[i]));
+    }
+}
+
+}  // namespace ea
+
+using namespace ea;
+
+extern "C" {
+
+const char* ea_strerror(int s) {
+    switch (s) {
+        case EA_OK: return "ok";
+        case EA_BAD_ROT_IN: return "BadRotIn: rot_in needs 1 to 3 jobs and K a multiple of 128";
+        case EA_UNPORTED_LINEAR_WALK: return "UnportedLinearWalk: only loads with bits 1 and 2 set are built";
+        case EA_UNEVEN_K_SPLIT: return "UnevenKSplit: K / 16 must split evenly over SK * WK";
+        case EA_UNPORTED_LINEAR_VARIANT: return "UnportedLinearVariant: no linear kernel for this width / codebook / warps";
+        case EA_TOO_MANY_EXPERTS: return "TooManyExperts: at most 4096 experts";
+        case EA_TOO_MANY_SLOTS: return "TooManySlots: at most 32 slots a row";
+        case EA_GROUP_SHARED_MEMORY: return "GroupSharedMemory: the picks do not fit in shared memory";
+        case EA_UNEVEN_SPLIT: return "UnevenSplit: K and N must split evenly over the tile setting";
+        case EA_BAD_ROW_STRIDE: return "BadRowStride: the trellis row stride is below N / 16";
+        case EA_UNPORTED_GROUPED_VARIANT: return "UnportedGroupedVariant: no grouped kernel for this tile setting";
+        case EA_BAD_WIDTH: return "BadWidth: the width must be a multiple of 128";
+        case EA_SCRATCH_TOO_SMALL: return "ScratchTooSmall: more rows than the scratch holds";
+        case EA_INVALID: return "Invalid: conflicting options";
+        case EA_NOT_GROUPABLE: return "NotGroupable: 1 to 3 layers of one K, width, codebook and warps, 1 to 128 rows";
+        case EA_HIP_FAILED: return "HIP call failed";
+        case EA_OUT_OF_DEVICE_MEMORY: return "out of device memory";
+        case EA_NOT_INITIALIZED: return "ea_init was not called on this device";
+        case EA_BAD_ARGUMENT: return "bad argument";
+        case EA_UNSUPPORTED_WIDTH: return "an expert width (K2) or codebook this build has no decoder for";
+        default: return "unknown status";
+    }
+}
+
+int ea_init(int device) {
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || device < 0 || device >= n) return EA_BAD_ARGUMENT;
+    int r = hip_status(hipSetDevice(device));
+    if (r) return r;
+    std::lock_guard<std::mutex> lk(g_mu);
+    if ((size_t)device >= g_ctx.size()) g_ctx.resize(device + 1);
+    DevCtx& c = g_ctx[device];
+    if (c.ready) return EA_OK;
+    hipDeviceProp_t p;
+    r = hip_status(hipGetDeviceProperties(&p, device));
+    if (r) return r;
+    c.device = device;
+    c.cus = p.multiProcessorCount;
+    c.lds_optin = p.sharedMemPerBlock;
+    r = hip_status(hipMalloc(&c.status, 256));
+    if (r) return r;
+    r = hip_status(hipMemset(c.status, 0, 256));
+    if (r) return r;
+    r = hip_status(hipDeviceSynchronize());
+    if (r) return r;
+    c.ready = true;
+    return EA_OK;
+}
+
+int ea_fini(void) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    for (auto& c : g_ctx)
+        if (c.ready) {
+            hipSetDevice(c.device);
+            hipFree(c.status);
+            c.status = nullptr;
+            c.ready = false;
+        }
+    return EA_OK;
+}
+
+int ea_device_status(int* code) {
+    EA_REQUIRE_CTX(c);
+    if (!code) return EA_BAD_ARGUMENT;
+    int r = hip_status(hipMemcpy(code, c->status, sizeof(int), hipMemcpyDeviceToHost));
+    if (r) return r;
+    return hip_status(hipMemset(c->status, 0, sizeof(int)));
+}
+
+static int unpack_launch(ea_stream_t stream, const void* t, void* w, uint32_t kdim, uint32_t n, uint32_t k2,
+                         uint32_t cb, int64_t stride_k, int64_t stride_nb) {
+    EA_REQUIRE_CTX(c);
+    if (!t || !w || kdim % 16 || n % 16 || kdim == 0 || n == 0) return EA_BAD_ARGUMENT;
+    if (k2 < 2 || k2 > 16 || cb > 2) return EA_UNSUPPORTED_WIDTH;
+    dim3 grid(n / 16, kdim / 16);
+    auto T = static_cast<const uint32_t*>(t);
+    auto W = static_cast<uint16_t*>(w);
+    hipStream_t s = as_stream(stream);
+    if (cb == 0) unpack_kernel<0><<<grid, 256, 0, s>>>(T, W, (int)n, (int)k2, stride_k, stride_nb);
+    else if (cb == 1) unpack_kernel<1><<<grid, 256, 0, s>>>(T, W, (int)n, (int)k2, stride_k, stride_nb);
+    else unpack_kernel<2><<<grid, 256, 0, s>>>(T, W, (int)n, (int)k2, stride_k, stride_nb);
+    return launched();
+}
+
+// The expert layout is the strided one with stride_k = (N / 16) * TW and stride_nb = 8 * TW.
+int ea_dequant(ea_stream_t stream, const void* trellis, void* w, uint32_t K, uint32_t N, uint32_t k2, uint32_t cb) {
+    const int64_t tw = 4 * (int64_t)k2;
+    return unpack_launch(stream, trellis, w, K, N, k2, cb, (int64_t)(N / 16) * tw, 8 * tw);
+}
+
+int ea_exl3_unpack(ea_stream_t stream, const void* t, void* w, uint32_t kdim, uint32_t n, uint32_t k2, uint32_t cb,
+                   int64_t stride_k, int64_t stride_nb) {
+    // every K2 in 2..16 and every codebook (the reference builds four of these pairs, exl3.zig:40)
+    if (k2 < 2 || k2 > 16 || cb > 2) return EA_UNPORTED_LINEAR_VARIANT;
+    return unpack_launch(stream, t, w, kdim, n, k2, cb, stride_k, stride_nb);
+}
+
+int ea_topk8(ea_stream_t stream, const float* logits, const float* bias, int32_t* pick, float* wts, uint32_t rows,
+             float scale, uint8_t* log) {
+    EA_REQUIRE_CTX(c);
+    if (!logits || !bias || !pick || !wts) return EA_BAD_ARGUMENT;
+    if (rows == 0) return EA_OK;
+    topk8_kernel<<<rows, 256, 0, as_stream(stream)>>>(logits, bias, pick, wts, scale, log);
+    return launched();
+}
+
+int ea_swiglu2(ea_stream_t stream, const void* g, const void* u, void* out, uint32_t rows, uint32_t width) {
+    EA_REQUIRE_CTX(c);
+    if (!g || !u || !out) return EA_BAD_ARGUMENT;
+    const size_t n = (size_t)rows * width;
+    if (n == 0) return EA_OK;
+    size_t blocks = (n + 255) / 256;
+    if (blocks > (size_t)c->cus * 16) blocks = (size_t)c->cus * 16;
+    swiglu2_kernel<<<(unsigned)blocks, 256, 0, as_stream(stream)>>>(static_cast<const uint16_t*>(g),
+                                                                   static_cast<const uint16_t*>(u),
+                                                                   static_cast<uint16_t*>(out), n);
+    return launched();
+}
+
+}  // extern "C"

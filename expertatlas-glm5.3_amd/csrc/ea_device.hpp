@@ -1,0 +1,171 @@
+// Device helpers shared by the gfx950 kernels: number formats, the path's exp, EXL3 trellis decode into
+// MFMA operand registers, and the 128-point Walsh-Hadamard transform on a 64-lane wavefront.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace ea {
+
+typedef _Float16 h2v __attribute__((ext_vector_type(2)));
+typedef _Float16 h4v __attribute__((ext_vector_type(4)));
+typedef _Float16 h8v __attribute__((ext_vector_type(8)));
+typedef float f4v __attribute__((ext_vector_type(4)));
+
+constexpr float HAD_SCALE = 0.08838834764831845f;  // 1 / sqrt(128) as fp32 (decode.cuh:163)
+
+enum Codebook : int { CB_3INST = 0, CB_MCG = 1, CB_MUL1 = 2 };
+enum DType : int { F16 = 0, BF16 = 1, F32 = 2 };
+
+// ---- number formats -------------------------------------------------------------------------------------------
+
+// An fp32 value the compiler must materialise as it stands: stops it fusing the multiply that made the value into
+// a following fp16 conversion (v_fma_mixlo_f16 rounds the exact product once, not the fp32 product).
+__device__ __forceinline__ float materialise(float x) {
+    asm volatile("" : "+v"(x));
+    return x;
+}
+
+__device__ __forceinline__ float h2f(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
+// fp32 -> fp16, round to nearest even, from the fp32 value itself.
+__device__ __forceinline__ uint16_t f2h(float f) { return __builtin_bit_cast(uint16_t, (_Float16)materialise(f)); }
+__device__ __forceinline__ float bf2f(uint16_t b) { return __builtin_bit_cast(float, (uint32_t)b << 16); }
+__device__ __forceinline__ uint16_t f2bf(float f) {
+    uint32_t u = __builtin_bit_cast(uint32_t, f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+__device__ __forceinline__ float bf16r(float x) { return bf2f(f2bf(x)); }
+
+// One element of an activation array of dtype dt as fp32.
+__device__ __forceinline__ float load_act(const void* p, int dt, size_t i) {
+    if (dt == F32) return static_cast<const float*>(p)[i];
+    const uint16_t v = static_cast<const uint16_t*>(p)[i];
+    return dt == BF16 ? bf2f(v) : h2f(v);
+}
+__device__ __forceinline__ void store_act(void* p, int dt, size_t i, float v) {
+    if (dt == F32) static_cast<float*>(p)[i] = v;
+    else static_cast<uint16_t*>(p)[i] = dt == BF16 ? f2bf(v) : f2h(v);
+}
+
+// The path's exp: Cody & Waite reduction x = n ln2 + r, a degree-7 Taylor polynomial by Horner with fma, 2^n by
+// exponent scaling. Only IEEE fma / add / multiply / ldexp, so the CPU checker computes the same bits.
+__device__ __forceinline__ float expf_path(float x) {
+    if (x != x) return x;
+    if (x > 88.72283935546875f) return __builtin_inff();
+    if (x < -103.972084045410156f) return 0.0f;
+    const float n = __builtin_rintf(x * 1.44269502162933349609f);
+    float r = __builtin_fmaf(-n, 0.693145751953125f, x);
+    r = __builtin_fmaf(-n, 1.42860682030941723212e-06f, r);
+    float p = 1.98412698412698412e-04f;
+    p = __builtin_fmaf(p, r, 1.38888888888888889e-03f);
+    p = __builtin_fmaf(p, r, 8.33333333333333333e-03f);
+    p = __builtin_fmaf(p, r, 4.16666666666666667e-02f);
+    p = __builtin_fmaf(p, r, 1.66666666666666667e-01f);
+    p = __builtin_fmaf(p, r, 0.5f);
+    p = __builtin_fmaf(p, r, 1.0f);
+    p = __builtin_fmaf(p, r, 1.0f);
+    const int ni = (int)n;
+    if (ni < -125) return __builtin_ldexpf(__builtin_ldexpf(p, ni + 64), -64);
+    return __builtin_ldexpf(p, ni);
+}
+
+// ---- EXL3 trellis -------------------------------------------------------------------------------------------
+// A 16x16 tile is a circular big-endian bit stream of 128 * K2 bits in 4 * K2 words; value p's 16-bit state is
+// stream bits [E(p) - 16, E(p)); value p = 8 L + j sits at row 2 (L & 3) + (j & 1) + 8 ((j >> 1) & 1), column
+// (L >> 2) + 8 (j >> 2) of the tile (decode.cuh:16-136).
+
+template <int K2>
+__host__ __device__ constexpr int stream_end(int p) {
+    return (K2 & 1) ? ((p + 1) * K2 - ((p + 1) & 1)) / 2 : (p + 1) * (K2 / 2);
+}
+
+// Codebook value of one 16-bit state as fp16 (decode.cuh:86-120). The state's bits above 15 are ignored.
+template <int CB>
+__device__ __forceinline__ _Float16 cb_value(uint32_t s) {
+    s &= 0xffffu;
+    if constexpr (CB == CB_MUL1) {
+        const uint32_t x = s * 0x83DCD12Du;
+        const uint32_t h = __builtin_amdgcn_udot4(x, 0x01010101u, 0x6400u, false);  // 1024 + byte sum, fp16 bits
+        return __builtin_fmaf16(__builtin_bit_cast(_Float16, (uint16_t)h), __builtin_bit_cast(_Float16, (uint16_t)0x1eee),
+                                __builtin_bit_cast(_Float16, (uint16_t)0xc931));
+    } else {
+        uint32_t x = (CB == CB_MCG) ? s * 0xCBAC1FEDu : s * 89226354u + 64248484u;
+        x = (x & 0x8FFF8FFFu) ^ 0x3B603B60u;
+        return __builtin_bit_cast(_Float16, (uint16_t)(x & 0xffffu)) + __builtin_bit_cast(_Float16, (uint16_t)(x >> 16));
+    }
+}
+
+// A lane's view of four consecutive stream values p0 .. p0 + 3 (p0 even) of a tile, for K2 <= 10: their four
+// windows lie inside the 32 stream bits that start at the first window, so one funnel shift of two words gives
+// all four. Lane constants: the two word indices and the shift.
+struct Quad {
+    int wa, wb, sh;
+};
+
+template <int K2>
+__host__ __device__ constexpr Quad quad_of(int p0) {
+    constexpr int TW = 4 * K2, NB = 128 * K2;
+    const int b0 = stream_end<K2>(p0) - 16 + NB;  // first window start, made positive
+    const int a = (b0 - 1) >> 5;                  // word pair (a, a + 1) holds bits [32a, 32a + 64) with b0 - 32a in 1..32
+    return Quad{a % TW, (a + 1) % TW, 32 - (b0 - 32 * a)};
+}
+
+// The four values from the lane's two words.
+template <int K2, int CB>
+__device__ __forceinline__ h4v decode_quad(uint32_t wa, uint32_t wb, int sh) {
+    static_assert(K2 >= 2 && K2 <= 10, "the four windows must fit in 32 stream bits");
+    const uint32_t seg = __builtin_amdgcn_alignbit(wa, wb, (uint32_t)sh);
+    constexpr int e0 = stream_end<K2>(0);
+    h4v v;
+    v[0] = cb_value<CB>(seg >> 16);
+    v[1] = cb_value<CB>(seg >> (16 - (stream_end<K2>(1) - e0)));
+    v[2] = cb_value<CB>(seg >> (16 - (stream_end<K2>(2) - e0)));
+    v[3] = cb_value<CB>(seg >> (16 - (stream_end<K2>(3) - e0)));
+    return v;
+}
+
+// MFMA 16x16x16 f16 B-operand layout for one tile: lane l holds B[k'][n] for n = l & 15 and k' = 4 (l >> 4) + i.
+// With g = l >> 4 and tile lane L = 4 (n & 7) + g, h = n >> 3, the stream values p0 = 8 L + 4 h + i sit at rows
+// k = 2 g + (i & 1) + 8 (i >> 1) of column n. So the lane decodes four consecutive values, and the A operand
+// (activations) must use the same k permutation: lane l of A holds rows 2g, 2g + 1, 2g + 8, 2g + 9.
+__host__ __device__ constexpr int mfma_lane_p0(int lane) {
+    const int n = lane & 15, g = (lane >> 4) & 3;
+    return 8 * (4 * (n & 7) + g) + 4 * (n >> 3);
+}
+
+// ---- Walsh-Hadamard over 128 values on a wavefront ------------------------------------------------------------
+// Lane j holds values 2j and 2j + 1. Levels run over index bits 0, 1, .., 6 in that order, each pair becoming
+// (lower + upper, lower - upper) in fp32: the reference's butterflies (decode.cuh:146-161), so the same bits.
+__device__ __forceinline__ void fwht128_w64(float& v0, float& v1, int lane) {
+    const float a = v0 + v1, b = v0 - v1;
+    v0 = a;
+    v1 = b;
+#pragma unroll
+    for (int m = 1; m < 64; m <<= 1) {
+        const float o0 = __shfl_xor(v0, m, 64), o1 = __shfl_xor(v1, m, 64);
+        const bool up = lane & m;
+        v0 = up ? o0 - v0 : v0 + o0;
+        v1 = up ? o1 - v1 : v1 + o1;
+    }
+}
+
+// 32-lane half-wave variant: lane j (0..31 within its half) holds values 4j .. 4j + 3.
+__device__ __forceinline__ void fwht128_h32(float (&v)[4], int lane) {
+    const float a = v[0] + v[1], b = v[0] - v[1], c = v[2] + v[3], d = v[2] - v[3];
+    v[0] = a + c;
+    v[1] = b + d;
+    v[2] = a - c;
+    v[3] = b - d;
+#pragma unroll
+    for (int m = 1; m < 32; m <<= 1) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const float o = __shfl_xor(v[j], m, 32);
+            v[j] = (lane & m) ? o - v[j] : v[j] + o;
+        }
+    }
+}
+
+}  // namespace ea

@@ -1,0 +1,487 @@
+// Routed experts, decode path: grouping, per-pair input rotation, the grouped EXL3 GEMV on MFMA, the gate/up
+// epilogue (FWHT, svh, SwiGLU, suh_d, FWHT) and the down epilogue with the slot-ordered combine.
+//
+// Semantics follow exl3_experts.cu / experts_grouped.cuh of the reference; the work decomposition is this
+// build's own: wave64 lanes decode trellis values straight into v_mfma_f32_16x16x32_f16 B operands (see
+// ea_device.hpp: mfma_lane_p0), and the wavefronts of a block split the K range and are summed in wave order.
+#include <hip/hip_runtime.h>
+
+#include "ea_device.hpp"
+#include "ea_experts.hpp"
+#include "ea_host.hpp"
+
+namespace ea {
+
+// ---- grouping ---------------------------------------------------------------------------------------------------
+constexpr int GROUP_THREADS = 1024;
+constexpr int GROUP_PER_THREAD = 4;
+
+// Distinct experts (< E) in id order; members[u][m] = row * 32 + slot in row order, -1 after the last
+// (exl3_experts.cu:36-90).
+__global__ void __launch_bounds__(GROUP_THREADS) group_kernel(const int* __restrict__ pick, int* __restrict__ uids,
+                                                              int* __restrict__ ucount, int* __restrict__ members,
+                                                              int R, int slots, int E, int maxm) {
+    extern __shared__ int sh_pick[];
+    __shared__ int wave_tot[GROUP_THREADS / 64];
+    const int n = R * slots;
+    for (int i = threadIdx.x; i < n; i += GROUP_THREADS) sh_pick[i] = pick[i];
+    __syncthreads();
+    int cnt[GROUP_PER_THREAD];
+    int used = 0;
+#pragma unroll
+    for (int q = 0; q < GROUP_PER_THREAD; ++q) {
+        const int e = threadIdx.x * GROUP_PER_THREAD + q;
+        int c = 0;
+        if (e < E)
+            for (int i = 0; i < n; ++i) c += sh_pick[i] == e;
+        cnt[q] = c;
+        used += c > 0;
+    }
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    int inc = used;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const int v = __shfl_up(inc, o, 64);
+        if (lane >= o) inc += v;
+    }
+    if (lane == 63) wave_tot[wave] = inc;
+    __syncthreads();
+    if (wave == 0) {
+        const int v = lane < GROUP_THREADS / 64 ? wave_tot[lane] : 0;
+        int s = v;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const int x = __shfl_up(s, o, 64);
+            if (lane >= o) s += x;
+        }
+        if (lane < GROUP_THREADS / 64) wave_tot[lane] = s - v;
+        if (lane == GROUP_THREADS / 64 - 1) ucount[0] = s;
+    }
+    __syncthreads();
+    int place = wave_tot[wave] + inc - used;
+#pragma unroll
+    for (int q = 0; q < GROUP_PER_THREAD; ++q) {
+        if (cnt[q] == 0) continue;
+        const int e = threadIdx.x * GROUP_PER_THREAD + q;
+        uids[place] = e;
+        int j = 0;
+        for (int i = 0; i < n && j < maxm; ++i)
+            if (sh_pick[i] == e) members[place * maxm + j++] = (i / slots) * 32 + (i % slots);
+        for (; j < maxm; ++j) members[place * maxm + j] = -1;
+        ++place;
+    }
+}
+
+// ---- per-pair input rotation ------------------------------------------------------------------------------------
+// Block (pair p, group of four 128-blocks of K, matrix): a wave a 128-block; lane j holds values 2j, 2j + 1.
+// out[p] = fp16((x[row] * suh[e]) @ H * HAD_SCALE) (exl3_experts.cu:116-134).
+__global__ void __launch_bounds__(256) rot_in_kernel(const void* __restrict__ x, int x_dtype, int x_stride,
+                                                     const int* __restrict__ pick, const uint16_t* __restrict__ suh0,
+                                                     const uint16_t* __restrict__ suh1, uint16_t* __restrict__ out0,
+                                                     uint16_t* __restrict__ out1, int K, int slots, int E) {
+    const int p = blockIdx.x, mat = blockIdx.z;
+    const int blk = blockIdx.y * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (blk * 128 >= K) return;
+    const int e = pick[p];
+    if (e < 0 || e >= E) return;
+    const int row = p / slots;
+    const int k = blk * 128 + 2 * lane;
+    const uint16_t* suh = (mat ? suh1 : suh0) + (size_t)e * K + k;
+    const size_t xi = (size_t)row * x_stride + k;
+    float v0 = load_act(x, x_dtype, xi) * h2f(suh[0]);
+    float v1 = load_act(x, x_dtype, xi + 1) * h2f(suh[1]);
+    fwht128_w64(v0, v1, lane);
+    uint16_t* o = (mat ? out1 : out0) + (size_t)p * K + k;
+    *reinterpret_cast<uint32_t*>(o) = (uint32_t)f2h(v0 * HAD_SCALE) | ((uint32_t)f2h(v1 * HAD_SCALE) << 16);
+}
+
+// ---- the grouped GEMV / GEMM core ---------------------------------------------------------------------------
+// acc[j] += A (16 member rows x the K range) @ W_q tile column nt0 + j, two k tiles a step (16x16x32 MFMA) and one
+// 16x16x16 step for an odd tail. xrow: this lane's member row (lane & 15) of fp16 inputs, or nullptr (zeros).
+template <int CB, int K2, int NTW>
+__device__ __forceinline__ void wave_tiles(const uint32_t* __restrict__ T, int ns, int kt0, int nkt, int nt0,
+                                           const uint16_t* __restrict__ xrow, int lane, f4v (&acc)[NTW]) {
+    constexpr int TW = 4 * K2;
+    const Quad q = quad_of<K2>(mfma_lane_p0(lane));
+    const int g = (lane >> 4) & 3;
+    const size_t kstride = (size_t)ns * TW;
+    const uint32_t* base = T + ((size_t)kt0 * ns + nt0) * TW;
+    int kt = 0;
+    for (; kt + 2 <= nkt; kt += 2) {
+        h8v a = {0, 0, 0, 0, 0, 0, 0, 0};
+        if (xrow) {
+            const uint16_t* xk = xrow + (kt0 + kt) * 16 + 2 * g;
+            const uint32_t a0 = *reinterpret_cast<const uint32_t*>(xk);
+            const uint32_t a1 = *reinterpret_cast<const uint32_t*>(xk + 8);
+            const uint32_t a2 = *reinterpret_cast<const uint32_t*>(xk + 16);
+            const uint32_t a3 = *reinterpret_cast<const uint32_t*>(xk + 24);
+            typedef uint32_t u4v __attribute__((ext_vector_type(4)));
+            const u4v au = {a0, a1, a2, a3};
+            a = __builtin_bit_cast(h8v, au);
+        }
+        const uint32_t* t0 = base + (size_t)kt * kstride;
+#pragma unroll
+        for (int j = 0; j < NTW; ++j) {
+            const uint32_t* ta = t0 + j * TW;
+            const uint32_t* tb = ta + kstride;
+            const h4v b0 = decode_quad<K2, CB>(ta[q.wa], ta[q.wb], q.sh);
+            const h4v b1 = decode_quad<K2, CB>(tb[q.wa], tb[q.wb], q.sh);
+            const h8v b = {b0[0], b0[1], b0[2], b0[3], b1[0], b1[1], b1[2], b1[3]};
+            acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, acc[j], 0, 0, 0);
+        }
+    }
+    if (kt < nkt) {
+        h4v a = {0, 0, 0, 0};
+        if (xrow) {
+            const uint16_t* xk = xrow + (kt0 + kt) * 16 + 2 * g;
+            typedef uint32_t u2v __attribute__((ext_vector_type(2)));
+            const u2v au = {*reinterpret_cast<const uint32_t*>(xk), *reinterpret_cast<const uint32_t*>(xk + 8)};
+            a = __builtin_bit_cast(h4v, au);
+        }
+        const uint32_t* t0 = base + (size_t)kt * kstride;
+#pragma unroll
+        for (int j = 0; j < NTW; ++j) {
+            const uint32_t* ta = t0 + j * TW;
+            const h4v b = decode_quad<K2, CB>(ta[q.wa], ta[q.wb], q.sh);
+            acc[j] = __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, acc[j], 0, 0, 0);
+        }
+    }
+}
+
+__device__ __forceinline__ void record_error(int* status, int code) { atomicCAS(status, 0, code); }
+
+// Block (expert u, n block of NTW tiles, (matrix, split, member tile)): NW waves split the split's k tiles in
+// equal consecutive ranges, their partial sums added in wave order into Z[mat][split][pair][n]
+// (experts_grouped.cuh:214-313). K2 comes from the expert's table entry at run time.
+template <int CB, int LO, int HI, int NTW, int NW>
+__global__ void __launch_bounds__(NW * 64) grouped_kernel(
+    const uint16_t* __restrict__ X0, const uint16_t* __restrict__ X1, const int64_t* __restrict__ TP0,
+    const int64_t* __restrict__ TP1, const int* __restrict__ K2_0, const int* __restrict__ K2_1,
+    const int* __restrict__ uids, const int* __restrict__ ucount, const int* __restrict__ members,
+    float* __restrict__ Z, int K, int N, int P, int SK, int maxm, int slots, int NS, int* __restrict__ status) {
+    const int u = blockIdx.x;
+    if (u >= ucount[0]) return;
+    const int MT = (maxm + 15) / 16;
+    const int mtile = blockIdx.z % MT;
+    const int split = (blockIdx.z / MT) % SK;
+    const int mat = blockIdx.z / MT / SK;
+    const uint16_t* X = mat ? X1 : X0;
+    const int e = uids[u];
+    const uint32_t* T = reinterpret_cast<const uint32_t*>(mat ? TP1[e] : TP0[e]);
+    const int k2 = mat ? K2_1[e] : K2_0[e];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int KT = K >> 4, ns = NS > 0 ? NS : (N >> 4);
+
+    __shared__ int rows_sh[16];
+    if (threadIdx.x < 16) {
+        const int m = mtile * 16 + threadIdx.x;
+        const int code = m < maxm ? members[u * maxm + m] : -1;
+        rows_sh[threadIdx.x] = code >= 0 ? (code >> 5) * slots + (code & 31) : -1;
+    }
+    __syncthreads();
+    if (rows_sh[0] < 0) return;  // members are packed first: this member tile is empty
+    const int r = rows_sh[lane & 15];
+    const uint16_t* xrow = r >= 0 ? X + (size_t)r * K : nullptr;
+
+    const int per_split = KT / SK, per_wave = per_split / NW;
+    const int kt0 = split * per_split + wave * per_wave;
+    const int nt0 = blockIdx.y * NTW;
+
+    f4v acc[NTW];
+#pragma unroll
+    for (int j = 0; j < NTW; ++j) acc[j] = f4v{0.f, 0.f, 0.f, 0.f};
+
+    bool ok = true;
+    switch (k2) {
+#define EA_CASE(K2_)                                                                             \
+    case K2_:                                                                                    \
+        if constexpr (K2_ >= LO && K2_ <= HI)                                                    \
+            wave_tiles<CB, K2_, NTW>(T, ns, kt0, per_wave, nt0, xrow, lane, acc);                \
+        else                                                                                     \
+            ok = false;                                                                          \
+        break;
+        EA_CASE(2) EA_CASE(3) EA_CASE(4) EA_CASE(5) EA_CASE(6) EA_CASE(7) EA_CASE(8) EA_CASE(9) EA_CASE(10)
+#undef EA_CASE
+        default:
+            ok = false;
+    }
+    if (!ok) {
+        if (threadIdx.x == 0) record_error(status, DEV_UNSUPPORTED_WIDTH);
+        return;
+    }
+
+    // wave partials through LDS, added in wave order; lane l holds D[4 (l >> 4) + i][l & 15] of each tile
+    __shared__ float red[NW][16][NTW * 16];
+#pragma unroll
+    for (int j = 0; j < NTW; ++j)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) red[wave][4 * (lane >> 4) + i][j * 16 + (lane & 15)] = acc[j][i];
+    __syncthreads();
+    for (int idx = threadIdx.x; idx < 16 * NTW * 16; idx += NW * 64) {
+        const int row = idx / (NTW * 16), col = idx % (NTW * 16);
+        const int rr = rows_sh[row];
+        if (rr < 0) continue;
+        float s = red[0][row][col];
+#pragma unroll
+        for (int w = 1; w < NW; ++w) s += red[w][row][col];
+        Z[(((size_t)mat * SK + split) * P + rr) * N + nt0 * 16 + col] = s;
+    }
+}
+
+// ---- gate/up epilogue -----------------------------------------------------------------------------------------
+// Wave (pair p, 128-block): splits summed in order, FWHT, * HAD_SCALE * svh, SwiGLU (act_mode 0: bf16 roundings,
+// 1: fp32; limit clamps), * suh_d, FWHT, xd = fp16(* HAD_SCALE) (exl3_experts.cu:142-184).
+__global__ void __launch_bounds__(64) gateup_epilogue_kernel(const float* __restrict__ Z, const int* __restrict__ pick,
+                                                             const uint16_t* __restrict__ svh_g,
+                                                             const uint16_t* __restrict__ svh_u,
+                                                             const uint16_t* __restrict__ suh_d,
+                                                             uint16_t* __restrict__ xd, int P, int N, int SK, int E,
+                                                             float limit, int act_mode) {
+    const int p = blockIdx.x, blk = blockIdx.y, lane = threadIdx.x;
+    const int e = pick[p];
+    if (e < 0 || e >= E) return;
+    const int n = blk * 128 + 2 * lane;
+    float g[2], u[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        float sg = 0.f, su = 0.f;
+        for (int s = 0; s < SK; ++s) {
+            sg += Z[((size_t)(0 * SK + s) * P + p) * N + n + j];
+            su += Z[((size_t)(1 * SK + s) * P + p) * N + n + j];
+        }
+        g[j] = sg;
+        u[j] = su;
+    }
+    fwht128_w64(g[0], g[1], lane);
+    fwht128_w64(u[0], u[1], lane);
+    float v[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const size_t at = (size_t)e * N + n + j;
+        float act;
+        if (act_mode == 0) {
+            const float gg = fminf(bf16r(g[j] * HAD_SCALE * h2f(svh_g[at])), limit);
+            const float uu = fminf(fmaxf(bf16r(u[j] * HAD_SCALE * h2f(svh_u[at])), -limit), limit);
+            act = bf16r(bf16r(gg / (1.f + expf_path(-gg))) * uu);
+        } else {
+            const float gg = fminf(g[j] * HAD_SCALE * h2f(svh_g[at]), limit);
+            const float uu = fminf(fmaxf(u[j] * HAD_SCALE * h2f(svh_u[at]), -limit), limit);
+            act = gg / (1.f + expf_path(-gg)) * uu;
+        }
+        v[j] = act * h2f(suh_d[at]);
+    }
+    fwht128_w64(v[0], v[1], lane);
+    *reinterpret_cast<uint32_t*>(xd + (size_t)p * N + n) =
+        (uint32_t)f2h(v[0] * HAD_SCALE) | ((uint32_t)f2h(v[1] * HAD_SCALE) << 16);
+}
+
+// ---- down epilogue + combine ----------------------------------------------------------------------------------
+// Block (row r, 128-block): wave w does slots w, w + NWV, ..: y[p] = FWHT(sum of splits) * HAD_SCALE * svh_d (a slot
+// whose pick is not an expert reads y as it is); then out[r] = fma chain over the slots in order from 0
+// (exl3_experts.cu:223-268).
+constexpr int DC_WAVES = 8;
+__global__ void __launch_bounds__(DC_WAVES * 64) down_combine_kernel(
+    const float* __restrict__ Z, const int* __restrict__ pick, const uint16_t* __restrict__ svh_d, float* __restrict__ y,
+    const float* __restrict__ wts, float* __restrict__ out, int P, int D, int SK, int E, int slots) {
+    __shared__ float part[32][128];
+    const int r = blockIdx.x, blk = blockIdx.y;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int n = blk * 128 + 2 * lane;
+    for (int k = wave; k < slots; k += DC_WAVES) {
+        const int p = r * slots + k;
+        const int e = pick[p];
+        float o[2];
+        if (e >= 0 && e < E) {
+            float v[2];
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                float s = 0.f;
+                for (int q = 0; q < SK; ++q) s += Z[((size_t)q * P + p) * D + n + j];
+                v[j] = s;
+            }
+            fwht128_w64(v[0], v[1], lane);
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                o[j] = v[j] * HAD_SCALE * h2f(svh_d[(size_t)e * D + n + j]);
+                y[(size_t)p * D + n + j] = o[j];
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < 2; ++j) o[j] = y[(size_t)p * D + n + j];
+        }
+        part[k][2 * lane] = o[0];
+        part[k][2 * lane + 1] = o[1];
+    }
+    __syncthreads();
+    if (wave != 0) return;
+    float a0 = 0.f, a1 = 0.f;
+    for (int q = 0; q < slots; ++q) {
+        const float w = wts[r * slots + q];
+        a0 = __builtin_fmaf(w, part[q][2 * lane], a0);
+        a1 = __builtin_fmaf(w, part[q][2 * lane + 1], a1);
+    }
+    out[(size_t)r * D + n] = a0;
+    out[(size_t)r * D + n + 1] = a1;
+}
+
+// ---- launchers --------------------------------------------------------------------------------------------------
+
+int launch_group(hipStream_t s, const int* pick, int* uids, int* ucount, int* members, uint32_t rows, uint32_t slots,
+                 uint32_t experts, uint32_t maxm) {
+    EA_REQUIRE_CTX(c);
+    if (experts > GROUP_THREADS * GROUP_PER_THREAD) return EA_TOO_MANY_EXPERTS;
+    if (slots > 32) return EA_TOO_MANY_SLOTS;
+    const size_t smem = (size_t)rows * slots * 4;
+    if (smem + GROUP_THREADS / 64 * 4 > c->lds_optin) return EA_GROUP_SHARED_MEMORY;
+    if (!pick || !uids || !ucount || !members) return EA_BAD_ARGUMENT;
+    group_kernel<<<1, GROUP_THREADS, smem, s>>>(pick, uids, ucount, members, (int)rows, (int)slots, (int)experts,
+                                                (int)maxm);
+    return launched();
+}
+
+int launch_rot_in(hipStream_t s, const void* x, int x_dtype, uint32_t x_stride, const int* pick, const uint16_t* suh0,
+                  const uint16_t* suh1, uint16_t* out0, uint16_t* out1, uint32_t rows, uint32_t kdim, uint32_t slots,
+                  uint32_t experts) {
+    EA_REQUIRE_CTX(c);
+    if (kdim % 128 != 0) return EA_BAD_ROT_IN;
+    if (x_dtype < 0 || x_dtype > 2 || !x || !pick) return EA_BAD_ARGUMENT;
+    if (rows * slots == 0) return EA_OK;
+    dim3 grid(rows * slots, (kdim / 128 + 3) / 4, 2);
+    rot_in_kernel<<<grid, 256, 0, s>>>(x, x_dtype, (int)x_stride, pick, suh0, suh1, out0, out1, (int)kdim,
+                                       (int)slots, (int)experts);
+    return launched();
+}
+
+template <int CB, int LO, int HI>
+static void grouped_dispatch(const ea_grouped_args& a, hipStream_t s, int nw, int ntw, int* status) {
+    const int MT = (a.maxm + 15) / 16;
+    dim3 grid(a.nexp_max, a.N / (16 * ntw), a.mats * a.SK * MT);
+    auto X0 = dptr<const uint16_t>(a.x0);
+    auto X1 = dptr<const uint16_t>(a.x1);
+    auto TP0 = dptr<const int64_t>(a.tp0);
+    auto TP1 = dptr<const int64_t>(a.tp1);
+    auto B0 = dptr<const int>(a.k2_0);
+    auto B1 = dptr<const int>(a.k2_1);
+    auto U = dptr<const int>(a.uids);
+    auto UC = dptr<const int>(a.ucount);
+    auto M = dptr<const int>(a.members);
+    auto Zp = dptr<float>(a.z);
+#define EA_GL(NTW_, NW_)                                                                                          \
+    grouped_kernel<CB, LO, HI, NTW_, NW_><<<grid, NW_ * 64, 0, s>>>(X0, X1, TP0, TP1, B0, B1, U, UC, M, Zp,      \
+                                                                   (int)a.K, (int)a.N, (int)a.P, (int)a.SK,      \
+                                                                   (int)a.maxm, (int)a.slots, (int)a.ns, status)
+#define EA_GL_NW(NTW_)                 \
+    if (nw == 8) EA_GL(NTW_, 8);       \
+    else if (nw == 4) EA_GL(NTW_, 4);  \
+    else if (nw == 2) EA_GL(NTW_, 2);  \
+    else EA_GL(NTW_, 1);
+    if (ntw == 4) {
+        EA_GL_NW(4)
+    } else if (ntw == 2) {
+        EA_GL_NW(2)
+    } else {
+        EA_GL_NW(1)
+    }
+#undef EA_GL_NW
+#undef EA_GL
+}
+
+int launch_grouped(hipStream_t s, const ea_grouped_args& a) {
+    EA_REQUIRE_CTX(c);
+    // the reference's launch checks (experts.zig:141-148)
+    if (a.warps == 0 || a.nt == 0 || a.SK == 0 || a.K % (16 * a.SK * a.warps) != 0 || a.N % (16 * a.nt) != 0)
+        return EA_UNEVEN_SPLIT;
+    if (a.ns != 0 && a.ns < a.N / 16) return EA_BAD_ROW_STRIDE;
+    if (a.cb > 2 || a.mats < 1 || a.mats > 2) return EA_UNPORTED_GROUPED_VARIANT;
+    const bool only8 = a.lo == 8 && a.hi == 8;
+    if (!only8 && !(a.lo >= 2 && a.hi <= 10)) return EA_UNPORTED_GROUPED_VARIANT;
+    if (!a.x0 || !a.x1 || !a.tp0 || !a.tp1 || !a.k2_0 || !a.k2_1 || !a.uids || !a.ucount || !a.members || !a.z)
+        return EA_BAD_ARGUMENT;
+    if (a.nexp_max == 0 || a.maxm == 0) return EA_OK;
+    // this build's tiling: NTW n tiles a wave, NW waves a block splitting the split's k tiles into equal ranges
+    const uint32_t nt16 = a.N / 16, per_split = a.K / 16 / a.SK;
+    const int ntw = nt16 % 4 == 0 ? 4 : (nt16 % 2 == 0 ? 2 : 1);
+    int nw = 1;
+    for (int cand : {8, 4, 2})
+        if (per_split % cand == 0 && per_split / cand >= 2) {
+            nw = cand;
+            break;
+        }
+    if (a.cb == 1) {
+        if (only8) grouped_dispatch<1, 8, 8>(a, s, nw, ntw, c->status);
+        else grouped_dispatch<1, 2, 10>(a, s, nw, ntw, c->status);
+    } else if (a.cb == 2) {
+        grouped_dispatch<2, 2, 10>(a, s, nw, ntw, c->status);
+    } else {
+        grouped_dispatch<0, 2, 10>(a, s, nw, ntw, c->status);
+    }
+    return launched();
+}
+
+int launch_gateup_epilogue(hipStream_t s, const float* z, const int* pick, const uint16_t* svh_g,
+                           const uint16_t* svh_u, const uint16_t* suh_d, uint16_t* xd, uint32_t rows, uint32_t p,
+                           uint32_t n, uint32_t sk, uint32_t slots, uint32_t experts, float limit, uint32_t act_mode) {
+    EA_REQUIRE_CTX(c);
+    if (n % 128 != 0) return EA_BAD_WIDTH;
+    if (!z || !pick || !svh_g || !svh_u || !suh_d || !xd) return EA_BAD_ARGUMENT;
+    if (rows * slots == 0 || n == 0) return EA_OK;
+    dim3 grid(rows * slots, n / 128);
+    gateup_epilogue_kernel<<<grid, 64, 0, s>>>(z, pick, svh_g, svh_u, suh_d, xd, (int)p, (int)n, (int)sk,
+                                               (int)experts, limit, (int)act_mode);
+    return launched();
+}
+
+int launch_down_combine(hipStream_t s, const float* z, const int* pick, const uint16_t* svh_d, float* y,
+                        const float* wts, float* out, uint32_t rows, uint32_t p, uint32_t d, uint32_t sk,
+                        uint32_t slots, uint32_t experts) {
+    EA_REQUIRE_CTX(c);
+    if (slots > 32) return EA_TOO_MANY_SLOTS;
+    if (d % 128 != 0) return EA_BAD_WIDTH;
+    if (!z || !pick || !svh_d || !y || !wts || !out) return EA_BAD_ARGUMENT;
+    if (rows == 0 || d == 0) return EA_OK;
+    dim3 grid(rows, d / 128);
+    down_combine_kernel<<<grid, DC_WAVES * 64, 0, s>>>(z, pick, svh_d, y, wts, out, (int)p, (int)d, (int)sk,
+                                                       (int)experts, (int)slots);
+    return launched();
+}
+
+}  // namespace ea
+
+using namespace ea;
+
+extern "C" {
+
+int ea_experts_group(ea_stream_t stream, const int32_t* pick, int32_t* uids, int32_t* ucount, int32_t* members,
+                     uint32_t rows, uint32_t slots, uint32_t experts, uint32_t maxm) {
+    return launch_group(as_stream(stream), pick, uids, ucount, members, rows, slots, experts, maxm);
+}
+
+int ea_experts_rot_in(ea_stream_t stream, const void* x, int x_dtype, uint32_t x_stride, const int32_t* pick,
+                      const void* suh0, const void* suh1, void* out0, void* out1, uint32_t rows, uint32_t kdim,
+                      uint32_t slots, uint32_t experts) {
+    return launch_rot_in(as_stream(stream), x, x_dtype, x_stride, pick, static_cast<const uint16_t*>(suh0),
+                         static_cast<const uint16_t*>(suh1), static_cast<uint16_t*>(out0),
+                         static_cast<uint16_t*>(out1), rows, kdim, slots, experts);
+}
+
+int ea_experts_grouped(ea_stream_t stream, const ea_grouped_args* a) {
+    if (!a) return EA_BAD_ARGUMENT;
+    return launch_grouped(as_stream(stream), *a);
+}
+
+int ea_experts_gateup_epilogue(ea_stream_t stream, const float* z, const int32_t* pick, const void* svh_g,
+                               const void* svh_u, const void* suh_d, void* xd, uint32_t rows, uint32_t p, uint32_t n,
+                               uint32_t sk, uint32_t slots, uint32_t experts, float limit, uint32_t act_mode) {
+    return launch_gateup_epilogue(as_stream(stream), z, pick, static_cast<const uint16_t*>(svh_g),
+                                  static_cast<const uint16_t*>(svh_u), static_cast<const uint16_t*>(suh_d),
+                                  static_cast<uint16_t*>(xd), rows, p, n, sk, slots, experts, limit, act_mode);
+}
+
+int ea_experts_down_combine(ea_stream_t stream, const float* z, const int32_t* pick, const void* svh_d, float* y,
+                            const float* wts, float* out, uint32_t rows, uint32_t p, uint32_t d, uint32_t sk,
+                            uint32_t slots, uint32_t experts) {
+    return launch_down_combine(as_stream(stream), z, pick, static_cast<const uint16_t*>(svh_d), y, wts, out, rows, p,
+                               d, sk, slots, experts);
+}
+
+}  // extern "C"

@@ -1,0 +1,24 @@
+// Launchers of the decode-path expert kernels (ea_experts.hip), shared with the layer orchestration.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "ea_exl3.h"
+
+namespace ea {
+
+int launch_group(hipStream_t s, const int* pick, int* uids, int* ucount, int* members, uint32_t rows, uint32_t slots,
+                 uint32_t experts, uint32_t maxm);
+int launch_rot_in(hipStream_t s, const void* x, int x_dtype, uint32_t x_stride, const int* pick, const uint16_t* suh0,
+                  const uint16_t* suh1, uint16_t* out0, uint16_t* out1, uint32_t rows, uint32_t kdim, uint32_t slots,
+                  uint32_t experts);
+int launch_grouped(hipStream_t s, const ea_grouped_args& a);
+int launch_gateup_epilogue(hipStream_t s, const float* z, const int* pick, const uint16_t* svh_g,
+                           const uint16_t* svh_u, const uint16_t* suh_d, uint16_t* xd, uint32_t rows, uint32_t p,
+                           uint32_t n, uint32_t sk, uint32_t slots, uint32_t experts, float limit, uint32_t act_mode);
+int launch_down_combine(hipStream_t s, const float* z, const int* pick, const uint16_t* svh_d, float* y,
+                        const float* wts, float* out, uint32_t rows, uint32_t p, uint32_t d, uint32_t sk,
+                        uint32_t slots, uint32_t experts);
+
+}  // namespace ea

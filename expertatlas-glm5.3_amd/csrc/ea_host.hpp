@@ -1,0 +1,45 @@
+// Host-side plumbing shared by the entry points: per-device context, status mapping, launch checks.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "ea_exl3.h"
+
+namespace ea {
+
+struct DevCtx {
+    bool ready = false;
+    int device = -1;
+    int cus = 0;
+    size_t lds_optin = 0;
+    int* status = nullptr;  // device int: a kernel's recorded error (unsupported width), 0 = none
+};
+
+// The context of the current device; nullptr before ea_init on it.
+DevCtx* ctx();
+
+inline int hip_status(hipError_t e) {
+    if (e == hipSuccess) return EA_OK;
+    if (e == hipErrorOutOfMemory) return EA_OUT_OF_DEVICE_MEMORY;
+    return EA_HIP_FAILED;
+}
+
+// Status of the launch just issued.
+inline int launched() { return hip_status(hipGetLastError()); }
+
+inline hipStream_t as_stream(ea_stream_t s) { return reinterpret_cast<hipStream_t>(s); }
+
+template <typename T>
+inline T* dptr(uint64_t a) {
+    return reinterpret_cast<T*>(static_cast<uintptr_t>(a));
+}
+
+// Device-side error codes written into DevCtx::status.
+enum DeviceError : int { DEV_UNSUPPORTED_WIDTH = EA_UNSUPPORTED_WIDTH };
+
+}  // namespace ea
+
+#define EA_REQUIRE_CTX(c)                 \
+    ea::DevCtx* c = ea::ctx();            \
+    if (!c || !c->ready) return EA_NOT_INITIALIZED

@@ -1,0 +1,217 @@
+/* ea_exl3.h: the C ABI of the MI355X (gfx950) EXL3 routed-expert path.
+ *
+ * Drop-in boundary for fiore-labo/ExpertAtlas-GLM5.3's expert dispatch and quantized-linear calls. Each entry
+ * point names the reference interface it replaces (paths relative to the reference repository). Conventions,
+ * as in the reference:
+ *   - every tensor is a raw device address; the caller owns every buffer (weights, tables, scratch);
+ *   - no entry point allocates, frees, synchronises or reads device data on the host, except the documented
+ *     set-up calls (ea_init, ea_*_scratch_init, ea_prompt_experts_supported);
+ *   - every call is asynchronous on `stream` (a hipStream_t; 0 = the null stream), capturable in a HIP graph,
+ *     and returns an ea_status checked before any launch;
+ *   - fp16 / bf16 arrays are 16-bit patterns; dtype codes follow exl3.zig:8 (0 fp16, 1 bf16, 2 fp32);
+ *   - codebooks: 0 3inst, 1 mcg, 2 mul1 (decode.cuh:13). K2 = 2 * bits a weight.
+ */
+#ifndef EA_EXL3_H
+#define EA_EXL3_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void* ea_stream_t;
+
+/* Status codes map one to one onto the reference's Zig error names. */
+typedef enum ea_status {
+    EA_OK = 0,
+    EA_BAD_ROT_IN = 1,                /* exl3.zig:79 error.BadRotIn */
+    EA_UNPORTED_LINEAR_WALK = 2,      /* exl3.zig:98 error.UnportedLinearWalk */
+    EA_UNEVEN_K_SPLIT = 3,            /* exl3.zig:102 error.UnevenKSplit */
+    EA_UNPORTED_LINEAR_VARIANT = 4,   /* exl3.zig:109,128 error.UnportedLinearVariant */
+    EA_TOO_MANY_EXPERTS = 5,          /* experts.zig:99 error.TooManyExperts */
+    EA_TOO_MANY_SLOTS = 6,            /* experts.zig:100,196 error.TooManySlots */
+    EA_GROUP_SHARED_MEMORY = 7,       /* experts.zig:105 error.GroupSharedMemory */
+    EA_UNEVEN_SPLIT = 8,              /* experts.zig:141 error.UnevenSplit */
+    EA_BAD_ROW_STRIDE = 9,            /* experts.zig:142 error.BadRowStride */
+    EA_UNPORTED_GROUPED_VARIANT = 10, /* experts.zig:148 error.UnportedGroupedVariant */
+    EA_BAD_WIDTH = 11,                /* experts.zig:175,197 error.BadWidth */
+    EA_SCRATCH_TOO_SMALL = 12,        /* moe.zig:285 error.ScratchTooSmall */
+    EA_INVALID = 13,                  /* prompt_experts.zig:147,150 error.Invalid */
+    EA_NOT_GROUPABLE = 14,            /* linear.zig:302,318 error.NotGroupable */
+    EA_HIP_FAILED = 15,               /* driver.zig:38-47 error.CudaFailed */
+    EA_OUT_OF_DEVICE_MEMORY = 16,     /* driver.zig error.OutOfDeviceMemory */
+    EA_NOT_INITIALIZED = 17,          /* a call before ea_init on this device */
+    EA_BAD_ARGUMENT = 18,             /* a null pointer or a size outside the documented range */
+    EA_UNSUPPORTED_WIDTH = 19         /* a K2 / codebook this build has no decoder for */
+} ea_status;
+
+enum { EA_F16 = 0, EA_BF16 = 1, EA_F32 = 2 };
+enum { EA_CB_3INST = 0, EA_CB_MCG = 1, EA_CB_MUL1 = 2 };
+
+const char* ea_strerror(int status);
+/* Set-up for the current device (the reference's Kernels.load: experts.zig:84, exl3.zig:63,
+ * prompt_experts.zig:72). Idempotent per device. */
+int ea_init(int device);
+int ea_fini(void);
+/* Device-side status word: kernels record an expert width they have no decoder for here instead of trapping
+ * (experts_grouped.cuh:265-287 traps). Reads and clears it; synchronous (tests and health checks only). */
+int ea_device_status(int* code);
+
+/* ---- trellis decode --------------------------------------------------------------------------------------- */
+
+/* W [K, N] fp16 from one expert-layout matrix (tile (kt, nt) at ((kt * N/16) + nt) * 4 * K2 words).
+ * Replaces tf_exl3x::dequant_kernel (experts_grouped.cuh:317-336). K2 in 2..16. */
+int ea_dequant(ea_stream_t stream, const void* trellis, void* w, uint32_t K, uint32_t N, uint32_t k2, uint32_t cb);
+
+/* W [K, N] fp16 from a strided layout (tile (kt, nt) at kt * stride_k + (nt / 8) * stride_nb + (nt % 8) * TW).
+ * Replaces exl3.Kernels.unpackW (exl3.zig:125-136; exl3_linear.cu:489-503). */
+int ea_exl3_unpack(ea_stream_t stream, const void* t, void* w, uint32_t kdim, uint32_t n, uint32_t k2, uint32_t cb,
+                   int64_t stride_k, int64_t stride_nb);
+
+/* ---- routed experts, decode path (experts.zig, moe.zig) ---------------------------------------------------- */
+
+/* uids [maxu], ucount [1], members [maxu, maxm] (row * 32 + slot; -1 padded) of R rows' picks [R, slots].
+ * Replaces experts.Kernels.group (experts.zig:98-118; exl3_experts.cu:36-90). */
+int ea_experts_group(ea_stream_t stream, const int32_t* pick, int32_t* uids, int32_t* ucount, int32_t* members,
+                     uint32_t rows, uint32_t slots, uint32_t experts, uint32_t maxm);
+
+/* out0 / out1 [rows * slots, kdim] fp16 = fp16(((x * suh) @ H) / sqrt(128)) of each routed slot's gate and up.
+ * Replaces experts.Kernels.rotIn (experts.zig:122-136; exl3_experts.cu:116-134); x_dtype adds fp16 and fp32
+ * inputs to the reference's bf16. */
+int ea_experts_rot_in(ea_stream_t stream, const void* x, int x_dtype, uint32_t x_stride, const int32_t* pick,
+                      const void* suh0, const void* suh1, void* out0, void* out1, uint32_t rows, uint32_t kdim,
+                      uint32_t slots, uint32_t experts);
+
+/* experts.zig:41-67 GroupedArgs (host side only). */
+typedef struct ea_grouped_args {
+    uint64_t x0, x1;       /* fp16 [P, K] rotated inputs of matrix 0 / 1 */
+    uint64_t tp0, tp1;     /* int64 [E] trellis pointers */
+    uint64_t k2_0, k2_1;   /* int32 [E] widths */
+    uint64_t uids, ucount, members;
+    uint64_t z;            /* fp32 [mats, SK, P, N] */
+    uint32_t K, N, P, SK, maxm, slots, nexp_max, mats, cb, nt, warps, pf, lo, hi, ns;
+} ea_grouped_args;
+
+/* One grouped launch. Replaces experts.Kernels.grouped (experts.zig:140-169; experts_grouped.cuh:214-313). */
+int ea_experts_grouped(ea_stream_t stream, const ea_grouped_args* a);
+
+/* xd [P, n] fp16 = rotate(SwiGLU(svh * rotate(sum of gate / up splits)) * suh_d).
+ * Replaces experts.Kernels.gateupEpilogue (experts.zig:174-190; exl3_experts.cu:142-184). */
+int ea_experts_gateup_epilogue(ea_stream_t stream, const float* z, const int32_t* pick, const void* svh_g,
+                               const void* svh_u, const void* suh_d, void* xd, uint32_t rows, uint32_t p, uint32_t n,
+                               uint32_t sk, uint32_t slots, uint32_t experts, float limit, uint32_t act_mode);
+
+/* y [P, d] = rotate(sum of down splits) * svh_d; out [rows, d] fp32 = fma chain over slots of wts * y.
+ * Replaces experts.Kernels.downCombine (experts.zig:195-211; exl3_experts.cu:223-268). */
+int ea_experts_down_combine(ea_stream_t stream, const float* z, const int32_t* pick, const void* svh_d, float* y,
+                            const float* wts, float* out, uint32_t rows, uint32_t p, uint32_t d, uint32_t sk,
+                            uint32_t slots, uint32_t experts);
+
+/* moe.zig:19-37 Routed: one layer's routed experts on the device. */
+typedef struct ea_routed {
+    uint64_t ptr[3];       /* gate, up, down: int64 [E] device tables of trellis addresses */
+    uint64_t k2[3];        /* int32 [E] device tables of widths */
+    uint64_t suh_g, suh_u, svh_g, svh_u, suh_d, svh_d;  /* fp16, stacked [E, D] / [E, I] */
+    uint32_t count, dims, width, cb;
+    uint32_t k2_gu[2];     /* (min, max) over gate and up */
+    uint32_t k2_d[2];
+} ea_routed;
+
+/* moe.zig:242-275 Scratch, carved from one caller-owned device buffer. */
+typedef struct ea_moe_scratch {
+    uint64_t xg, xu, xd, z, y, ids, count, members;
+    uint64_t sync;         /* completion counters of the one-launch layer (zeroed by ea_moe_scratch_init) */
+    uint32_t rows, slots;
+} ea_moe_scratch;
+
+size_t ea_moe_scratch_bytes(const ea_routed* ex, uint32_t rows, uint32_t slots);
+/* Carves `base` (ea_moe_scratch_bytes long, 256-byte aligned) and fills it as moe.zig:271-272 does
+ * (zeros; members -1), asynchronously on `stream`. */
+int ea_moe_scratch_init(ea_stream_t stream, ea_moe_scratch* s, void* base, size_t bytes, const ea_routed* ex,
+                        uint32_t rows, uint32_t slots);
+
+/* out fp32 [R, D] = the R rows' routed experts weighted by wts. Replaces moe.routed (moe.zig:279-293).
+ * x: [R, D] rows x_stride apart; pick int32 / wts fp32 [R, slots]. */
+int ea_moe_routed(ea_stream_t stream, const void* x, int x_dtype, uint32_t x_stride, const int32_t* pick,
+                  const float* wts, const ea_routed* ex, const ea_moe_scratch* s, float* out, uint32_t R);
+
+/* ---- routed experts, prefill path (prompt_experts.zig) ----------------------------------------------------- */
+
+typedef struct ea_prompt_scratch {
+    uint64_t sorted, items, count, xd, plane;  /* plane 0: no deterministic pair plane */
+    uint64_t xg, xu, z;                        /* this build's rotated inputs and partial sums */
+    uint32_t rows, slots, max_items;
+} ea_prompt_scratch;
+
+/* Whether the prefill kernels cover `ex` (prompt_experts.zig:46-61); reads the width tables (synchronous). */
+int ea_prompt_experts_supported(const ea_routed* ex, int* ok);
+size_t ea_prompt_scratch_bytes(const ea_routed* ex, uint32_t rows, uint32_t slots, int planes);
+int ea_prompt_scratch_init(ea_stream_t stream, ea_prompt_scratch* s, void* base, size_t bytes, const ea_routed* ex,
+                           uint32_t rows, uint32_t slots, int planes);
+
+/* out [R, D] fp32 (fp16 with half_sums) = sum over slots of wts * expert(x), rounded through bf16 when do_round.
+ * Replaces prompt_experts.run (prompt_experts.zig:146-248). */
+int ea_prompt_experts_run(ea_stream_t stream, const void* x, int x_dtype, uint32_t xstride, const int32_t* pick,
+                          const float* wts, const ea_routed* ex, const ea_prompt_scratch* s, void* out, uint32_t R,
+                          int do_round, int half_sums);
+
+/* ---- EXL3 linear (exl3.zig, linear.zig) -------------------------------------------------------------------- */
+
+#define EA_MAX_JOBS 3
+/* exl3.zig:12-28, byte for byte (88 / 272 / 48 bytes). */
+typedef struct ea_job {
+    uint64_t xh, T;
+    int64_t stride_k, stride_nb;
+    uint64_t svh, bias, y, Z, counters;
+    int32_t y_dtype, N, SK, start;
+} ea_job;
+typedef struct ea_jobs {
+    ea_job j[EA_MAX_JOBS];
+    int32_t n;
+} ea_jobs;
+typedef struct ea_rot_jobs {
+    uint64_t suh[EA_MAX_JOBS], xh[EA_MAX_JOBS];
+} ea_rot_jobs;
+
+/* xh_j [m, kdim] fp16 = fp16(((x * suh_j) @ H) / sqrt(128)) for 1..3 jobs. Replaces exl3.Kernels.rotIn
+ * (exl3.zig:78-91; exl3_linear.cu:152-173). */
+int ea_exl3_rot_in(ea_stream_t stream, const void* x, int x_dtype, const ea_rot_jobs* jobs, uint32_t njobs,
+                   uint32_t m, uint32_t kdim);
+/* One launch over `jobs`. Replaces exl3.Kernels.linear (exl3.zig:95-121; exl3_linear.cu:231-484). */
+int ea_exl3_linear(ea_stream_t stream, const ea_jobs* jobs, uint32_t m, uint32_t kdim, uint32_t k2, uint32_t cb,
+                   uint32_t wk, uint32_t loads);
+
+/* linear.zig:10-30 Linear (words in the strips layout [N/128][K/16][8][TW]). */
+typedef struct ea_linear {
+    uint64_t words, suh, svh, counters;  /* counters: int32 [8 * N / 128], zero; left zero by the kernel */
+    uint32_t k, n, k2, cb, sk, wk;
+} ea_linear;
+typedef struct ea_linear_scratch {
+    uint64_t xh[EA_MAX_JOBS], z[EA_MAX_JOBS];
+} ea_linear_scratch;
+
+/* linear.zig:198-214 */
+void ea_linear_plan(uint32_t k, uint32_t n, uint32_t* sk, uint32_t* wk);
+/* linear.zig:301-325: outs[j] = x @ W_j for 1..3 groupable layers, m <= 128 rows (rot_in + one linear launch). */
+int ea_linear_call(ea_stream_t stream, const ea_linear_scratch* s, const ea_linear* const* ls, uint32_t nls,
+                   const void* x, int x_dtype, uint32_t m, const uint64_t* outs, const int* out_dtypes);
+int ea_linear_call_rotated(ea_stream_t stream, const ea_linear_scratch* s, const ea_linear* const* ls, uint32_t nls,
+                           uint32_t m, const uint64_t* outs, const int* out_dtypes);
+
+/* ---- routing input and the shared expert's activation ------------------------------------------------------ */
+
+/* pick int32 / wts fp32 [rows, 8] from logits fp32 [rows, 256] and bias fp32 [256]: sigmoid + bias, top 8 (the
+ * lower id on a tie), wts = sigmoid / (their sum + 1e-20) * scale; log: 0 or a byte per pick.
+ * Replaces ops.topk (ops.zig:189-191; native_ops.cu:998-1068). */
+int ea_topk8(ea_stream_t stream, const float* logits, const float* bias, int32_t* pick, float* wts, uint32_t rows,
+             float scale, uint8_t* log);
+
+/* out = bf16(bf16(silu(g)) * u) over rows of `width` bf16. Replaces ops.swiglu2 (native_ops.cu:429-441). */
+int ea_swiglu2(ea_stream_t stream, const void* g, const void* u, void* out, uint32_t rows, uint32_t width);
+
+#ifdef __cplusplus
+}
+#endif
+#endif
