@@ -126,6 +126,36 @@ __device__ __forceinline__ h4v decode_quad(uint32_t wa, uint32_t wb, int sh) {
     return v;
 }
 
+// Wider widths (K2 11..16): the four windows span up to 40 stream bits, so the lane reads three words and makes a
+// 64-bit segment from two funnel shifts.
+struct Quad3 {
+    int w0, w1, w2, sh;
+};
+
+template <int K2>
+__host__ __device__ constexpr Quad3 quad3_of(int p0) {
+    constexpr int TW = 4 * K2, NB = 128 * K2;
+    const int b0 = stream_end<K2>(p0) - 16 + NB;
+    const int a = (b0 - 1) >> 5;
+    return Quad3{a % TW, (a + 1) % TW, (a + 2) % TW, 32 - (b0 - 32 * a)};
+}
+
+template <int K2, int CB>
+__device__ __forceinline__ h4v decode_quad3(uint32_t w0, uint32_t w1, uint32_t w2, int sh) {
+    static_assert(K2 >= 11 && K2 <= 16, "three-word form");
+    const uint32_t hi = __builtin_amdgcn_alignbit(w0, w1, (uint32_t)sh);
+    const uint32_t lo = __builtin_amdgcn_alignbit(w1, w2, (uint32_t)sh);
+    constexpr int e0 = stream_end<K2>(0);
+    h4v v;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int d = (i == 0) ? 0 : (i == 1 ? stream_end<K2>(1) - e0 : (i == 2 ? stream_end<K2>(2) - e0 : stream_end<K2>(3) - e0));
+        const uint32_t s = d <= 16 ? (hi >> (16 - d)) : __builtin_amdgcn_alignbit(hi, lo, (uint32_t)(48 - d));
+        v[i] = cb_value<CB>(s);
+    }
+    return v;
+}
+
 // MFMA 16x16x16 f16 B-operand layout for one tile: lane l holds B[k'][n] for n = l & 15 and k' = 4 (l >> 4) + i.
 // With g = l >> 4 and tile lane L = 4 (n & 7) + g, h = n >> 3, the stream values p0 = 8 L + 4 h + i sit at rows
 // k = 2 g + (i & 1) + 8 (i >> 1) of column n. So the lane decodes four consecutive values, and the A operand

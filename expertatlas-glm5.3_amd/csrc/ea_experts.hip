@@ -8,6 +8,7 @@
 
 #include "ea_device.hpp"
 #include "ea_experts.hpp"
+#include "ea_gemm.hpp"
 #include "ea_host.hpp"
 
 namespace ea {
@@ -95,61 +96,6 @@ __global__ void __launch_bounds__(256) rot_in_kernel(const void* __restrict__ x,
     *reinterpret_cast<uint32_t*>(o) = (uint32_t)f2h(v0 * HAD_SCALE) | ((uint32_t)f2h(v1 * HAD_SCALE) << 16);
 }
 
-// ---- the grouped GEMV / GEMM core ---------------------------------------------------------------------------
-// acc[j] += A (16 member rows x the K range) @ W_q tile column nt0 + j, two k tiles a step (16x16x32 MFMA) and one
-// 16x16x16 step for an odd tail. xrow: this lane's member row (lane & 15) of fp16 inputs, or nullptr (zeros).
-template <int CB, int K2, int NTW>
-__device__ __forceinline__ void wave_tiles(const uint32_t* __restrict__ T, int ns, int kt0, int nkt, int nt0,
-                                           const uint16_t* __restrict__ xrow, int lane, f4v (&acc)[NTW]) {
-    constexpr int TW = 4 * K2;
-    const Quad q = quad_of<K2>(mfma_lane_p0(lane));
-    const int g = (lane >> 4) & 3;
-    const size_t kstride = (size_t)ns * TW;
-    const uint32_t* base = T + ((size_t)kt0 * ns + nt0) * TW;
-    int kt = 0;
-    for (; kt + 2 <= nkt; kt += 2) {
-        h8v a = {0, 0, 0, 0, 0, 0, 0, 0};
-        if (xrow) {
-            const uint16_t* xk = xrow + (kt0 + kt) * 16 + 2 * g;
-            const uint32_t a0 = *reinterpret_cast<const uint32_t*>(xk);
-            const uint32_t a1 = *reinterpret_cast<const uint32_t*>(xk + 8);
-            const uint32_t a2 = *reinterpret_cast<const uint32_t*>(xk + 16);
-            const uint32_t a3 = *reinterpret_cast<const uint32_t*>(xk + 24);
-            typedef uint32_t u4v __attribute__((ext_vector_type(4)));
-            const u4v au = {a0, a1, a2, a3};
-            a = __builtin_bit_cast(h8v, au);
-        }
-        const uint32_t* t0 = base + (size_t)kt * kstride;
-#pragma unroll
-        for (int j = 0; j < NTW; ++j) {
-            const uint32_t* ta = t0 + j * TW;
-            const uint32_t* tb = ta + kstride;
-            const h4v b0 = decode_quad<K2, CB>(ta[q.wa], ta[q.wb], q.sh);
-            const h4v b1 = decode_quad<K2, CB>(tb[q.wa], tb[q.wb], q.sh);
-            const h8v b = {b0[0], b0[1], b0[2], b0[3], b1[0], b1[1], b1[2], b1[3]};
-            acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, acc[j], 0, 0, 0);
-        }
-    }
-    if (kt < nkt) {
-        h4v a = {0, 0, 0, 0};
-        if (xrow) {
-            const uint16_t* xk = xrow + (kt0 + kt) * 16 + 2 * g;
-            typedef uint32_t u2v __attribute__((ext_vector_type(2)));
-            const u2v au = {*reinterpret_cast<const uint32_t*>(xk), *reinterpret_cast<const uint32_t*>(xk + 8)};
-            a = __builtin_bit_cast(h4v, au);
-        }
-        const uint32_t* t0 = base + (size_t)kt * kstride;
-#pragma unroll
-        for (int j = 0; j < NTW; ++j) {
-            const uint32_t* ta = t0 + j * TW;
-            const h4v b = decode_quad<K2, CB>(ta[q.wa], ta[q.wb], q.sh);
-            acc[j] = __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, acc[j], 0, 0, 0);
-        }
-    }
-}
-
-__device__ __forceinline__ void record_error(int* status, int code) { atomicCAS(status, 0, code); }
-
 // Block (expert u, n block of NTW tiles, (matrix, split, member tile)): NW waves split the split's k tiles in
 // equal consecutive ranges, their partial sums added in wave order into Z[mat][split][pair][n]
 // (experts_grouped.cuh:214-313). K2 comes from the expert's table entry at run time.
@@ -181,30 +127,20 @@ __global__ void __launch_bounds__(NW * 64) grouped_kernel(
     __syncthreads();
     if (rows_sh[0] < 0) return;  // members are packed first: this member tile is empty
     const int r = rows_sh[lane & 15];
-    const uint16_t* xrow = r >= 0 ? X + (size_t)r * K : nullptr;
+    const uint16_t* const xrow[1] = {r >= 0 ? X + (size_t)r * K : nullptr};
 
     const int per_split = KT / SK, per_wave = per_split / NW;
     const int kt0 = split * per_split + wave * per_wave;
     const int nt0 = blockIdx.y * NTW;
 
-    f4v acc[NTW];
+    f4v acc[1][NTW];
 #pragma unroll
-    for (int j = 0; j < NTW; ++j) acc[j] = f4v{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < NTW; ++j) acc[0][j] = f4v{0.f, 0.f, 0.f, 0.f};
 
-    bool ok = true;
-    switch (k2) {
-#define EA_CASE(K2_)                                                                             \
-    case K2_:                                                                                    \
-        if constexpr (K2_ >= LO && K2_ <= HI)                                                    \
-            wave_tiles<CB, K2_, NTW>(T, ns, kt0, per_wave, nt0, xrow, lane, acc);                \
-        else                                                                                     \
-            ok = false;                                                                          \
-        break;
-        EA_CASE(2) EA_CASE(3) EA_CASE(4) EA_CASE(5) EA_CASE(6) EA_CASE(7) EA_CASE(8) EA_CASE(9) EA_CASE(10)
-#undef EA_CASE
-        default:
-            ok = false;
-    }
+    const uint32_t* base = T + ((size_t)kt0 * ns + nt0) * 4 * k2;
+    const bool ok = EA_K2_SWITCH(k2, LO, HI,
+                                 (wave_tiles<CB, K2V, NTW, 1>(base, (size_t)ns * 4 * K2V, per_wave, kt0 * 16, xrow,
+                                                              lane, acc)));
     if (!ok) {
         if (threadIdx.x == 0) record_error(status, DEV_UNSUPPORTED_WIDTH);
         return;
@@ -215,7 +151,7 @@ __global__ void __launch_bounds__(NW * 64) grouped_kernel(
 #pragma unroll
     for (int j = 0; j < NTW; ++j)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) red[wave][4 * (lane >> 4) + i][j * 16 + (lane & 15)] = acc[j][i];
+        for (int i = 0; i < 4; ++i) red[wave][4 * (lane >> 4) + i][j * 16 + (lane & 15)] = acc[0][j][i];
     __syncthreads();
     for (int idx = threadIdx.x; idx < 16 * NTW * 16; idx += NW * 64) {
         const int row = idx / (NTW * 16), col = idx % (NTW * 16);
@@ -282,7 +218,7 @@ __global__ void __launch_bounds__(64) gateup_epilogue_kernel(const float* __rest
 constexpr int DC_WAVES = 8;
 __global__ void __launch_bounds__(DC_WAVES * 64) down_combine_kernel(
     const float* __restrict__ Z, const int* __restrict__ pick, const uint16_t* __restrict__ svh_d, float* __restrict__ y,
-    const float* __restrict__ wts, float* __restrict__ out, int P, int D, int SK, int E, int slots) {
+    const float* __restrict__ wts, float* __restrict__ out, int P, int D, int SK, int E, int slots, int skip_invalid) {
     __shared__ float part[32][128];
     const int r = blockIdx.x, blk = blockIdx.y;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -305,6 +241,8 @@ __global__ void __launch_bounds__(DC_WAVES * 64) down_combine_kernel(
                 o[j] = v[j] * HAD_SCALE * h2f(svh_d[(size_t)e * D + n + j]);
                 y[(size_t)p * D + n + j] = o[j];
             }
+        } else if (skip_invalid) {
+            o[0] = o[1] = 0.f;
         } else {
 #pragma unroll
             for (int j = 0; j < 2; ++j) o[j] = y[(size_t)p * D + n + j];
@@ -393,8 +331,10 @@ int launch_grouped(hipStream_t s, const ea_grouped_args& a) {
         return EA_UNEVEN_SPLIT;
     if (a.ns != 0 && a.ns < a.N / 16) return EA_BAD_ROW_STRIDE;
     if (a.cb > 2 || a.mats < 1 || a.mats > 2) return EA_UNPORTED_GROUPED_VARIANT;
+    // the K2 ranges: [8, 8], else [2, 10], else [2, 16] (experts.zig:143-145)
     const bool only8 = a.lo == 8 && a.hi == 8;
-    if (!only8 && !(a.lo >= 2 && a.hi <= 10)) return EA_UNPORTED_GROUPED_VARIANT;
+    const bool to10 = a.lo >= 2 && a.hi <= 10;
+    if (a.lo < 2 || a.hi > 16) return EA_UNPORTED_GROUPED_VARIANT;
     if (!a.x0 || !a.x1 || !a.tp0 || !a.tp1 || !a.k2_0 || !a.k2_1 || !a.uids || !a.ucount || !a.members || !a.z)
         return EA_BAD_ARGUMENT;
     if (a.nexp_max == 0 || a.maxm == 0) return EA_OK;
@@ -409,11 +349,12 @@ int launch_grouped(hipStream_t s, const ea_grouped_args& a) {
         }
     if (a.cb == 1) {
         if (only8) grouped_dispatch<1, 8, 8>(a, s, nw, ntw, c->status);
-        else grouped_dispatch<1, 2, 10>(a, s, nw, ntw, c->status);
+        else if (to10) grouped_dispatch<1, 2, 10>(a, s, nw, ntw, c->status);
+        else grouped_dispatch<1, 2, 16>(a, s, nw, ntw, c->status);
     } else if (a.cb == 2) {
-        grouped_dispatch<2, 2, 10>(a, s, nw, ntw, c->status);
+        grouped_dispatch<2, 2, 16>(a, s, nw, ntw, c->status);
     } else {
-        grouped_dispatch<0, 2, 10>(a, s, nw, ntw, c->status);
+        grouped_dispatch<0, 2, 16>(a, s, nw, ntw, c->status);
     }
     return launched();
 }
@@ -433,7 +374,7 @@ int launch_gateup_epilogue(hipStream_t s, const float* z, const int* pick, const
 
 int launch_down_combine(hipStream_t s, const float* z, const int* pick, const uint16_t* svh_d, float* y,
                         const float* wts, float* out, uint32_t rows, uint32_t p, uint32_t d, uint32_t sk,
-                        uint32_t slots, uint32_t experts) {
+                        uint32_t slots, uint32_t experts, bool skip_invalid) {
     EA_REQUIRE_CTX(c);
     if (slots > 32) return EA_TOO_MANY_SLOTS;
     if (d % 128 != 0) return EA_BAD_WIDTH;
@@ -441,7 +382,7 @@ int launch_down_combine(hipStream_t s, const float* z, const int* pick, const ui
     if (rows == 0 || d == 0) return EA_OK;
     dim3 grid(rows, d / 128);
     down_combine_kernel<<<grid, DC_WAVES * 64, 0, s>>>(z, pick, svh_d, y, wts, out, (int)p, (int)d, (int)sk,
-                                                       (int)experts, (int)slots);
+                                                       (int)experts, (int)slots, skip_invalid ? 1 : 0);
     return launched();
 }
 

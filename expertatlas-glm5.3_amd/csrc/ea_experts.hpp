@@ -19,6 +19,6 @@ int launch_gateup_epilogue(hipStream_t s, const float* z, const int* pick, const
                            uint32_t n, uint32_t sk, uint32_t slots, uint32_t experts, float limit, uint32_t act_mode);
 int launch_down_combine(hipStream_t s, const float* z, const int* pick, const uint16_t* svh_d, float* y,
                         const float* wts, float* out, uint32_t rows, uint32_t p, uint32_t d, uint32_t sk,
-                        uint32_t slots, uint32_t experts);
+                        uint32_t slots, uint32_t experts, bool skip_invalid = false);
 
 }  // namespace ea

@@ -1,0 +1,118 @@
+// The MFMA core shared by the expert GEMV / GEMM and the EXL3 linear: a wavefront multiplies up to MG groups of 16
+// activation rows by a strip of trellis tiles, decoding each tile once into v_mfma_f32_16x16x32_f16 B operands.
+#pragma once
+
+#include "ea_device.hpp"
+
+namespace ea {
+
+// A lane's constant view of any tile for K2 (its word indices and funnel shift; see quad_of / quad3_of).
+template <int K2, int CB>
+struct TileLane {
+    int w0, w1, w2, sh;
+    __device__ __forceinline__ explicit TileLane(int lane) {
+        if constexpr (K2 <= 10) {
+            const Quad q = quad_of<K2>(mfma_lane_p0(lane));
+            w0 = q.wa;
+            w1 = q.wb;
+            w2 = 0;
+            sh = q.sh;
+        } else {
+            const Quad3 q = quad3_of<K2>(mfma_lane_p0(lane));
+            w0 = q.w0;
+            w1 = q.w1;
+            w2 = q.w2;
+            sh = q.sh;
+        }
+    }
+    // This lane's four B values of the tile starting at `tile`.
+    __device__ __forceinline__ h4v decode(const uint32_t* __restrict__ tile) const {
+        if constexpr (K2 <= 10) return decode_quad<K2, CB>(tile[w0], tile[w1], sh);
+        else return decode_quad3<K2, CB>(tile[w0], tile[w1], tile[w2], sh);
+    }
+};
+
+// The lane's A operand of a two-tile k step at k = k0 (16x16x32): rows k0 + 2g, +1, +8, +9 and the same 16 later,
+// g = lane >> 4; the same k permutation as the decoded B operand.
+__device__ __forceinline__ h8v load_a8(const uint16_t* __restrict__ xrow, int k0, int lane) {
+    typedef uint32_t u4v __attribute__((ext_vector_type(4)));
+    if (!xrow) return h8v{0, 0, 0, 0, 0, 0, 0, 0};
+    const uint16_t* xk = xrow + k0 + 2 * ((lane >> 4) & 3);
+    const u4v au = {*reinterpret_cast<const uint32_t*>(xk), *reinterpret_cast<const uint32_t*>(xk + 8),
+                    *reinterpret_cast<const uint32_t*>(xk + 16), *reinterpret_cast<const uint32_t*>(xk + 24)};
+    return __builtin_bit_cast(h8v, au);
+}
+
+__device__ __forceinline__ h4v load_a4(const uint16_t* __restrict__ xrow, int k0, int lane) {
+    typedef uint32_t u2v __attribute__((ext_vector_type(2)));
+    if (!xrow) return h4v{0, 0, 0, 0};
+    const uint16_t* xk = xrow + k0 + 2 * ((lane >> 4) & 3);
+    const u2v au = {*reinterpret_cast<const uint32_t*>(xk), *reinterpret_cast<const uint32_t*>(xk + 8)};
+    return __builtin_bit_cast(h4v, au);
+}
+
+// acc[m][j] += rows(m) @ tiles: tile (t, j) of the strip at base + t * kstride + j * TW words for t in [0, nkt);
+// xrow[m]: this lane's activation row (lane & 15) of row group m, or nullptr; k0: the k of tile 0.
+// Output layout of acc[m][j]: lane l holds D[4 (l >> 4) + i][l & 15] (row, column within the 16 x 16 tile).
+template <int CB, int K2, int NTW, int MG>
+__device__ __forceinline__ void wave_tiles(const uint32_t* __restrict__ base, size_t kstride, int nkt, int k0,
+                                           const uint16_t* const (&xrow)[MG], int lane, f4v (&acc)[MG][NTW]) {
+    constexpr int TW = 4 * K2;
+    const TileLane<K2, CB> tl(lane);
+    int t = 0;
+    for (; t + 2 <= nkt; t += 2) {
+        h8v a[MG];
+#pragma unroll
+        for (int m = 0; m < MG; ++m) a[m] = load_a8(xrow[m], k0 + t * 16, lane);
+        const uint32_t* t0 = base + (size_t)t * kstride;
+#pragma unroll
+        for (int j = 0; j < NTW; ++j) {
+            const h4v b0 = tl.decode(t0 + j * TW);
+            const h4v b1 = tl.decode(t0 + kstride + j * TW);
+            const h8v b = {b0[0], b0[1], b0[2], b0[3], b1[0], b1[1], b1[2], b1[3]};
+#pragma unroll
+            for (int m = 0; m < MG; ++m) acc[m][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[m], b, acc[m][j], 0, 0, 0);
+        }
+    }
+    if (t < nkt) {
+        h4v a[MG];
+#pragma unroll
+        for (int m = 0; m < MG; ++m) a[m] = load_a4(xrow[m], k0 + t * 16, lane);
+        const uint32_t* t0 = base + (size_t)t * kstride;
+#pragma unroll
+        for (int j = 0; j < NTW; ++j) {
+            const h4v b = tl.decode(t0 + j * TW);
+#pragma unroll
+            for (int m = 0; m < MG; ++m) acc[m][j] = __builtin_amdgcn_mfma_f32_16x16x16f16(a[m], b, acc[m][j], 0, 0, 0);
+        }
+    }
+}
+
+__device__ __forceinline__ void record_error(int* status, int code) { atomicCAS(status, 0, code); }
+
+// Dispatch a runtime K2 to wave_tiles<..., K2, ...> for K2 in [LO, HI]; false when outside.
+#define EA_K2_SWITCH(k2, LO, HI, CALL)                                        \
+    [&]() -> bool {                                                           \
+        switch (k2) {                                                         \
+            EA_K2_CASE(2, LO, HI, CALL) EA_K2_CASE(3, LO, HI, CALL)           \
+            EA_K2_CASE(4, LO, HI, CALL) EA_K2_CASE(5, LO, HI, CALL)           \
+            EA_K2_CASE(6, LO, HI, CALL) EA_K2_CASE(7, LO, HI, CALL)           \
+            EA_K2_CASE(8, LO, HI, CALL) EA_K2_CASE(9, LO, HI, CALL)           \
+            EA_K2_CASE(10, LO, HI, CALL) EA_K2_CASE(11, LO, HI, CALL)         \
+            EA_K2_CASE(12, LO, HI, CALL) EA_K2_CASE(13, LO, HI, CALL)         \
+            EA_K2_CASE(14, LO, HI, CALL) EA_K2_CASE(15, LO, HI, CALL)         \
+            EA_K2_CASE(16, LO, HI, CALL)                                      \
+            default: return false;                                            \
+        }                                                                     \
+    }()
+#define EA_K2_CASE(K2_, LO, HI, CALL)                    \
+    case K2_:                                            \
+        if constexpr (K2_ >= LO && K2_ <= HI) {          \
+            constexpr int K2V = K2_;                     \
+            CALL;                                        \
+            return true;                                 \
+        } else {                                         \
+            return false;                                \
+        }
+
+}  // namespace ea

@@ -31,9 +31,12 @@ inline int launched() { return hip_status(hipGetLastError()); }
 inline hipStream_t as_stream(ea_stream_t s) { return reinterpret_cast<hipStream_t>(s); }
 
 template <typename T>
-inline T* dptr(uint64_t a) {
+__host__ __device__ inline T* dptr(uint64_t a) {
     return reinterpret_cast<T*>(static_cast<uintptr_t>(a));
 }
+
+// Fills n 32-bit words at p with v by a kernel (capturable; no hipMemsetAsync).
+int fill_words(hipStream_t s, void* p, uint32_t v, size_t n);
 
 // Device-side error codes written into DevCtx::status.
 enum DeviceError : int { DEV_UNSUPPORTED_WIDTH = EA_UNSUPPORTED_WIDTH };

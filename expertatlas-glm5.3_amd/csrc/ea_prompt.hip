@@ -1,0 +1,342 @@
+// Routed experts of prompt chunks (hundreds to thousands of rows): route the pairs into items of at most IPM pairs
+// of one expert, then per item one MFMA GEMM that decodes each trellis tile once for all of the item's rows
+// (prompt_experts.cu / prompt_experts.zig of the reference give the interface and the item scheme).
+//
+// A pass over <= 4096 rows: route -> per-pair input rotation -> item GEMM gate|up -> gate/up epilogue -> item GEMM
+// down -> down epilogue + slot-ordered combine [-> bf16 rounding]. Every row's arithmetic is independent of which
+// item or M-tile it lands in (MFMA rows do not mix), and the combine adds the slots in order, so the output is the
+// same on every run (the reference's deterministic mode; its atomic mode is not reproduced).
+#include <hip/hip_runtime.h>
+
+#include "ea_device.hpp"
+#include "ea_experts.hpp"
+#include "ea_gemm.hpp"
+#include "ea_host.hpp"
+
+namespace ea {
+
+constexpr int IPM = 112;           // routed pairs an item (prompt_experts.cu:55-58, TF_PE_GPM)
+constexpr int IPM_TILES = IPM / 16;
+constexpr uint32_t CHUNK_ROWS = 4096;  // rows a pass at most (prompt_experts.zig:17)
+constexpr int ROUTE_THREADS = 1024;
+
+// One block: per-expert counts, exclusive scans of counts and items over experts, items (e, first, cnt <= IPM) in
+// expert order, and sorted[] = pair ids grouped by expert (order within an expert: arrival).
+// (prompt_experts.cu:162-244 with by_count off.)
+__global__ void __launch_bounds__(ROUTE_THREADS) route_kernel(const int* __restrict__ pick, int n, int E,
+                                                             int* __restrict__ sorted, int* __restrict__ items,
+                                                             int* __restrict__ item_count, int max_items) {
+    extern __shared__ int sh[];
+    int* cnt = sh;        // [E]
+    int* cur = sh + E;    // [E]
+    __shared__ int wsum[ROUTE_THREADS / 64][2];
+    for (int e = threadIdx.x; e < E; e += ROUTE_THREADS) cnt[e] = 0;
+    __syncthreads();
+    for (int i = threadIdx.x; i < n; i += ROUTE_THREADS) {
+        const int e = pick[i];
+        if (e >= 0 && e < E) atomicAdd(&cnt[e], 1);
+    }
+    __syncthreads();
+    const int per = (E + ROUTE_THREADS - 1) / ROUTE_THREADS;
+    const int e0 = threadIdx.x * per;
+    int c_sum = 0, i_sum = 0;
+    for (int q = 0; q < per; ++q) {
+        const int e = e0 + q;
+        if (e < E) {
+            c_sum += cnt[e];
+            i_sum += (cnt[e] + IPM - 1) / IPM;
+        }
+    }
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    int ci = c_sum, ii = i_sum;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const int a = __shfl_up(ci, o, 64), b = __shfl_up(ii, o, 64);
+        if (lane >= o) {
+            ci += a;
+            ii += b;
+        }
+    }
+    if (lane == 63) {
+        wsum[wave][0] = ci;
+        wsum[wave][1] = ii;
+    }
+    __syncthreads();
+    if (wave == 0) {
+        const int a = lane < ROUTE_THREADS / 64 ? wsum[lane][0] : 0, b = lane < ROUTE_THREADS / 64 ? wsum[lane][1] : 0;
+        int sa = a, sb = b;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const int x = __shfl_up(sa, o, 64), y = __shfl_up(sb, o, 64);
+            if (lane >= o) {
+                sa += x;
+                sb += y;
+            }
+        }
+        if (lane < ROUTE_THREADS / 64) {
+            wsum[lane][0] = sa - a;
+            wsum[lane][1] = sb - b;
+        }
+        if (lane == ROUTE_THREADS / 64 - 1) item_count[0] = min(sb, max_items);
+    }
+    __syncthreads();
+    int off = wsum[wave][0] + ci - c_sum, it = wsum[wave][1] + ii - i_sum;
+    for (int q = 0; q < per; ++q) {
+        const int e = e0 + q;
+        if (e >= E) break;
+        const int c = cnt[e];
+        cur[e] = off;
+        for (int f = 0; f < c; f += IPM, ++it)
+            if (it < max_items) {
+                items[3 * it] = e;
+                items[3 * it + 1] = off + f;
+                items[3 * it + 2] = min(IPM, c - f);
+            }
+        off += c;
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < n; i += ROUTE_THREADS) {
+        const int e = pick[i];
+        if (e >= 0 && e < E) sorted[atomicAdd(&cur[e], 1)] = i;
+    }
+}
+
+// Block (item, n block of NW * NTW tiles, matrix): wave w covers NTW n tiles over the whole K range for all of the
+// item's rows (IPM_TILES groups of 16), so each trellis tile is decoded once per item. Z[mat][pair][n] fp32.
+template <int CB, int LO, int HI, int NTW, int NW>
+__global__ void __launch_bounds__(NW * 64) item_gemm_kernel(
+    const uint16_t* __restrict__ X0, const uint16_t* __restrict__ X1, const int64_t* __restrict__ TP0,
+    const int64_t* __restrict__ TP1, const int* __restrict__ K2_0, const int* __restrict__ K2_1,
+    const int* __restrict__ sorted, const int* __restrict__ items, const int* __restrict__ item_count,
+    float* __restrict__ Z, int K, int N, int P, int* __restrict__ status) {
+    const int item = blockIdx.x;
+    if (item >= item_count[0]) return;
+    const int e = items[3 * item], first = items[3 * item + 1], cnt = items[3 * item + 2];
+    const int mat = blockIdx.z;
+    const uint16_t* X = mat ? X1 : X0;
+    const uint32_t* T = reinterpret_cast<const uint32_t*>(mat ? TP1[e] : TP0[e]);
+    const int k2 = mat ? K2_1[e] : K2_0[e];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    __shared__ int pair_sh[IPM];
+    if (threadIdx.x < IPM) pair_sh[threadIdx.x] = (int)threadIdx.x < cnt ? sorted[first + threadIdx.x] : -1;
+    __syncthreads();
+    const int nt0 = (blockIdx.y * NW + wave) * NTW;
+    if (nt0 * 16 >= N) return;
+    const uint16_t* xrow[IPM_TILES];
+#pragma unroll
+    for (int m = 0; m < IPM_TILES; ++m) {
+        const int p = pair_sh[m * 16 + (lane & 15)];
+        xrow[m] = p >= 0 ? X + (size_t)p * K : nullptr;
+    }
+    f4v acc[IPM_TILES][NTW];
+#pragma unroll
+    for (int m = 0; m < IPM_TILES; ++m)
+#pragma unroll
+        for (int j = 0; j < NTW; ++j) acc[m][j] = f4v{0.f, 0.f, 0.f, 0.f};
+    const int ns = N >> 4;
+    const uint32_t* base = T + (size_t)nt0 * 4 * k2;
+    const bool ok = EA_K2_SWITCH(k2, LO, HI,
+                                 (wave_tiles<CB, K2V, NTW, IPM_TILES>(base, (size_t)ns * 4 * K2V, K >> 4, 0, xrow,
+                                                                      lane, acc)));
+    if (!ok) {
+        if (lane == 0) record_error(status, DEV_UNSUPPORTED_WIDTH);
+        return;
+    }
+    float* Zm = Z + (size_t)mat * P * N;
+#pragma unroll
+    for (int m = 0; m < IPM_TILES; ++m)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int row = m * 16 + 4 * (lane >> 4) + i;
+            const int p = pair_sh[row];
+            if (p < 0) continue;
+#pragma unroll
+            for (int j = 0; j < NTW; ++j) Zm[(size_t)p * N + (nt0 + j) * 16 + (lane & 15)] = acc[m][j][i];
+        }
+}
+
+// out fp32 -> bf16 -> fp32 in place (prompt_experts.zig:246), or fp32 -> fp16 into a half output.
+__global__ void round_kernel(float* __restrict__ out, size_t n) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+        out[i] = bf16r(out[i]);
+}
+__global__ void to_half_kernel(const float* __restrict__ in, uint16_t* __restrict__ out, size_t n) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+        out[i] = f2h(in[i]);
+}
+
+static size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
+
+struct PromptLayout {
+    size_t sorted, items, count, xd, plane, xg, xu, z, total;
+    uint32_t rows, max_items;
+};
+
+static PromptLayout prompt_layout(const ea_routed* ex, uint32_t rows, uint32_t slots) {
+    PromptLayout l{};
+    const uint32_t r = rows < CHUNK_ROWS ? rows : CHUNK_ROWS;
+    const size_t n = (size_t)r * slots, D = ex->dims, I = ex->width;
+    l.rows = r;
+    l.max_items = (uint32_t)(n / IPM + (n < ex->count ? n : ex->count));
+    size_t off = 0;
+    auto take = [&](size_t b) {
+        const size_t at = off;
+        off += align256(b);
+        return at;
+    };
+    l.sorted = take(n * 4);
+    l.items = take(3 * (size_t)l.max_items * 4);
+    l.count = take(16);
+    l.xd = take(n * I * 2);
+    l.plane = take(n * D * 4);   // per-pair down outputs (the reference's pair plane)
+    l.xg = take(n * D * 2);
+    l.xu = take(n * D * 2);
+    l.z = take(2 * n * I * 4);
+    l.total = off;
+    return l;
+}
+
+template <int CB, int LO, int HI>
+static void item_gemm(hipStream_t s, const uint16_t* X0, const uint16_t* X1, const int64_t* TP0, const int64_t* TP1,
+                      const int* B0, const int* B1, const int* sorted, const int* items, const int* count, float* Z,
+                      int K, int N, int P, int mats, uint32_t max_items, int* status) {
+    constexpr int NTW = 2, NW = 4;
+    dim3 grid(max_items, (N / 16 + NTW * NW - 1) / (NTW * NW), mats);
+    item_gemm_kernel<CB, LO, HI, NTW, NW><<<grid, NW * 64, 0, s>>>(X0, X1, TP0, TP1, B0, B1, sorted, items, count, Z, K,
+                                                                   N, P, status);
+}
+
+static void item_gemm_dispatch(hipStream_t s, uint32_t cb, bool wide, const uint16_t* X0, const uint16_t* X1,
+                               const int64_t* TP0, const int64_t* TP1, const int* B0, const int* B1,
+                               const int* sorted, const int* items, const int* count, float* Z, int K, int N, int P,
+                               int mats, uint32_t max_items, int* status) {
+    (void)wide;
+    if (cb == 1) {
+        item_gemm<1, 2, 16>(s, X0, X1, TP0, TP1, B0, B1, sorted, items, count, Z, K, N, P, mats, max_items, status);
+    } else if (cb == 2) {
+        item_gemm<2, 2, 16>(s, X0, X1, TP0, TP1, B0, B1, sorted, items, count, Z, K, N, P, mats, max_items, status);
+    } else {
+        item_gemm<0, 2, 16>(s, X0, X1, TP0, TP1, B0, B1, sorted, items, count, Z, K, N, P, mats, max_items, status);
+    }
+}
+
+}  // namespace ea
+
+using namespace ea;
+
+extern "C" {
+
+int ea_prompt_experts_supported(const ea_routed* ex, int* ok) {
+    EA_REQUIRE_CTX(c);
+    if (!ex || !ok) return EA_BAD_ARGUMENT;
+    *ok = 0;
+    if (ex->cb > 2 || ex->width % 128 || ex->dims % 128 || ex->count == 0) return EA_OK;
+    for (int m = 0; m < 3; ++m) {
+        int32_t* k2 = new int32_t[ex->count];
+        const int r = hip_status(hipMemcpy(k2, dptr<void>(ex->k2[m]), ex->count * 4, hipMemcpyDeviceToHost));
+        bool good = r == EA_OK;
+        for (uint32_t e = 0; good && e < ex->count; ++e) good = k2[e] >= 2 && k2[e] <= 16;
+        delete[] k2;
+        if (r) return r;
+        if (!good) return EA_OK;
+    }
+    *ok = 1;
+    return EA_OK;
+}
+
+size_t ea_prompt_scratch_bytes(const ea_routed* ex, uint32_t rows, uint32_t slots, int planes) {
+    (void)planes;
+    if (!ex || rows == 0 || slots == 0) return 0;
+    return prompt_layout(ex, rows, slots).total;
+}
+
+int ea_prompt_scratch_init(ea_stream_t stream, ea_prompt_scratch* s, void* base, size_t bytes, const ea_routed* ex,
+                           uint32_t rows, uint32_t slots, int planes) {
+    (void)planes;  // the pair plane is always there: the slots are always added in order
+    EA_REQUIRE_CTX(c);
+    if (!s || !base || !ex || rows == 0 || slots == 0 || slots > 32) return EA_BAD_ARGUMENT;
+    if (reinterpret_cast<uintptr_t>(base) & 255) return EA_BAD_ARGUMENT;
+    const PromptLayout l = prompt_layout(ex, rows, slots);
+    if (bytes < l.total) return EA_SCRATCH_TOO_SMALL;
+    const uint64_t b = reinterpret_cast<uintptr_t>(base);
+    s->sorted = b + l.sorted;
+    s->items = b + l.items;
+    s->count = b + l.count;
+    s->xd = b + l.xd;
+    s->plane = b + l.plane;
+    s->xg = b + l.xg;
+    s->xu = b + l.xu;
+    s->z = b + l.z;
+    s->rows = l.rows;
+    s->slots = slots;
+    s->max_items = l.max_items;
+    // only the count word needs a defined start (prompt_experts.zig:109-110)
+    return fill_words(as_stream(stream), dptr<void>(s->count), 0u, 4);
+}
+
+int ea_prompt_experts_run(ea_stream_t stream, const void* x, int x_dtype, uint32_t xstride, const int32_t* pick,
+                          const float* wts, const ea_routed* ex, const ea_prompt_scratch* sc, void* out, uint32_t R,
+                          int do_round, int half_sums) {
+    EA_REQUIRE_CTX(c);
+    if (half_sums && do_round) return EA_INVALID;  // prompt_experts.zig:147
+    if (!x || !pick || !wts || !ex || !sc || !out) return EA_BAD_ARGUMENT;
+    if (x_dtype < 0 || x_dtype > 2 || sc->slots == 0) return EA_BAD_ARGUMENT;
+    if (ex->width % 128 || ex->dims % 128) return EA_BAD_WIDTH;
+    hipStream_t s = as_stream(stream);
+    const uint32_t D = ex->dims, I = ex->width, E = ex->count, S = sc->slots;
+    const size_t xb = x_dtype == 2 ? 4 : 2;
+    const bool wide = ex->k2_gu[1] > 10 || ex->k2_d[1] > 10;
+    for (uint32_t r0 = 0; r0 < R; r0 += sc->rows) {
+        const uint32_t n = R - r0 < sc->rows ? R - r0 : sc->rows;
+        const uint32_t pairs = n * S;
+        const uint32_t items_n = (uint32_t)(pairs / IPM + (pairs < E ? pairs : E));
+        const uint32_t max_items = items_n < sc->max_items ? items_n : sc->max_items;
+        const char* xs = static_cast<const char*>(x) + (size_t)r0 * xstride * xb;
+        const int32_t* pk = pick + (size_t)r0 * S;
+        const float* wt = wts + (size_t)r0 * S;
+        route_kernel<<<1, ROUTE_THREADS, 2 * E * sizeof(int), s>>>(pk, (int)pairs, (int)E, dptr<int>(sc->sorted),
+                                                                  dptr<int>(sc->items), dptr<int>(sc->count),
+                                                                  (int)max_items);
+        int r = launched();
+        if (r) return r;
+        r = launch_rot_in(s, xs, x_dtype, xstride, pk, dptr<const uint16_t>(ex->suh_g), dptr<const uint16_t>(ex->suh_u),
+                          dptr<uint16_t>(sc->xg), dptr<uint16_t>(sc->xu), n, D, S, E);
+        if (r) return r;
+        item_gemm_dispatch(s, ex->cb, wide, dptr<const uint16_t>(sc->xg), dptr<const uint16_t>(sc->xu),
+                           dptr<const int64_t>(ex->ptr[0]), dptr<const int64_t>(ex->ptr[1]),
+                           dptr<const int>(ex->k2[0]), dptr<const int>(ex->k2[1]), dptr<const int>(sc->sorted),
+                           dptr<const int>(sc->items), dptr<const int>(sc->count), dptr<float>(sc->z), (int)D, (int)I,
+                           (int)pairs, 2, max_items, c->status);
+        r = launched();
+        if (r) return r;
+        r = launch_gateup_epilogue(s, dptr<const float>(sc->z), pk, dptr<const uint16_t>(ex->svh_g),
+                                   dptr<const uint16_t>(ex->svh_u), dptr<const uint16_t>(ex->suh_d),
+                                   dptr<uint16_t>(sc->xd), n, pairs, I, 1, S, E, __builtin_inff(), 1);
+        if (r) return r;
+        item_gemm_dispatch(s, ex->cb, wide, dptr<const uint16_t>(sc->xd), dptr<const uint16_t>(sc->xd),
+                           dptr<const int64_t>(ex->ptr[2]), dptr<const int64_t>(ex->ptr[2]),
+                           dptr<const int>(ex->k2[2]), dptr<const int>(ex->k2[2]), dptr<const int>(sc->sorted),
+                           dptr<const int>(sc->items), dptr<const int>(sc->count), dptr<float>(sc->plane), (int)I,
+                           (int)D, (int)pairs, 1, max_items, c->status);
+        r = launched();
+        if (r) return r;
+        // slots without an expert add nothing (the reference's route skips them); fp16 sums go through an fp32
+        // staging buffer (xg, free by now)
+        float* o32 = half_sums ? dptr<float>(sc->xg) : static_cast<float*>(out) + (size_t)r0 * D;
+        r = launch_down_combine(s, dptr<const float>(sc->plane), pk, dptr<const uint16_t>(ex->svh_d),
+                                dptr<float>(sc->plane), wt, o32, n, pairs, D, 1, S, E, true);
+        if (r) return r;
+        const size_t cnt = (size_t)n * D;
+        if (half_sums) {
+            to_half_kernel<<<1024, 256, 0, s>>>(o32, static_cast<uint16_t*>(out) + (size_t)r0 * D, cnt);
+            r = launched();
+        } else if (do_round) {
+            round_kernel<<<1024, 256, 0, s>>>(o32, cnt);
+            r = launched();
+        }
+        if (r) return r;
+    }
+    return EA_OK;
+}
+
+}  // extern "C"

@@ -302,13 +302,16 @@ void or_rot_in(const void* x, int x_dtype, int x_stride, const int* pick, const 
 /* W_q [K, N] fp32 of an expert-layout matrix whose trellis rows are ns tiles apart. */
 static float* dequant_f32(const uint32_t* T, int ns, int K, int N, int k2, int cb) {
     float* W = (float*)malloc(sizeof(float) * (size_t)K * N);
-    float w[256];
-    for (int kt = 0; kt < K / 16; ++kt)
+    (void)lut_of(cb); /* built before the threads start */
+#pragma omp parallel for schedule(static)
+    for (int kt = 0; kt < K / 16; ++kt) {
+        float w[256];
         for (int nt = 0; nt < N / 16; ++nt) {
             decode_tile_f32(T + ((size_t)kt * ns + nt) * (4 * k2), k2, cb, w);
             for (int r = 0; r < 16; ++r)
                 for (int c = 0; c < 16; ++c) W[(size_t)(kt * 16 + r) * N + nt * 16 + c] = w[r * 16 + c];
         }
+    }
     return W;
 }
 
@@ -319,16 +322,18 @@ void or_grouped(const or_grouped_args* a) {
     const int KT = a->K >> 4, NS = a->ns > 0 ? a->ns : a->N >> 4;
     const int per_split = KT / a->SK, W = a->warps > 0 ? a->warps : 1, per_warp = per_split / W;
     const int N = a->N;
-    float* acc = (float*)malloc(sizeof(float) * (size_t)W * N);
     for (int u = 0; u < *a->ucount && u < a->nexp_max; ++u) {
         const int e = a->uids[u];
         for (int mat = 0; mat < a->mats; ++mat) {
             const uint16_t* X = mat ? a->x1 : a->x0;
             float* Wq = dequant_f32(mat ? a->tp1[e] : a->tp0[e], NS, a->K, N, mat ? a->k2_1[e] : a->k2_0[e], a->cb);
-            for (int m = 0; m < a->maxm; ++m) {
+            int nm = 0;
+            while (nm < a->maxm && a->members[u * a->maxm + nm] >= 0) ++nm;
+#pragma omp parallel for schedule(dynamic)
+            for (int m = 0; m < nm; ++m) {
                 const int code = a->members[u * a->maxm + m];
-                if (code < 0) break;
                 const int r = (code >> 5) * a->slots + (code & 31);
+                float* acc = (float*)malloc(sizeof(float) * (size_t)W * N);
                 for (int split = 0; split < a->SK; ++split) {
                     memset(acc, 0, sizeof(float) * (size_t)W * N);
                     for (int w = 0; w < W; ++w) {
@@ -347,11 +352,11 @@ void or_grouped(const or_grouped_args* a) {
                         z[n] = s;
                     }
                 }
+                free(acc);
             }
             free(Wq);
         }
     }
-    free(acc);
 }
 
 /* exl3_experts.cu:142-184 */
@@ -547,16 +552,20 @@ void or_exl3_linear(const uint16_t* xh, const uint32_t* T, int64_t stride_k, int
                     const uint16_t* bias, void* y, int y_dtype, int M, int K, int N, int k2, int cb, int SK, int WK) {
     const int KT = K / 16, per_warp = KT / SK / WK, TW = 4 * k2;
     float* W = (float*)malloc(sizeof(float) * (size_t)K * N);
-    float w[256];
-    for (int kt = 0; kt < KT; ++kt)
+    (void)lut_of(cb);
+#pragma omp parallel for schedule(static)
+    for (int kt = 0; kt < KT; ++kt) {
+        float w[256];
         for (int nt = 0; nt < N / 16; ++nt) {
             decode_tile_f32(T + kt * stride_k + (nt / 8) * stride_nb + (nt % 8) * TW, k2, cb, w);
             for (int r = 0; r < 16; ++r)
                 for (int c = 0; c < 16; ++c) W[(size_t)(kt * 16 + r) * N + nt * 16 + c] = w[r * 16 + c];
         }
-    float* acc = (float*)malloc(sizeof(float) * (size_t)SK * WK * N);
-    float v[128];
+    }
+#pragma omp parallel for schedule(dynamic)
     for (int r = 0; r < M; ++r) {
+        float* acc = (float*)malloc(sizeof(float) * (size_t)SK * WK * N);
+        float v[128];
         memset(acc, 0, sizeof(float) * (size_t)SK * WK * N);
         for (int s = 0; s < SK; ++s)
             for (int wk = 0; wk < WK; ++wk) {
@@ -586,9 +595,9 @@ void or_exl3_linear(const uint16_t* xh, const uint32_t* T, int64_t stride_k, int
                 store_y(y, y_dtype, (size_t)r * N + nb * 128 + c, o);
             }
         }
+        free(acc);
     }
     free(W);
-    free(acc);
 }
 
 /* ------------------------------------------------------------------------------------------------ */

@@ -1,0 +1,182 @@
+"""GPU parity of the EXL3 linear (the shared expert) and the prefill path through the C ABI against the CPU oracle:
+unpack bit-exact, rot_in bit-exact, linear outputs within fp32-accumulation tolerance with the split-K counters
+left at zero, the route exactly, and prompt_experts.run within 2e-3 * RMS(out) (also deterministic run to run)."""
+import numpy as np
+import pytest
+
+import oracle as orc
+from helpers import assert_close_rms, oracle_routed
+
+pytestmark = pytest.mark.gpu
+torch = pytest.importorskip("torch")
+
+
+@pytest.fixture(scope="module")
+def ea():
+    from ea_exl3 import device, linear, moe, prompt_experts, synth
+
+    device.init(0)
+    return device, linear, moe, prompt_experts, synth
+
+
+def _case(synth, M, K, N, k2, seed):
+    T = synth.trellis(seed, 0, 0, 0, K, N, k2)
+    suh = synth.scales(seed + 1, K, 1.0)
+    svh = synth.scales(seed + 2, N, 0.02)
+    x = synth.activations(seed + 3, M, K, "bf16")
+    return T, suh, svh, x
+
+
+@pytest.mark.parametrize("k2,cb", [(8, 1), (10, 2), (12, 2), (6, 1)])
+def test_unpack_bit_exact(ea, k2, cb):
+    device, linear, _, _, synth = ea
+    K, N = 256, 512
+    T = synth.trellis(60, 0, 0, 0, K, N, k2)
+    S = linear.strips(T, K, N, k2)
+    tw = 4 * k2
+    want = orc.dequant_expert(T, K, N, k2, cb)
+    dS, dW = device.upload(S), device.zeros((K, N), torch.int16)
+    linear.Kernels().unpack_w(device.stream(), dS.data_ptr(), dW.data_ptr(), K, N, k2, cb, 8 * tw, (K // 16) * 8 * tw)
+    np.testing.assert_array_equal(device.download(dW), want)
+
+
+@pytest.mark.parametrize("M,K,N,k2,cb,y_dtype", [
+    (1, 6144, 256, 8, 1, 1),     # the shared expert's gate / up at batch 1 (plan: SK 8, WK 4), bf16 out
+    (1, 256, 6144, 8, 1, 2),     # its down (SK 1), fp32 out
+    (16, 6144, 256, 10, 2, 2),   # 5-bit mul1 (the real checkpoints' shared expert), 16 rows
+    (40, 1024, 640, 8, 2, 0),    # three row passes, fp16 out
+    (128, 512, 384, 6, 1, 2),    # the most rows a call takes
+])
+def test_linear_call(ea, M, K, N, k2, cb, y_dtype):
+    device, linear, _, _, synth = ea
+    T, suh, svh, x = _case(synth, M, K, N, k2, 61 + M)
+    lin = linear.Linear(T, suh, svh, K, N, k2, cb)
+    xh_w = orc.exl3_rot_in(x, suh, M, K, bf16=True)
+    tw = 4 * k2
+    y_w = orc.exl3_linear(xh_w, linear.strips(T, K, N, k2), 8 * tw, (K // 16) * 8 * tw, svh, M, K, N, k2, cb, lin.sk,
+                          lin.wk, y_dtype=2)
+    sc = linear.Scratch(128, K, lin.sk * 128 * N)
+    dx = device.upload(x)
+    y = device.zeros((M, N), torch.float32 if y_dtype == 2 else torch.int16)
+    for rep in range(2):  # twice: the counters must be back at zero after each call
+        linear.call(device.stream(), sc, [lin], dx.data_ptr(), 1, M, [y.data_ptr()], [y_dtype])
+        np.testing.assert_array_equal(device.download(sc.xh[0][: M * K].view(torch.int16)).reshape(M, K), xh_w)
+        got = device.download(y)
+        if y_dtype == 2:
+            assert_close_rms(got, y_w, 1e-4, f"linear M={M} rep={rep}")
+        else:  # one rounding to fp16 / bf16 of the fp32 result: half an ulp of the format, plus the fp32 slack
+            got = got.view(np.float16).astype(np.float32) if y_dtype == 0 else synth.bf16_to_f32(got)
+            eps = 2.0 ** -11 if y_dtype == 0 else 2.0 ** -8
+            bound = eps * np.abs(y_w) + 1e-4 * np.sqrt(np.mean(y_w.astype(np.float64) ** 2))
+            assert np.all(np.abs(got - y_w) <= bound), f"linear M={M}: rounded output off"
+        assert int(device.download(lin.counters).sum()) == 0
+
+
+def test_linear_three_jobs_one_launch(ea):
+    device, linear, _, _, synth = ea
+    M, K = 3, 1024
+    shapes = [(256, 8), (512, 8), (128, 8)]
+    lins, wants, outs = [], [], []
+    x = synth.activations(70, M, K, "f16")
+    for i, (N, k2) in enumerate(shapes):
+        T = synth.trellis(71 + i, 0, 0, 0, K, N, k2)
+        suh, svh = synth.scales(72 + i, K, 1.0), synth.scales(73 + i, N, 0.02)
+        lin = linear.Linear(T, suh, svh, K, N, k2, 1)
+        lins.append(lin)
+        xh = orc.exl3_rot_in(x, suh, M, K)
+        tw = 4 * k2
+        wants.append(orc.exl3_linear(xh, linear.strips(T, K, N, k2), 8 * tw, (K // 16) * 8 * tw, svh, M, K, N, k2,
+                                     1, lin.sk, lin.wk))
+        outs.append(device.zeros((M, N), torch.float32))
+    sc = linear.Scratch(M, K, max(l.sk * M * l.n for l in lins))
+    linear.call(device.stream(), sc, lins, device.upload(x).data_ptr(), 0, M, [o.data_ptr() for o in outs], [2, 2, 2])
+    for o, w, l in zip(outs, wants, lins):
+        assert_close_rms(device.download(o), w, 1e-4, "job")
+        assert int(device.download(l.counters).sum()) == 0
+
+
+def test_linear_errors(ea):
+    device, linear, _, _, synth = ea
+    from ea_exl3._lib import EaError
+
+    T, suh, svh, x = _case(synth, 1, 256, 128, 8, 80)
+    a = linear.Linear(T, suh, svh, 256, 128, 8, 1)
+    T2 = synth.trellis(81, 0, 0, 0, 512, 128, 8)
+    b = linear.Linear(T2, synth.scales(82, 512, 1.0), svh, 512, 128, 8, 1)
+    sc = linear.Scratch(1, 512, 4096)
+    y = device.zeros((1, 128), torch.float32)
+    with pytest.raises(EaError) as e:  # different K: not groupable (linear.zig:270-275)
+        linear.call(device.stream(), sc, [a, b], device.upload(x).data_ptr(), 1, 1, [y.data_ptr()] * 2, [2, 2])
+    assert e.value.code == 14
+    with pytest.raises(EaError) as e:  # 129 rows
+        linear.call(device.stream(), sc, [a], device.upload(x).data_ptr(), 1, 129, [y.data_ptr()], [2])
+    assert e.value.code == 14
+
+
+# ---- prefill -------------------------------------------------------------------------------------------------------
+
+def _prompt_case(ea, R, E, D, I, k2, seed, x_dtype=1, zipf=True):
+    device, _, moe, pe, synth = ea
+    slots = 8
+    pick = synth.picks_zipf(seed, R, 1.1, E, slots) if zipf else synth.picks_uniform(seed, R, E, slots)
+    wts = synth.routing_weights(seed + 1, R, slots)
+    host = synth.HostLayer(seed + 2, experts=E, dims=D, width=I, k2=k2, only=np.unique(pick))
+    x = synth.activations(seed + 3, R, D, ["f16", "bf16", "f32"][x_dtype])
+    ex = moe.Routed(host)
+    assert pe.supported(ex)
+    sc = pe.Scratch(ex, R, slots)
+    dx, dp, dw = device.upload(x), device.upload(pick), device.upload(wts)
+    return host, ex, sc, x, pick, wts, dx, dp, dw
+
+
+@pytest.mark.parametrize("R,E,D,I,k2", [(130, 64, 512, 256, 8), (300, 256, 1024, 256, "mixed"), (40, 32, 256, 128, 6)])
+def test_prompt_experts_run(ea, R, E, D, I, k2):
+    device, _, _, pe, synth = ea
+    k2v = synth.mixed_widths(5, E) if k2 == "mixed" else k2
+    host, ex, sc, x, pick, wts, dx, dp, dw = _prompt_case(ea, R, E, D, I, k2v, 100 + R)
+    want = orc.prompt_experts(x, pick, wts, oracle_routed(host), R, 8, bf16=True)
+    out = device.zeros((R, D), torch.float32)
+    pe.run(device.stream(), dx.data_ptr(), D, dp.data_ptr(), dw.data_ptr(), ex, sc, out.data_ptr(), R, do_round=False)
+    got = device.download(out)
+    assert_close_rms(got, want, 2e-3, "prompt experts")
+    # the same bits on a second run (slots added in order, no atomics in the sums)
+    out2 = device.zeros((R, D), torch.float32)
+    pe.run(device.stream(), dx.data_ptr(), D, dp.data_ptr(), dw.data_ptr(), ex, sc, out2.data_ptr(), R, do_round=False)
+    np.testing.assert_array_equal(device.download(out2), got)
+    # do_round: each value through bf16
+    pe.run(device.stream(), dx.data_ptr(), D, dp.data_ptr(), dw.data_ptr(), ex, sc, out2.data_ptr(), R, do_round=True)
+    np.testing.assert_array_equal(device.download(out2), synth.bf16_to_f32(synth.bf16_bits(got)))
+    assert device.device_status() == 0
+
+
+def test_prompt_experts_full_shape_512(ea):
+    """BASELINE config 4 at its real shape: 512 rows, D 6144, I 256, 256 experts, Zipf(1.1), 4 bits, fp16 x."""
+    device, _, _, pe, synth = ea
+    R, D = 512, 6144
+    host, ex, sc, x, pick, wts, dx, dp, dw = _prompt_case(ea, R, 256, D, 256, 8, 200, x_dtype=0)
+    want = orc.prompt_experts(x, pick, wts, oracle_routed(host), R, 8)
+    out = device.zeros((R, D), torch.float32)
+    pe.run(device.stream(), dx.data_ptr(), D, dp.data_ptr(), dw.data_ptr(), ex, sc, out.data_ptr(), R,
+           do_round=False, x_dtype=0)
+    assert_close_rms(device.download(out), want, 2e-3, "prompt experts R=512")
+
+
+def test_prompt_half_sums_and_invalid(ea):
+    device, _, _, pe, synth = ea
+    from ea_exl3._lib import EaError
+
+    R, D = 20, 256
+    host, ex, sc, x, pick, wts, dx, dp, dw = _prompt_case(ea, R, 16, D, 128, 8, 300)
+    out = device.zeros((R, D), torch.float32)
+    with pytest.raises(EaError) as e:  # prompt_experts.zig:147: half sums and rounding together
+        pe.run(device.stream(), dx.data_ptr(), D, dp.data_ptr(), dw.data_ptr(), ex, sc, out.data_ptr(), R,
+               do_round=True, half_sums=True)
+    assert e.value.code == 13
+    pick2 = pick.copy()
+    pick2[0, 3] = -1  # a slot that is not an expert adds nothing
+    want = orc.prompt_experts(x, pick2, wts, oracle_routed(host), R, 8, bf16=True)
+    h = device.zeros((R, D), torch.float16)
+    pe.run(device.stream(), dx.data_ptr(), D, device.upload(pick2).data_ptr(), dw.data_ptr(), ex, sc, h.data_ptr(), R,
+           do_round=False, half_sums=True)
+    got = device.download(h).view(np.float16).astype(np.float32)
+    assert_close_rms(got, want, 2e-3, "half sums")
