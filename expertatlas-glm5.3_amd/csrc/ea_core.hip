@@ -5,6 +5,7 @@
 #include <vector>
 
 #include "ea_device.hpp"
+#include "ea_gemm.hpp"
 #include "ea_host.hpp"
 
 namespace ea {
@@ -23,22 +24,30 @@ DevCtx* ctx() {
 }
 
 // ---- dequantisation -------------------------------------------------------------------------------------------
-// One block a tile, one thread a value: thread (k, n) of the tile finds its stream value p by inverting the
-// placement (decode.cuh:134-136), reads the 16-bit window from two words and writes W[k][n] (coalesced rows).
+// A wave a tile, through the same lane decoder the GEMM kernels feed to MFMA (TileLane): lane l decodes the four
+// values of column l & 15 at rows 2g, 2g + 1, 2g + 8, 2g + 9 (g = l >> 4), so the bit-exact dequant tests pin
+// exactly the values the matrix products consume.
+template <int CB, int K2>
+__device__ __forceinline__ void unpack_tile(const uint32_t* __restrict__ tile, uint16_t* __restrict__ W, int N, int kt,
+                                            int nt, int lane) {
+    const TileLane<K2, CB> tl(lane);
+    const u2v v = tl.decode(tile);
+    const int n = nt * 16 + (lane & 15), g = (lane >> 4) & 3;
+    uint16_t* w = W + (size_t)(kt * 16 + 2 * g) * N + n;
+    w[0] = (uint16_t)(v.x & 0xffffu);
+    w[N] = (uint16_t)(v.x >> 16);
+    w[8 * (size_t)N] = (uint16_t)(v.y & 0xffffu);
+    w[9 * (size_t)N] = (uint16_t)(v.y >> 16);
+}
+
 template <int CB>
 __global__ void __launch_bounds__(256) unpack_kernel(const uint32_t* __restrict__ T, uint16_t* __restrict__ W, int N,
                                                      int k2, int64_t stride_k, int64_t stride_nb) {
-    const int nt = blockIdx.x, kt = blockIdx.y;
-    const int k = threadIdx.x >> 4, n = threadIdx.x & 15;
-    const int L = 4 * (n & 7) + ((k & 7) >> 1);
-    const int p = 8 * L + 4 * (n >> 3) + (k & 1) + 2 * (k >> 3);
-    const int TW = 4 * k2, NB = 128 * k2;
-    const int e = (k2 & 1) ? ((p + 1) * k2 - ((p + 1) & 1)) / 2 : (p + 1) * (k2 / 2);
-    const int b = (e - 16 + NB) % NB;
-    const uint32_t* tile = T + kt * stride_k + (nt >> 3) * stride_nb + (nt & 7) * TW;
-    const uint64_t q = ((uint64_t)tile[b >> 5] << 32) | tile[((b >> 5) + 1) % TW];
-    const uint32_t s = (uint32_t)(q >> (48 - (b & 31))) & 0xffffu;
-    W[(size_t)(kt * 16 + k) * N + nt * 16 + n] = __builtin_bit_cast(uint16_t, cb_value<CB>(s));
+    const int nt = blockIdx.x * 4 + (threadIdx.x >> 6), kt = blockIdx.y, lane = threadIdx.x & 63;
+    if (nt * 16 >= N) return;
+    const uint32_t* tile = T + kt * stride_k + (nt >> 3) * stride_nb + (nt & 7) * 4 * k2;
+    const bool ok = EA_K2_SWITCH(k2, 2, 16, (unpack_tile<CB, K2V>(tile, W, N, kt, nt, lane)));
+    (void)ok;
 }
 
 // ---- router top-8 ----------------------------------------------------------------------------------------------
@@ -106,6 +115,10 @@ __global__ void __launch_bounds__(256) swiglu2_kernel(const uint16_t* __restrict
     }
 }
 
+__global__ void __launch_bounds__(256) add_f32_kernel(float* __restrict__ a, const float* __restrict__ b, size_t n) {
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256) a[i] = a[i] + b[i];
+}
+
 }  // namespace ea
 
 using namespace ea;
@@ -134,6 +147,7 @@ const char* ea_strerror(int s) {
         case EA_NOT_INITIALIZED: return "ea_init was not called on this device";
         case EA_BAD_ARGUMENT: return "bad argument";
         case EA_UNSUPPORTED_WIDTH: return "an expert width (K2) or codebook this build has no decoder for";
+        case EA_WAIT_TIMEOUT: return "a dependency wait of the one-launch layer ran out (overlapping calls on one scratch?)";
         default: return "unknown status";
     }
 }
@@ -188,7 +202,7 @@ static int unpack_launch(ea_stream_t stream, const void* t, void* w, uint32_t kd
     EA_REQUIRE_CTX(c);
     if (!t || !w || kdim % 16 || n % 16 || kdim == 0 || n == 0) return EA_BAD_ARGUMENT;
     if (k2 < 2 || k2 > 16 || cb > 2) return EA_UNSUPPORTED_WIDTH;
-    dim3 grid(n / 16, kdim / 16);
+    dim3 grid((n / 16 + 3) / 4, kdim / 16);
     auto T = static_cast<const uint32_t*>(t);
     auto W = static_cast<uint16_t*>(w);
     hipStream_t s = as_stream(stream);
@@ -230,6 +244,16 @@ int ea_swiglu2(ea_stream_t stream, const void* g, const void* u, void* out, uint
     swiglu2_kernel<<<(unsigned)blocks, 256, 0, as_stream(stream)>>>(static_cast<const uint16_t*>(g),
                                                                    static_cast<const uint16_t*>(u),
                                                                    static_cast<uint16_t*>(out), n);
+    return launched();
+}
+
+int ea_add_f32(ea_stream_t stream, float* a, const float* b, size_t n) {
+    EA_REQUIRE_CTX(c);
+    if (!a || !b) return EA_BAD_ARGUMENT;
+    if (n == 0) return EA_OK;
+    size_t blocks = (n + 255) / 256;
+    if (blocks > (size_t)c->cus * 8) blocks = (size_t)c->cus * 8;
+    add_f32_kernel<<<(unsigned)blocks, 256, 0, as_stream(stream)>>>(a, b, n);
     return launched();
 }
 

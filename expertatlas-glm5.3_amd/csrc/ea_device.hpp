@@ -10,6 +10,11 @@ namespace ea {
 typedef _Float16 h2v __attribute__((ext_vector_type(2)));
 typedef _Float16 h4v __attribute__((ext_vector_type(4)));
 typedef _Float16 h8v __attribute__((ext_vector_type(8)));
+// Decoded B operands travel as packed words (two fp16 values a word, the first in the low half) and become h4v / h8v
+// only as whole registers: hipcc has mis-compiled fp16 element reads of a bit-cast vector (every element read as
+// element 0), so no code here reads single fp16 elements of a decoded pair.
+typedef uint32_t u2v __attribute__((ext_vector_type(2)));
+typedef uint32_t u4v __attribute__((ext_vector_type(4)));
 typedef float f4v __attribute__((ext_vector_type(4)));
 
 constexpr float HAD_SCALE = 0.08838834764831845f;  // 1 / sqrt(128) as fp32 (decode.cuh:163)
@@ -97,6 +102,32 @@ __device__ __forceinline__ _Float16 cb_value(uint32_t s) {
     }
 }
 
+// Two codebook values of two clean 16-bit states as a packed fp16 pair (the first in the low half): the same bits
+// as cb_value in 3.5 VALU instructions a value. mcg / 3inst: one multiply (and add) a state, two byte permutes
+// that pair the low halves and the high halves, one v_bitop3 a pair for (x & 0x8FFF8FFF) ^ 0x3B603B60 (truth table
+// 0x6A over (x, mask, pattern)), one packed fp16 add. mul1: multiply, byte sum by v_dot4, one packed fp16 fma.
+template <int CB>
+__device__ __forceinline__ uint32_t cb_pair(uint32_t s0, uint32_t s1) {
+    if constexpr (CB == CB_MUL1) {
+        const uint32_t h0 = __builtin_amdgcn_udot4(s0 * 0x83DCD12Du, 0x01010101u, 0x6400u, false);
+        const uint32_t h1 = __builtin_amdgcn_udot4(s1 * 0x83DCD12Du, 0x01010101u, 0x6400u, false);
+        const h2v hh = __builtin_bit_cast(h2v, h0 | (h1 << 16));
+        const h2v c1 = {__builtin_bit_cast(_Float16, (uint16_t)0x1eee), __builtin_bit_cast(_Float16, (uint16_t)0x1eee)};
+        const h2v c0 = {__builtin_bit_cast(_Float16, (uint16_t)0xc931), __builtin_bit_cast(_Float16, (uint16_t)0xc931)};
+        return __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(hh, c1, c0));
+    } else {
+        const uint32_t x0 = (CB == CB_MCG) ? s0 * 0xCBAC1FEDu : s0 * 89226354u + 64248484u;
+        const uint32_t x1 = (CB == CB_MCG) ? s1 * 0xCBAC1FEDu : s1 * 89226354u + 64248484u;
+        // the mask and xor are the same in both halves, so pair the low halves and the high halves first: one
+        // bitop3 ((x & m) ^ c, table 0x6A) each, then one packed fp16 add gives both values
+        const uint32_t lo = __builtin_amdgcn_perm(x1, x0, 0x05040100u);  // (x0.lo, x1.lo)
+        const uint32_t hi = __builtin_amdgcn_perm(x1, x0, 0x07060302u);  // (x0.hi, x1.hi)
+        const h2v a = __builtin_bit_cast(h2v, __builtin_amdgcn_bitop3_b32(lo, 0x8FFF8FFFu, 0x3B603B60u, 0x6A));
+        const h2v b = __builtin_bit_cast(h2v, __builtin_amdgcn_bitop3_b32(hi, 0x8FFF8FFFu, 0x3B603B60u, 0x6A));
+        return __builtin_bit_cast(uint32_t, a + b);
+    }
+}
+
 // A lane's view of four consecutive stream values p0 .. p0 + 3 (p0 even) of a tile, for K2 <= 10: their four
 // windows lie inside the 32 stream bits that start at the first window, so one funnel shift of two words gives
 // all four. Lane constants: the two word indices and the shift.
@@ -112,18 +143,17 @@ __host__ __device__ constexpr Quad quad_of(int p0) {
     return Quad{a % TW, (a + 1) % TW, 32 - (b0 - 32 * a)};
 }
 
-// The four values from the lane's two words.
+// The four values from the lane's two words: one funnel shift, then a bit-field extract a state.
 template <int K2, int CB>
-__device__ __forceinline__ h4v decode_quad(uint32_t wa, uint32_t wb, int sh) {
+__device__ __forceinline__ u2v decode_quad(uint32_t wa, uint32_t wb, int sh) {
     static_assert(K2 >= 2 && K2 <= 10, "the four windows must fit in 32 stream bits");
     const uint32_t seg = __builtin_amdgcn_alignbit(wa, wb, (uint32_t)sh);
     constexpr int e0 = stream_end<K2>(0);
-    h4v v;
-    v[0] = cb_value<CB>(seg >> 16);
-    v[1] = cb_value<CB>(seg >> (16 - (stream_end<K2>(1) - e0)));
-    v[2] = cb_value<CB>(seg >> (16 - (stream_end<K2>(2) - e0)));
-    v[3] = cb_value<CB>(seg >> (16 - (stream_end<K2>(3) - e0)));
-    return v;
+    const uint32_t s0 = seg >> 16;
+    const uint32_t s1 = __builtin_amdgcn_ubfe(seg, 16 - (stream_end<K2>(1) - e0), 16);
+    const uint32_t s2 = __builtin_amdgcn_ubfe(seg, 16 - (stream_end<K2>(2) - e0), 16);
+    const uint32_t s3 = __builtin_amdgcn_ubfe(seg, 16 - (stream_end<K2>(3) - e0), 16);
+    return u2v{cb_pair<CB>(s0, s1), cb_pair<CB>(s2, s3)};
 }
 
 // Wider widths (K2 11..16): the four windows span up to 40 stream bits, so the lane reads three words and makes a
@@ -141,19 +171,19 @@ __host__ __device__ constexpr Quad3 quad3_of(int p0) {
 }
 
 template <int K2, int CB>
-__device__ __forceinline__ h4v decode_quad3(uint32_t w0, uint32_t w1, uint32_t w2, int sh) {
+__device__ __forceinline__ u2v decode_quad3(uint32_t w0, uint32_t w1, uint32_t w2, int sh) {
     static_assert(K2 >= 11 && K2 <= 16, "three-word form");
     const uint32_t hi = __builtin_amdgcn_alignbit(w0, w1, (uint32_t)sh);
     const uint32_t lo = __builtin_amdgcn_alignbit(w1, w2, (uint32_t)sh);
     constexpr int e0 = stream_end<K2>(0);
-    h4v v;
+    uint32_t s[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int d = (i == 0) ? 0 : (i == 1 ? stream_end<K2>(1) - e0 : (i == 2 ? stream_end<K2>(2) - e0 : stream_end<K2>(3) - e0));
-        const uint32_t s = d <= 16 ? (hi >> (16 - d)) : __builtin_amdgcn_alignbit(hi, lo, (uint32_t)(48 - d));
-        v[i] = cb_value<CB>(s);
+        s[i] = d <= 16 ? __builtin_amdgcn_ubfe(hi, 16 - d, 16)
+                       : (__builtin_amdgcn_alignbit(hi, lo, (uint32_t)(48 - d)) & 0xffffu);
     }
-    return v;
+    return u2v{cb_pair<CB>(s[0], s[1]), cb_pair<CB>(s[2], s[3])};
 }
 
 // MFMA 16x16x16 f16 B-operand layout for one tile: lane l holds B[k'][n] for n = l & 15 and k' = 4 (l >> 4) + i.

@@ -6,9 +6,15 @@
 
 namespace ea {
 
+typedef const __attribute__((address_space(1))) uint32_t* gptr_u32;
+
+// A global-memory load the compiler can see is global (not flat): trellis tables hold plain 64-bit addresses.
+__device__ __forceinline__ uint32_t gload(const uint32_t* p) { return *(gptr_u32)(p); }
+
 // A lane's constant view of any tile for K2 (its word indices and funnel shift; see quad_of / quad3_of).
 template <int K2, int CB>
 struct TileLane {
+    static constexpr int NW = K2 <= 10 ? 2 : 3;  // words a lane reads from a tile
     int w0, w1, w2, sh;
     __device__ __forceinline__ explicit TileLane(int lane) {
         if constexpr (K2 <= 10) {
@@ -25,17 +31,28 @@ struct TileLane {
             sh = q.sh;
         }
     }
+    // This lane's words of the tile starting at `tile`.
+    __device__ __forceinline__ void fetch(const uint32_t* __restrict__ tile, uint32_t (&w)[NW]) const {
+        w[0] = gload(tile + w0);
+        w[1] = gload(tile + w1);
+        if constexpr (NW == 3) w[2] = gload(tile + w2);
+    }
+    // The four values as two packed words (values 0, 1 in .x; 2, 3 in .y).
+    __device__ __forceinline__ u2v decode(const uint32_t (&w)[NW]) const {
+        if constexpr (K2 <= 10) return decode_quad<K2, CB>(w[0], w[1], sh);
+        else return decode_quad3<K2, CB>(w[0], w[1], w[2], sh);
+    }
     // This lane's four B values of the tile starting at `tile`.
-    __device__ __forceinline__ h4v decode(const uint32_t* __restrict__ tile) const {
-        if constexpr (K2 <= 10) return decode_quad<K2, CB>(tile[w0], tile[w1], sh);
-        else return decode_quad3<K2, CB>(tile[w0], tile[w1], tile[w2], sh);
+    __device__ __forceinline__ u2v decode(const uint32_t* __restrict__ tile) const {
+        uint32_t w[NW];
+        fetch(tile, w);
+        return decode(w);
     }
 };
 
 // The lane's A operand of a two-tile k step at k = k0 (16x16x32): rows k0 + 2g, +1, +8, +9 and the same 16 later,
 // g = lane >> 4; the same k permutation as the decoded B operand.
 __device__ __forceinline__ h8v load_a8(const uint16_t* __restrict__ xrow, int k0, int lane) {
-    typedef uint32_t u4v __attribute__((ext_vector_type(4)));
     if (!xrow) return h8v{0, 0, 0, 0, 0, 0, 0, 0};
     const uint16_t* xk = xrow + k0 + 2 * ((lane >> 4) & 3);
     const u4v au = {*reinterpret_cast<const uint32_t*>(xk), *reinterpret_cast<const uint32_t*>(xk + 8),
@@ -44,7 +61,6 @@ __device__ __forceinline__ h8v load_a8(const uint16_t* __restrict__ xrow, int k0
 }
 
 __device__ __forceinline__ h4v load_a4(const uint16_t* __restrict__ xrow, int k0, int lane) {
-    typedef uint32_t u2v __attribute__((ext_vector_type(2)));
     if (!xrow) return h4v{0, 0, 0, 0};
     const uint16_t* xk = xrow + k0 + 2 * ((lane >> 4) & 3);
     const u2v au = {*reinterpret_cast<const uint32_t*>(xk), *reinterpret_cast<const uint32_t*>(xk + 8)};
@@ -54,34 +70,67 @@ __device__ __forceinline__ h4v load_a4(const uint16_t* __restrict__ xrow, int k0
 // acc[m][j] += rows(m) @ tiles: tile (t, j) of the strip at base + t * kstride + j * TW words for t in [0, nkt);
 // xrow[m]: this lane's activation row (lane & 15) of row group m, or nullptr; k0: the k of tile 0.
 // Output layout of acc[m][j]: lane l holds D[4 (l >> 4) + i][l & 15] (row, column within the 16 x 16 tile).
+// Software-pipelined: the trellis words of the next two-tile step are in flight while this step decodes.
 template <int CB, int K2, int NTW, int MG>
 __device__ __forceinline__ void wave_tiles(const uint32_t* __restrict__ base, size_t kstride, int nkt, int k0,
                                            const uint16_t* const (&xrow)[MG], int lane, f4v (&acc)[MG][NTW]) {
     constexpr int TW = 4 * K2;
-    const TileLane<K2, CB> tl(lane);
-    int t = 0;
-    for (; t + 2 <= nkt; t += 2) {
-        h8v a[MG];
-#pragma unroll
-        for (int m = 0; m < MG; ++m) a[m] = load_a8(xrow[m], k0 + t * 16, lane);
+    using TL = TileLane<K2, CB>;
+    constexpr int NWD = TL::NW;
+    const TL tl(lane);
+    uint32_t wa[NTW][2][NWD], wb[NTW][2][NWD];
+    auto fetch = [&](uint32_t (&w)[NTW][2][NWD], int t) {
         const uint32_t* t0 = base + (size_t)t * kstride;
 #pragma unroll
         for (int j = 0; j < NTW; ++j) {
-            const h4v b0 = tl.decode(t0 + j * TW);
-            const h4v b1 = tl.decode(t0 + kstride + j * TW);
-            const h8v b = {b0[0], b0[1], b0[2], b0[3], b1[0], b1[1], b1[2], b1[3]};
+            tl.fetch(t0 + j * TW, w[j][0]);
+            tl.fetch(t0 + kstride + j * TW, w[j][1]);
+        }
+    };
+    // the activations of a step are loaded before the next step's trellis words, so waiting for them leaves the
+    // trellis prefetch in flight (loads complete in issue order)
+    auto load_a = [&](h8v (&a)[MG], int t) {
+#pragma unroll
+        for (int m = 0; m < MG; ++m) a[m] = load_a8(xrow[m], k0 + t * 16, lane);
+    };
+    auto compute = [&](uint32_t (&w)[NTW][2][NWD], const h8v (&a)[MG]) {
+#pragma unroll
+        for (int j = 0; j < NTW; ++j) {
+            const u2v b0 = tl.decode(w[j][0]);
+            const u2v b1 = tl.decode(w[j][1]);
+            const h8v b = __builtin_bit_cast(h8v, (u4v{b0.x, b0.y, b1.x, b1.y}));
 #pragma unroll
             for (int m = 0; m < MG; ++m) acc[m][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[m], b, acc[m][j], 0, 0, 0);
         }
+    };
+    const int steps = nkt >> 1;
+    if (steps > 0) fetch(wa, 0);
+    int s = 0;
+    for (; s + 2 <= steps; s += 2) {
+        h8v a0[MG], a1[MG];
+        load_a(a0, 2 * s);
+        fetch(wb, 2 * s + 2);
+        asm volatile("" ::: "memory");  // keep the prefetch issued ahead of this step's decode
+        compute(wa, a0);
+        load_a(a1, 2 * s + 2);
+        if (s + 2 < steps) fetch(wa, 2 * s + 4);
+        asm volatile("" ::: "memory");
+        compute(wb, a1);
     }
-    if (t < nkt) {
+    if (s < steps) {
+        h8v a0[MG];
+        load_a(a0, 2 * s);
+        compute(wa, a0);
+    }
+    if (nkt & 1) {
+        const int t = nkt - 1;
         h4v a[MG];
 #pragma unroll
         for (int m = 0; m < MG; ++m) a[m] = load_a4(xrow[m], k0 + t * 16, lane);
         const uint32_t* t0 = base + (size_t)t * kstride;
 #pragma unroll
         for (int j = 0; j < NTW; ++j) {
-            const h4v b = tl.decode(t0 + j * TW);
+            const h4v b = __builtin_bit_cast(h4v, tl.decode(t0 + j * TW));
 #pragma unroll
             for (int m = 0; m < MG; ++m) acc[m][j] = __builtin_amdgcn_mfma_f32_16x16x16f16(a[m], b, acc[m][j], 0, 0, 0);
         }

@@ -14,7 +14,7 @@ constexpr uint32_t DOWN_CFG[4] = {8, 4, 1, 1};
 static size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
 
 struct MoeLayout {
-    size_t xg, xu, xd, z, y, ids, count, members, sync, total;
+    size_t xg, xu, xd, z, y, ids, count, members, sync, fused, fused_bytes, total;
 };
 
 static MoeLayout moe_layout(const ea_routed* ex, uint32_t rows, uint32_t slots) {
@@ -37,6 +37,8 @@ static MoeLayout moe_layout(const ea_routed* ex, uint32_t rows, uint32_t slots) 
     l.count = take(16);
     l.members = take(maxu * rows * 4);
     l.sync = take(4096);
+    l.fused_bytes = dl_region_bytes(rows, slots, (uint32_t)D, (uint32_t)I, ex->count);
+    l.fused = take(l.fused_bytes);
     l.total = off;
     return l;
 }
@@ -82,6 +84,7 @@ int ea_moe_scratch_init(ea_stream_t stream, ea_moe_scratch* s, void* base, size_
     s->count = b + l.count;
     s->members = b + l.members;
     s->sync = b + l.sync;
+    s->fused = l.fused_bytes ? b + l.fused : 0;
     s->rows = rows;
     s->slots = slots;
     // moe.zig:271-272: everything zero, members -1
@@ -100,6 +103,9 @@ int ea_moe_routed(ea_stream_t stream, const void* x, int x_dtype, uint32_t x_str
     if (R > sc->rows) return EA_SCRATCH_TOO_SMALL;
     if (R == 0) return EA_OK;
     hipStream_t s = as_stream(stream);
+    const int f = decode_layer(s, x, x_dtype, x_stride, nullptr, nullptr, 0.f, const_cast<int32_t*>(pick),
+                               const_cast<float*>(wts), ex, nullptr, sc, out, R);
+    if (f != EA_UNPORTED_GROUPED_VARIANT) return f;
     const uint32_t D = ex->dims, I = ex->width, E = ex->count, slots = sc->slots, P = R * slots;
     const uint32_t maxu = P < E ? P : E;
     int r = launch_group(s, pick, dptr<int>(sc->ids), dptr<int>(sc->count), dptr<int>(sc->members), R, slots, E, R);

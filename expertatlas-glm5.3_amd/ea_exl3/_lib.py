@@ -34,7 +34,7 @@ class Routed(C.Structure):
 
 class MoeScratch(C.Structure):
     _fields_ = [("xg", U64), ("xu", U64), ("xd", U64), ("z", U64), ("y", U64), ("ids", U64), ("count", U64),
-                ("members", U64), ("sync", U64), ("rows", U32), ("slots", U32)]
+                ("members", U64), ("sync", U64), ("fused", U64), ("rows", U32), ("slots", U32)]
 
 
 class PromptScratch(C.Structure):
@@ -97,6 +97,8 @@ SIGNATURES = {
                                      C.POINTER(U64), C.POINTER(C.c_int)]),
     "ea_topk8": (I32, [P, P, P, P, P, U32, F32, P]),
     "ea_swiglu2": (I32, [P, P, P, P, U32, U32]),
+    "ea_add_f32": (I32, [P, P, P, C.c_size_t]),
+    "ea_ffn_moe_decode": (I32, [P, P, I32, U32, P, P, F32, P, P, C.POINTER(Routed), P, C.POINTER(MoeScratch), P, U32]),
 }
 
 _lib = None

@@ -83,3 +83,18 @@ def routed(stream: int, x: int, x_stride: int, pick: int, wts: int, ex: Routed, 
     """moe.routed (moe.zig:279-293): out fp32 [R, D] = the routed experts of R rows weighted by wts."""
     check(lib().ea_moe_routed(stream, x, x_dtype, x_stride, pick, wts, C.byref(ex.c), C.byref(s.c), out, R),
           "routed")
+
+
+def ffn_decode(stream: int, x: int, x_stride: int, logits: int, bias: int, scale: float, pick: int, wts: int,
+               ex: Routed, shared, s: Scratch, out: int, R: int, x_dtype: int = 1) -> None:
+    """ffnMain's expert part in one launch (forward.zig:2361-2403): top-8 of logits into pick / wts, then out fp32
+    [R, D] = moe.routed(x) + the shared expert's mlp(x). shared: (gate, up, down) ctypes ea_linear structs, or None
+    for the routed part alone."""
+    arr = None
+    if shared is not None:
+        from ._lib import Linear as _Linear
+
+        arr = (C.POINTER(_Linear) * 3)(*[C.pointer(l) for l in shared])
+    check(lib().ea_ffn_moe_decode(stream, x, x_dtype, x_stride, logits, bias, scale, pick, wts, C.byref(ex.c),
+                                  C.addressof(arr) if arr is not None else None,
+                                  C.byref(s.c), out, R), "ffn_decode")

@@ -12,3 +12,8 @@ def topk(stream: int, logits: int, bias: int, pick: int, wts: int, rows: int, sc
 def swiglu2(stream: int, g: int, u: int, out: int, rows: int, width: int) -> None:
     """out = bf16(bf16(silu(g)) * u), bf16 rows of `width`."""
     check(lib().ea_swiglu2(stream, g, u, out, rows, width), "swiglu2")
+
+
+def add_f32(stream: int, a: int, b: int, n: int) -> None:
+    """a += b over n fp32 values (glue.addF32)."""
+    check(lib().ea_add_f32(stream, a, b, n), "addF32")

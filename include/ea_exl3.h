@@ -44,7 +44,9 @@ typedef enum ea_status {
     EA_OUT_OF_DEVICE_MEMORY = 16,     /* driver.zig error.OutOfDeviceMemory */
     EA_NOT_INITIALIZED = 17,          /* a call before ea_init on this device */
     EA_BAD_ARGUMENT = 18,             /* a null pointer or a size outside the documented range */
-    EA_UNSUPPORTED_WIDTH = 19         /* a K2 / codebook this build has no decoder for */
+    EA_UNSUPPORTED_WIDTH = 19,        /* a K2 / codebook this build has no decoder for */
+    EA_WAIT_TIMEOUT = 20              /* a one-launch layer's dependency wait ran out (its scratch was shared by
+                                         overlapping calls); the launch drained, its output is not valid */
 } ea_status;
 
 enum { EA_F16 = 0, EA_BF16 = 1, EA_F32 = 2 };
@@ -122,7 +124,8 @@ typedef struct ea_routed {
 /* moe.zig:242-275 Scratch, carved from one caller-owned device buffer. */
 typedef struct ea_moe_scratch {
     uint64_t xg, xu, xd, z, y, ids, count, members;
-    uint64_t sync;         /* completion counters of the one-launch layer (zeroed by ea_moe_scratch_init) */
+    uint64_t sync;         /* reserved counters (zeroed by ea_moe_scratch_init) */
+    uint64_t fused;        /* the one-launch decode layer's region (rows <= 16), else 0; zeroed by init */
     uint32_t rows, slots;
 } ea_moe_scratch;
 
@@ -133,9 +136,12 @@ int ea_moe_scratch_init(ea_stream_t stream, ea_moe_scratch* s, void* base, size_
                         uint32_t rows, uint32_t slots);
 
 /* out fp32 [R, D] = the R rows' routed experts weighted by wts. Replaces moe.routed (moe.zig:279-293).
- * x: [R, D] rows x_stride apart; pick int32 / wts fp32 [R, slots]. */
+ * x: [R, D] rows x_stride apart; pick int32 / wts fp32 [R, slots]. With a scratch of at most 16 rows, widths
+ * 2..10, mcg or mul1 and I of 128 or 256, the layer is one persistent launch; otherwise the six-launch sequence of
+ * moe.zig:279-293. */
 int ea_moe_routed(ea_stream_t stream, const void* x, int x_dtype, uint32_t x_stride, const int32_t* pick,
                   const float* wts, const ea_routed* ex, const ea_moe_scratch* s, float* out, uint32_t R);
+
 
 /* ---- routed experts, prefill path (prompt_experts.zig) ----------------------------------------------------- */
 
@@ -210,6 +216,24 @@ int ea_topk8(ea_stream_t stream, const float* logits, const float* bias, int32_t
 
 /* out = bf16(bf16(silu(g)) * u) over rows of `width` bf16. Replaces ops.swiglu2 (native_ops.cu:429-441). */
 int ea_swiglu2(ea_stream_t stream, const void* g, const void* u, void* out, uint32_t rows, uint32_t width);
+
+/* a[i] += b[i] for n fp32 values: the routed part plus the shared expert (forward.zig:2403 -> glue.addF32,
+ * glue.cu:57). */
+int ea_add_f32(ea_stream_t stream, float* a, const float* b, size_t n);
+
+/* ---- the decode layer in one launch ------------------------------------------------------------------------- */
+
+/* ffnMain's expert part for a decode window in one launch: pick / wts [R, 8] = top-8 of logits [R, 256] (as
+ * ea_topk8, written out), out [R, D] = moe.routed(x) + the shared expert's mlp(x) (gate and up EXL3 linears with
+ * bf16 outputs, swiglu2, the down linear with fp32 output), or the routed part alone when shared is NULL.
+ * Replaces the sequence ops.topk -> moe.routed -> forward.mlp -> glue.addF32 of forward.zig:2361-2403 (the
+ * reference's decode graph issues those as separate launches). shared: gate, up, down ea_linear (k, n = D, I / I, D;
+ * one width in 2..10 and one codebook among the three). Needs s from ea_moe_scratch_init with rows <= 16, R <= rows,
+ * E = 256, slots = 8, I of 128 or 256, routed widths 2..10, codebooks mcg / mul1; EA_UNPORTED_GROUPED_VARIANT
+ * otherwise. Concurrent calls sharing one scratch race. */
+int ea_ffn_moe_decode(ea_stream_t stream, const void* x, int x_dtype, uint32_t x_stride, const float* logits,
+                      const float* bias, float scale, int32_t* pick, float* wts, const ea_routed* ex,
+                      const ea_linear* const* shared, const ea_moe_scratch* s, float* out, uint32_t R);
 
 #ifdef __cplusplus
 }

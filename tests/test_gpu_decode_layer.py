@@ -1,0 +1,145 @@
+"""GPU parity of the one-launch decode layer through the C ABI. ea_ffn_moe_decode (top-8 from the router logits, the
+routed experts, the shared expert's mlp and their sum) is checked against the oracle's composition of the same
+reference steps (forward.zig:2361-2403): ops.topk -> moe.routed -> gate / up EXL3 linears with bf16 outputs ->
+swiglu2 -> down linear (fp32) -> addF32. pick / wts must match bit for bit; out within 2e-3 * RMS(out), the north
+star's bar. Calls repeat on one scratch with changing row counts, which exercises the launch-generation flags and
+the counters the kernel leaves at zero."""
+import numpy as np
+import pytest
+
+import oracle as orc
+from helpers import assert_close_rms, oracle_routed
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+
+@pytest.fixture(scope="module")
+def ea():
+    from ea_exl3 import device, linear, moe, synth
+
+    device.init(0)
+    return device, linear, moe, synth
+
+
+class SharedHost:
+    """The shared expert of one rank as three EXL3 linears (gate, up: D -> I; down: I -> D) on the host and device."""
+
+    def __init__(self, linear, synth, seed, D, I, k2, cb):
+        self.D, self.I, self.k2, self.cb = D, I, k2, cb
+        shapes = [(D, I), (D, I), (I, D)]
+        self.T = [synth.trellis(seed, 0, m, 0, K, N, k2) for m, (K, N) in enumerate(shapes)]
+        self.suh = [synth.scales(seed + 1 + m, K, 1.0) for m, (K, N) in enumerate(shapes)]
+        self.svh = [synth.scales(seed + 4 + m, N, 0.02) for m, (K, N) in enumerate(shapes)]
+        self.lin = [linear.Linear(self.T[m], self.suh[m], self.svh[m], K, N, k2, cb) for m, (K, N) in enumerate(shapes)]
+        self.strips = [linear.strips(self.T[m], K, N, k2) for m, (K, N) in enumerate(shapes)]
+
+    def oracle(self, x, R, bf16):
+        """forward.mlp (forward.zig:2328-2341): bf16 gate / up, swiglu2, fp32 down."""
+        tw = 4 * self.k2
+        outs = []
+        for m in range(2):
+            xh = orc.exl3_rot_in(x, self.suh[m], R, self.D, bf16=bf16)
+            outs.append(orc.exl3_linear(xh, self.strips[m], 8 * tw, (self.D // 16) * 8 * tw, self.svh[m], R, self.D,
+                                        self.I, self.k2, self.cb, self.lin[m].sk, self.lin[m].wk, y_dtype=1))
+        act = orc.swiglu2(outs[0], outs[1])
+        xh = orc.exl3_rot_in(act, self.suh[2], R, self.I, bf16=True)
+        return orc.exl3_linear(xh, self.strips[2], 8 * tw, (self.I // 16) * 8 * tw, self.svh[2], R, self.I, self.D,
+                               self.k2, self.cb, self.lin[2].sk, self.lin[2].wk, y_dtype=2)
+
+
+def _run(ea, host, shared, sc, ex, x, logits, bias, R, x_dtype):
+    device, _, moe, _ = ea
+    D = host.dims
+    dx, dl, db = device.upload(x), device.upload(logits), device.upload(bias)
+    dp, dw = device.zeros((R, 8), torch.int32), device.zeros((R, 8), torch.float32)
+    out = device.zeros((R, D), torch.float32)
+    moe.ffn_decode(device.stream(), dx.data_ptr(), D, dl.data_ptr(), db.data_ptr(), 2.5, dp.data_ptr(), dw.data_ptr(),
+                   ex, None if shared is None else [l.c for l in shared.lin], sc, out.data_ptr(), R, x_dtype=x_dtype)
+    got = device.download(out), device.download(dp), device.download(dw)
+    assert device.device_status() == 0
+    return got
+
+
+def _want(host, shared, x, logits, bias, R, bf16):
+    pick, wts = orc.topk8(logits, bias)
+    want = orc.moe_routed(x, pick, wts, oracle_routed(host), R, 8, bf16=bf16)
+    if shared is not None:
+        want = want + shared.oracle(x, R, bf16)
+    return want, pick, wts
+
+
+def _layer_for(synth, seed, logits_list, bias, E, D, I, k2, cb):
+    picks = np.concatenate([orc.topk8(l, bias)[0].reshape(-1) for l in logits_list])
+    return synth.HostLayer(seed, experts=E, dims=D, width=I, k2=k2, cb=cb, only=np.unique(picks))
+
+
+def _case(ea, rows_seq, D, I, k2, cb, shared_k2, shared_cb, x_dtype, seed, cap=16):
+    device, linear, moe, synth = ea
+    E = 256
+    logits_list, bias = [], None
+    for i, R in enumerate(rows_seq):
+        l, b = synth.logits(seed + i, R)
+        bias = b if bias is None else bias
+        logits_list.append(l)
+    host = _layer_for(synth, seed + 10, logits_list, bias, E, D, I, k2, cb)
+    shared = None if shared_k2 is None else SharedHost(linear, synth, seed + 20, D, I, shared_k2, shared_cb)
+    ex = moe.Routed(host)
+    sc = moe.Scratch(ex, cap, 8)
+    for i, R in enumerate(rows_seq):
+        x = synth.activations(seed + 30 + i, R, D, ["f16", "bf16"][x_dtype])
+        out, pick, wts = _run(ea, host, shared, sc, ex, x, logits_list[i], bias, R, x_dtype)
+        want, pick_w, wts_w = _want(host, shared, x, logits_list[i], bias, R, x_dtype == 1)
+        np.testing.assert_array_equal(pick, pick_w)
+        np.testing.assert_array_equal(wts, wts_w)
+        assert_close_rms(out, want, 2e-3, f"ffn decode R={R} call {i}")
+
+
+def test_ffn_decode_config2_shape(ea):
+    """BASELINE config 2 at its real shape: one token, D 6144, 256 experts x I 256 at 4 bits (mcg), the 4-bit shared
+    expert; three calls on one scratch."""
+    _case(ea, [1, 1, 1], 6144, 256, 8, 1, 8, 1, 0, 100)
+
+
+def test_ffn_decode_rows_change(ea):
+    """16 rows, then 3, then 16 again on one scratch; 3-bit routed experts, a 5-bit mul1 shared expert (the real
+    checkpoints' format), bf16 activations."""
+    _case(ea, [16, 3, 16], 6144, 256, 6, 1, 10, 2, 1, 200)
+
+
+def test_ffn_decode_mixed_widths(ea):
+    """Config 3's routed part: 16 rows, 70 % of the experts at 3 bits, the rest at 4; shared expert at 4 bits."""
+    device, linear, moe, synth = ea
+    _case(ea, [16], 6144, 256, synth.mixed_widths(301, 256), 1, 8, 1, 0, 300)
+
+
+def test_ffn_decode_routed_only_i128(ea):
+    """No shared expert, I = 128 (a TP=16 shard), mul1 routed experts."""
+    _case(ea, [5, 2], 2048, 128, 10, 2, None, None, 0, 400)
+
+
+def test_moe_routed_fused_matches_sequence(ea):
+    """ea_moe_routed takes the one-launch path for a scratch of <= 16 rows and the six-launch sequence above that;
+    both must meet the bar against the oracle on the same inputs (and agree with each other to the same bar)."""
+    device, linear, moe, synth = ea
+    R, E, D, I = 12, 256, 2048, 256
+    pick = synth.picks_uniform(500, R, E, 8)
+    pick[2, 3] = pick[2, 5]  # a row may name one expert twice (the caller's pick, not top-k's): two members
+    pick[2, 5] = pick[2, 3]
+    wts = synth.routing_weights(501, R, 8)
+    host = synth.HostLayer(502, experts=E, dims=D, width=I, k2=8, only=np.unique(pick))
+    x = synth.activations(503, R, D, "f16")
+    want = orc.moe_routed(x, pick, wts, oracle_routed(host), R, 8)
+    ex = moe.Routed(host)
+    dx, dp, dw = device.upload(x), device.upload(pick), device.upload(wts)
+    outs = []
+    for cap in (16, 32):
+        sc = moe.Scratch(ex, cap, 8)
+        assert (sc.c.fused != 0) == (cap <= 16)
+        out = device.zeros((R, D), torch.float32)
+        moe.routed(device.stream(), dx.data_ptr(), D, dp.data_ptr(), dw.data_ptr(), ex, sc, out.data_ptr(), R, x_dtype=0)
+        outs.append(device.download(out))
+        assert device.device_status() == 0
+        assert_close_rms(outs[-1], want, 2e-3, f"moe.routed cap={cap}")
+    assert_close_rms(outs[0], outs[1], 2e-3, "fused vs sequence")
