@@ -1,21 +1,27 @@
 #!/usr/bin/env python3
 """Benchmark of the EXL3 routed-expert path on one MI355X (gfx950).
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config decode|multi|prefill512|prefill2048|linear|stack]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config decode|multi|stack|linear|prefill512|prefill2048]
 
-A step is one pass of the hot path over one batch of synthetic input:
-  decode (default, BASELINE config 2): one GLM-5.3 MoE layer of a TP=8 rank at batch 1 -- router top-8 from logits,
-      the routed experts (moe.routed), the shared expert (EXL3 linears + SwiGLU) and their sum;
-  multi (config 3): the same layer at 16 rows, uniform top-8, 70 % of experts at 3 bits;
-  prefill512 / prefill2048 (config 4): prompt_experts.run over 512 / 2048 rows with Zipf(1.1) routing;
-  linear (config 1): one 4-bit EXL3 linear 6144 x 2048 at one row;
-  stack (config 5): 75 resident decode layers, one token through all of them.
-Expert shards live in HBM; the decode configs cycle through several distinct layers and draw fresh routing each step,
-so the touched experts are not resident in the 256 MB Infinity Cache. Prints one JSON line.
+A step is one pass of the hot path over one batch of synthetic input, with every input already in HBM:
+  decode (default; BASELINE config 2): one GLM-5.3 MoE layer of a TP=8 rank at batch 1 -- router top-8 from logits,
+      the routed experts (moe.routed), the shared expert (EXL3 linears + SwiGLU) and their sum, as the one launch of
+      ea_ffn_moe_decode;
+  multi (config 3): the same layer at 16 rows, uniform top-8, 70 % of the experts at 3 bits;
+  stack (config 5): 75 resident layers (3-bit for 70 % of the experts), one token through all of them (us / token);
+  linear (config 1): one 4-bit EXL3 linear 6144 x 2048 at one row (linear.call);
+  prefill512 / prefill2048 (config 4): prompt_experts.run over 512 / 2048 rows with Zipf(1.1) routing.
+The decode configs cycle through several distinct resident layers and draw fresh router logits every layer, so the
+touched experts are not sitting in the 256 MB Infinity Cache. Prints one JSON line.
+
+The dominant kernel's roofline is measured live: HIP events around each of its launches (on the stream the launches
+go to) over a second pass identical to the timed one; its algorithmic bytes per launch are the trellis + scales of
+every distinct expert the launch touches, the shared expert, the activations, logits and outputs.
 """
 from __future__ import annotations
 
 import argparse
+import ctypes as C
 import json
 import os
 import sys
@@ -27,6 +33,7 @@ sys.path.insert(0, os.path.join(ROOT, "expertatlas-glm5.3_amd"))
 HBM_PEAK_GBS = 8000.0        # MI355X HBM3E, GB/s
 FP16_PEAK_TFLOPS = 2500.0    # MI355X dense fp16 MFMA, TFLOP/s
 D, I, E, SLOTS = 6144, 256, 256, 8
+ROUTED_SCALE = 2.5           # config.zig:97,165 routed_scaling
 
 
 def baseline_metric() -> str:
@@ -40,8 +47,11 @@ def parse():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--config", default="decode",
-                    choices=["decode", "multi", "prefill512", "prefill2048", "linear", "stack"])
+                    choices=["decode", "multi", "stack", "linear", "prefill512", "prefill2048"])
     ap.add_argument("--layers", type=int, default=8, help="distinct resident layers the decode configs cycle through")
+    ap.add_argument("--path", default="fused", choices=["fused", "sequence"],
+                    help="decode configs: the one-launch layer, or the reference's launch sequence (topk, "
+                         "moe.routed's six launches, the shared expert's linears, swiglu2, add)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a plain device copy of known size (for HBM counter calibration)")
@@ -49,30 +59,33 @@ def parse():
     return ap.parse_args()
 
 
-# ---- the workloads ---------------------------------------------------------------------------------------------------
+# ---- the decode workloads ------------------------------------------------------------------------------------------
 
-class DecodeLayerBench:
-    """Router top-8 + routed experts + shared expert + sum, R rows, cycling `layers` resident layers."""
+class DecodeBench:
+    """`per_step` layers a step (1, or 75 for the stack), each router top-8 + routed experts + shared expert + sum on
+    R rows; layer launch j uses resident layer j mod n_layers."""
 
-    def __init__(self, R: int, layers: int, mixed: bool, seed: int, steps_total: int):
+    def __init__(self, R: int, n_layers: int, per_step: int, mixed: bool, seed: int, steps_total: int, path: str):
         import numpy as np
         import torch
         from ea_exl3 import device, experts, linear, moe, ops, synth
+        from ea_exl3._lib import Linear as _Linear, lib
         from ea_exl3.resident import DeviceRouted, DeviceShared
 
         self.torch, self.np = torch, np
         self.device, self.experts, self.linear, self.moe, self.ops = device, experts, linear, moe, ops
-        self.R = R
+        self.R, self.per_step, self.path = R, per_step, path
         k2 = synth.mixed_widths(seed, E) if mixed else 8
-        self.layers = [DeviceRouted(seed + 17 * l, E, D, I, k2=k2, cb=1) for l in range(layers)]
-        self.shared = [DeviceShared(seed + 1000 + l, D, I, 8, 1) for l in range(layers)]
+        self.layers = [DeviceRouted(seed + 17 * l, E, D, I, k2=k2, cb=1) for l in range(n_layers)]
+        self.shared = [DeviceShared(seed + 1000 + l, D, I, 8, 1) for l in range(n_layers)]
         gen = torch.Generator(device="cuda")
         gen.manual_seed(seed + 7)
         self.x = torch.randn((R, D), device="cuda", generator=gen).to(torch.float16)
-        self.logits = torch.randn((steps_total, R, E), device="cuda", generator=gen)
+        launches = steps_total * per_step
+        self.logits = torch.randn((launches, R, E), device="cuda", generator=gen)
         self.bias = 0.1 * torch.randn(E, device="cuda", generator=gen)
-        self.pick = torch.zeros((R, SLOTS), dtype=torch.int32, device="cuda")
-        self.wts = torch.zeros((R, SLOTS), dtype=torch.float32, device="cuda")
+        self.pick = torch.zeros((launches, R, SLOTS), dtype=torch.int32, device="cuda")
+        self.wts = torch.zeros((launches, R, SLOTS), dtype=torch.float32, device="cuda")
         self.out = torch.zeros((R, D), dtype=torch.float32, device="cuda")
         self.sy = torch.zeros((R, D), dtype=torch.float32, device="cuda")
         self.g = torch.zeros((R, I), dtype=torch.bfloat16, device="cuda")
@@ -89,37 +102,63 @@ class DecodeLayerBench:
         self.lscratch = linear.Scratch(R, D, sk_max * R * D)
         self.k = experts.Kernels.load()
         self.s = device.stream()
+        # the one-launch path's arguments, built once: a layer costs the host one foreign call
+        self.fn = lib().ea_ffn_moe_decode
+        self._sh_arrays = [(C.POINTER(_Linear) * 3)(C.pointer(sh.gate.c), C.pointer(sh.up.c), C.pointer(sh.down.c))
+                           for sh in self.shared]
+        self._sh_ptr = [C.addressof(a) for a in self._sh_arrays]
+        self._ex_ref = [C.byref(e.c) for e in self.ex]
+        self._sc_ref = C.byref(self.scratch.c)
+        self._logits0, self._pick0, self._wts0 = self.logits.data_ptr(), self.pick.data_ptr(), self.wts.data_ptr()
+        self._x, self._bias, self._out = self.x.data_ptr(), self.bias.data_ptr(), self.out.data_ptr()
+
+    def layer_of(self, j: int) -> int:
+        return j % len(self.layers)
+
+    def launch(self, j: int) -> None:
+        """Layer launch j."""
+        if self.path != "fused":
+            self.sequence(j)
+            return
+        l, R = self.layer_of(j), self.R
+        r = self.fn(self.s, self._x, 0, D, self._logits0 + j * R * E * 4, self._bias, ROUTED_SCALE,
+                    self._pick0 + j * R * SLOTS * 4, self._wts0 + j * R * SLOTS * 4, self._ex_ref[l],
+                    self._sh_ptr[l], self._sc_ref, self._out, R)
+        if r:
+            from ea_exl3._lib import check
+
+            check(r, "ffn_decode")
 
     def step(self, i: int) -> None:
-        l = i % len(self.layers)
-        s, R = self.s, self.R
-        self.ops.topk(s, self.logits[i].data_ptr(), self.bias.data_ptr(), self.pick.data_ptr(), self.wts.data_ptr(), R)
-        self.moe.routed(s, self.x.data_ptr(), D, self.pick.data_ptr(), self.wts.data_ptr(), self.ex[l], self.scratch,
-                        self.out.data_ptr(), R, x_dtype=0)
-        self.shared_expert(l)
-        self.ops.add_f32(s, self.out.data_ptr(), self.sy.data_ptr(), R * D)
+        for q in range(self.per_step):
+            self.launch(i * self.per_step + q)
 
-    def shared_expert(self, l: int) -> None:
-        # forward.zig:2328-2341 mlp: gate and up (bf16 out), SwiGLU, down (fp32 out)
-        sh, s, R = self.shared[l], self.s, self.R
-        self.linear.call(s, self.lscratch, [sh.gate, sh.up], self.x.data_ptr(), 0, R,
-                         [self.g.data_ptr(), self.u.data_ptr()], [1, 1])
-        self.ops.swiglu2(s, self.g.data_ptr(), self.u.data_ptr(), self.act.data_ptr(), R, I)
-        self.linear.call(s, self.lscratch, [sh.down], self.act.data_ptr(), 1, R, [self.sy.data_ptr()], [2])
-
-    # the routed sequence of moe.routed issued launch by launch, with events around the grouped launches
-    def step_instrumented(self, i: int, ev: list) -> None:
+    def step_events(self, i: int, ev: list) -> None:
         torch = self.torch
-        l = i % len(self.layers)
+        for q in range(self.per_step):
+            j = i * self.per_step + q
+            if self.path == "fused":
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record()
+                self.launch(j)
+                e1.record()
+                ev.append((j, e0, e1, "layer"))
+            else:
+                self.sequence(j, ev)
+
+    # the reference's launch sequence: ops.topk, moe.routed's six launches, forward.mlp, glue.addF32
+    def sequence(self, j: int, ev: list | None = None) -> None:
+        torch = self.torch
+        l = self.layer_of(j)
         s, R = self.s, self.R
         sc, ex = self.scratch.c, self.ex[l].c
+        pick, wts = self.pick[j].data_ptr(), self.wts[j].data_ptr()
         P = R * SLOTS
         maxu = min(P, E)
-        self.ops.topk(s, self.logits[i].data_ptr(), self.bias.data_ptr(), self.pick.data_ptr(), self.wts.data_ptr(), R)
+        self.ops.topk(s, self.logits[j].data_ptr(), self._bias, pick, wts, R)
         k = self.k
-        k.group(s, self.pick.data_ptr(), sc.ids, sc.count, sc.members, R, SLOTS, E, R)
-        k.rot_in(s, self.x.data_ptr(), D, self.pick.data_ptr(), ex.suh_g, ex.suh_u, sc.xg, sc.xu, R, D, SLOTS, E,
-                 x_dtype=0)
+        k.group(s, pick, sc.ids, sc.count, sc.members, R, SLOTS, E, R)
+        k.rot_in(s, self._x, D, pick, ex.suh_g, ex.suh_u, sc.xg, sc.xu, R, D, SLOTS, E, x_dtype=0)
         a = self.experts.grouped_args(x0=sc.xg, x1=sc.xu, tp0=ex.ptr[0], tp1=ex.ptr[1], k2_0=ex.k2[0], k2_1=ex.k2[1],
                                       uids=sc.ids, ucount=sc.count, members=sc.members, z=sc.z, K=D, N=I, P=P, SK=4,
                                       maxm=R, slots=SLOTS, nexp_max=maxu, mats=2, cb=1, nt=8, warps=4, pf=1,
@@ -128,9 +167,7 @@ class DecodeLayerBench:
         e0.record()
         k.grouped(s, a)
         e1.record()
-        ev.append(("gateup", e0, e1))
-        k.gateup_epilogue(s, sc.z, self.pick.data_ptr(), ex.svh_g, ex.svh_u, ex.suh_d, sc.xd, R, P, I, 4, SLOTS, E,
-                          float("inf"), 1)
+        k.gateup_epilogue(s, sc.z, pick, ex.svh_g, ex.svh_u, ex.suh_d, sc.xd, R, P, I, 4, SLOTS, E, float("inf"), 1)
         d = self.experts.grouped_args(x0=sc.xd, x1=sc.xd, tp0=ex.ptr[2], tp1=ex.ptr[2], k2_0=ex.k2[2], k2_1=ex.k2[2],
                                       uids=sc.ids, ucount=sc.count, members=sc.members, z=sc.z, K=I, N=D, P=P, SK=1,
                                       maxm=R, slots=SLOTS, nexp_max=maxu, mats=1, cb=1, nt=8, warps=4, pf=1,
@@ -139,44 +176,46 @@ class DecodeLayerBench:
         e2.record()
         k.grouped(s, d)
         e3.record()
-        ev.append(("down", e2, e3))
-        k.down_combine(s, sc.z, self.pick.data_ptr(), ex.svh_d, sc.y, self.wts.data_ptr(), self.out.data_ptr(), R, P, D,
-                       1, SLOTS, E)
-        self.shared_expert(l)
-        self.ops.add_f32(s, self.out.data_ptr(), self.sy.data_ptr(), R * D)
+        if ev is not None:
+            ev.append((j, e0, e1, "gateup"))
+            ev.append((j, e2, e3, "down"))
+        k.down_combine(s, sc.z, pick, ex.svh_d, sc.y, wts, self._out, R, P, D, 1, SLOTS, E)
+        sh = self.shared[l]
+        self.linear.call(s, self.lscratch, [sh.gate, sh.up], self._x, 0, R, [self.g.data_ptr(), self.u.data_ptr()],
+                         [1, 1])
+        self.ops.swiglu2(s, self.g.data_ptr(), self.u.data_ptr(), self.act.data_ptr(), R, I)
+        self.linear.call(s, self.lscratch, [sh.down], self.act.data_ptr(), 1, R, [self.sy.data_ptr()], [2])
+        self.ops.add_f32(s, self._out, self.sy.data_ptr(), R * D)
 
-    def layer_bytes(self, i: int) -> tuple[int, int]:
-        """Algorithmic bytes and flops of step i: the trellis + scales of every distinct expert it touches, the
-        shared expert, the activations in and out and the logits."""
-        pick = self.np.asarray(self.pick.cpu())
-        return self._bytes_of(i, pick)
-
-    def _bytes_of(self, i, pick):
-        l = i % len(self.layers)
-        distinct = sorted(set(int(e) for e in pick.reshape(-1)))
+    def launch_bytes(self, j: int, picks) -> tuple[int, int]:
+        """Algorithmic bytes and flops of layer launch j: the trellis + scales of every distinct expert it touches,
+        the shared expert, the activations in, the logits and bias, pick / wts and the fp32 output."""
+        l = self.layer_of(j)
+        distinct = sorted(set(int(e) for e in picks[j].reshape(-1)))
         b = sum(self.layers[l].expert_bytes(e) for e in distinct) + self.shared[l].bytes()
-        b += self.R * D * 2 + self.R * E * 4 + self.R * D * 4
+        b += self.R * D * 2 + self.R * E * 4 + E * 4 + self.R * D * 4 + 2 * self.R * SLOTS * 4
         f = 2 * (self.R * SLOTS + self.R) * 3 * D * I
-        return b, f, distinct
+        return b, f
 
-    def grouped_bytes(self, distinct: list, l: int) -> tuple[int, int]:
-        """Algorithmic bytes of the gate|up and the down grouped launches: the touched experts' trellis, the
-        rotated inputs read and the partial sums written."""
-        lay = self.layers[l]
+    def grouped_bytes(self, j: int, picks, which: str) -> int:
+        """The sequence path's grouped launches: touched experts' trellis, rotated inputs read, partial sums written."""
+        lay = self.layers[self.layer_of(j)]
+        distinct = sorted(set(int(e) for e in picks[j].reshape(-1)))
         P = self.R * SLOTS
-        gu = sum(int(lay.bytes[0][e] + lay.bytes[1][e]) for e in distinct) + 2 * P * D * 2 + 2 * 4 * P * I * 4
-        dn = sum(int(lay.bytes[2][e]) for e in distinct) + P * I * 2 + P * D * 4
-        return gu, dn
+        if which == "gateup":
+            return sum(int(lay.bytes[0][e] + lay.bytes[1][e]) for e in distinct) + 2 * P * D * 2 + 2 * 4 * P * I * 4
+        return sum(int(lay.bytes[2][e]) for e in distinct) + P * I * 2 + P * D * 4
 
 
-def time_steps(fn, steps: int, warmup: int, torch) -> float:
+def time_steps(fn, steps: int, warmup: int, torch, first: int = 0) -> float:
+    """Milliseconds a step over `steps` steps after `warmup` untimed ones, between two synchronised events."""
     for i in range(warmup):
-        fn(i)
+        fn(first + i)
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()
     for i in range(steps):
-        fn(warmup + i)
+        fn(first + warmup + i)
     e1.record()
     torch.cuda.synchronize()
     return e0.elapsed_time(e1) / steps
@@ -195,9 +234,10 @@ def copy_calibration(torch) -> None:
 
 # ---- the CPU baseline -------------------------------------------------------------------------------------------------
 
-def cpu_baseline_decode(seed: int, budget_s: float = 12.0) -> dict:
-    """The C oracle (OpenMP) on the host cores, on config 2's work: the layer at batch 1 with 8 routed experts and
-    the shared expert, fresh routing per layer. A bounded sample: layers until `budget_s` seconds have passed."""
+def cpu_baseline_decode(seed: int, R: int = 1, mixed: bool = False, budget_s: float = 12.0, layers_per_unit: int = 1,
+                        unit: str = "us/layer") -> dict:
+    """The C oracle (OpenMP) on the host cores on the decode layer's work: R rows, 8 routed experts a row (fresh
+    routing per layer) and the shared expert. A bounded sample: whole layers until `budget_s` seconds have passed."""
     import numpy as np
 
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
@@ -205,32 +245,34 @@ def cpu_baseline_decode(seed: int, budget_s: float = 12.0) -> dict:
     from ea_exl3 import synth
 
     rng = np.random.default_rng(seed)
-    x = synth.activations(seed, 1, D, "f16")
-    sh = [synth.trellis(seed, 99, m, 0, k, n, 8) for m, (k, n) in enumerate(((D, I), (D, I), (I, D)))]
-    sh_s = [orc.expert_to_strips(sh[m], k, n, 8) for m, (k, n) in enumerate(((D, I), (D, I), (I, D)))]
+    x = synth.activations(seed, R, D, "f16")
+    shapes = ((D, I), (D, I), (I, D))
+    sh = [synth.trellis(seed, 99, m, 0, k, n, 8) for m, (k, n) in enumerate(shapes)]
+    sh_s = [orc.expert_to_strips(sh[m], k, n, 8) for m, (k, n) in enumerate(shapes)]
     suh = [synth.scales(seed + m, k, 1.0) for m, k in enumerate((D, D, I))]
     svh = [synth.scales(seed + 10 + m, n, 0.02) for m, n in enumerate((I, I, D))]
     tw = 32
+    k2 = synth.mixed_widths(seed, E) if mixed else 8
 
     def run(pick, wts, host):
         r = _oracle_routed(orc, host)
-        out = orc.moe_routed(x, pick, wts, r, 1, SLOTS)
-        xh = [orc.exl3_rot_in(x, suh[m], 1, D) for m in (0, 1)]
+        out = orc.moe_routed(x, pick, wts, r, R, SLOTS)
+        xh = [orc.exl3_rot_in(x, suh[m], R, D) for m in (0, 1)]
         sk, wk = orc.linear_plan(D, I)
-        g = orc.exl3_linear(xh[0], sh_s[0], 8 * tw, (D // 16) * 8 * tw, svh[0], 1, D, I, 8, 1, sk, wk, y_dtype=1)
-        u = orc.exl3_linear(xh[1], sh_s[1], 8 * tw, (D // 16) * 8 * tw, svh[1], 1, D, I, 8, 1, sk, wk, y_dtype=1)
+        g = orc.exl3_linear(xh[0], sh_s[0], 8 * tw, (D // 16) * 8 * tw, svh[0], R, D, I, 8, 1, sk, wk, y_dtype=1)
+        u = orc.exl3_linear(xh[1], sh_s[1], 8 * tw, (D // 16) * 8 * tw, svh[1], R, D, I, 8, 1, sk, wk, y_dtype=1)
         act = orc.swiglu2(g, u)
-        xd = orc.exl3_rot_in(act, suh[2], 1, I, bf16=True)
+        xd = orc.exl3_rot_in(act, suh[2], R, I, bf16=True)
         sk, wk = orc.linear_plan(I, D)
-        sy = orc.exl3_linear(xd, sh_s[2], 8 * tw, (I // 16) * 8 * tw, svh[2], 1, I, D, 8, 1, sk, wk)
+        sy = orc.exl3_linear(xd, sh_s[2], 8 * tw, (I // 16) * 8 * tw, svh[2], R, I, D, 8, 1, sk, wk)
         return out + sy
 
-    # warm the codebook table and the page cache, then time whole layers (host data built outside the clock)
+    # host data built outside the clock; one warm-up layer, then whole layers
     cases = []
     for i in range(3):
-        pick = np.sort(rng.choice(E, SLOTS, replace=False)).astype(np.int32).reshape(1, SLOTS)
-        cases.append((pick, synth.routing_weights(seed + i, 1, SLOTS),
-                      synth.HostLayer(seed + i, experts=E, dims=D, width=I, k2=8, only=pick.reshape(-1))))
+        pick = np.stack([np.sort(rng.choice(E, SLOTS, replace=False)) for _ in range(R)]).astype(np.int32)
+        cases.append((pick, synth.routing_weights(seed + i, R, SLOTS),
+                      synth.HostLayer(seed + i, experts=E, dims=D, width=I, k2=k2, only=np.unique(pick))))
     run(*cases[0])
     n, t_total = 0, 0.0
     while t_total < budget_s and n < 40:
@@ -240,9 +282,14 @@ def cpu_baseline_decode(seed: int, budget_s: float = 12.0) -> dict:
         t_total += time.perf_counter() - t0
         n += 1
     threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
-    return {"value": round(t_total / n * 1e6, 1), "unit": "us/layer", "cores": threads, "kind": "port",
-            "sample": f"{n} config-2 layers (batch 1: 8 routed 4-bit experts + 4-bit shared expert, D 6144, I 256) "
-                      f"through the C oracle with OpenMP, {threads} threads"}
+    per_layer = t_total / n * 1e6
+    bits = "3/4-bit mixed" if mixed else "4-bit"
+    sample = (f"{n} layers of {R} row(s) (8 routed {bits} experts a row + a 4-bit shared expert, D 6144, I 256) "
+              f"through the C oracle with OpenMP, {threads} threads")
+    if layers_per_unit > 1:
+        sample += f"; the per-layer time x {layers_per_unit} layers"
+    return {"value": round(per_layer * layers_per_unit, 1), "unit": unit, "cores": threads, "kind": "port",
+            "sample": sample}
 
 
 def _oracle_routed(orc, host):
@@ -257,7 +304,155 @@ def _oracle_routed(orc, host):
                       host.dims, host.width, host.cb)
 
 
-# ---- main ---------------------------------------------------------------------------------------------------------
+# ---- the workloads' lines ------------------------------------------------------------------------------------------
+
+DATA = ("synthetic: seeded random EXL3 trellis words generated on the GPU (any bit stream is a valid tile), "
+        "random-sign fp16 scales sized for N(0, 0.02) weights, N(0,1) fp16 activations, N(0,1) router logits "
+        "fresh every layer")
+
+WORKLOADS = {  # name -> (workload, rows, mixed widths, layers a step, unit)
+    "decode": ("config 2: one GLM-5.3 MoE layer at batch-1 decode, one TP=8 rank's shard (D 6144, 256 routed "
+               "experts x I 256 + shared expert, EXL3 4-bit mcg), router top-8 from logits", 1, False, 1, "us/layer"),
+    "multi": ("config 3: the same layer at 16 rows (4 conversations x 4 draft rows), uniform top-8 routing, 70 % of "
+              "the routed experts at 3 bits", 16, True, 1, "us/layer"),
+    "stack": ("config 5: 75 resident MoE layers of one TP=8 rank (3-bit for 70 % of the routed experts, 4-bit "
+              "shared experts), one token through all of them", 1, True, 75, "us/token"),
+}
+
+
+def _line(args, value, unit, ms, config, roofline, cpu) -> dict:
+    return {"metric": baseline_metric(), "value": round(value, 3), "unit": unit, "n_gpus": 1, "steps": args.steps,
+            "warmup": args.warmup, "ms_per_step": round(ms, 6), "higher_is_better": False, "scaling": "weak",
+            "vs_baseline": None, "dtype": "fp16", "data": DATA, "config": config, "roofline": roofline,
+            "cpu_baseline": cpu}
+
+
+def run_decode(args, torch, np) -> dict:
+    workload, R, mixed, per_step, unit = WORKLOADS[args.config]
+    n_layers = 75 if args.config == "stack" else args.layers
+    total = args.warmup + args.steps
+    bench = DecodeBench(R, n_layers, per_step, mixed, args.seed, 2 * total + 2, args.path)
+    # the timed region: K whole steps
+    ms = time_steps(bench.step, args.steps, args.warmup, torch)
+    # the same number of steps again with events around each launch of the dominant kernel
+    ev = []
+    for i in range(args.warmup):
+        bench.step(total + i)
+    torch.cuda.synchronize()
+    for i in range(args.steps):
+        bench.step_events(total + args.warmup + i, ev)
+    torch.cuda.synchronize()
+    picks = bench.pick.cpu().numpy()
+    durs = [a.elapsed_time(b) for _, a, b, _ in ev]
+    if args.path == "fused":
+        nbytes = [bench.launch_bytes(j, picks)[0] for j, _, _, _ in ev]
+        kernel = ("decode_layer_kernel (ea_ffn_moe_decode: top-8, the routed experts' gate|up and down, the shared "
+                  "expert and the combine in one persistent launch)")
+    else:
+        nbytes = [bench.grouped_bytes(j, picks, w) for j, _, _, w in ev]
+        kernel = "grouped_kernel (the routed experts' EXL3 grouped GEMV: gate|up and down launches)"
+    avg_ms = sum(durs) / len(durs)
+    avg_b = sum(nbytes) / len(nbytes)
+    achieved = avg_b / (avg_ms * 1e-3) / 1e9
+    # the step's own roofline, from the timed steps' launches
+    first = args.warmup * per_step
+    lb = [bench.launch_bytes(first + j, picks) for j in range(args.steps * per_step)]
+    step_b = sum(b for b, _ in lb) / args.steps
+    step_f = sum(f for _, f in lb) / args.steps
+    us = ms * 1e3
+    t_roof_us = max(step_b / (HBM_PEAK_GBS * 1e9), step_f / (FP16_PEAK_TFLOPS * 1e12)) * 1e6
+    config = {"workload": workload, "path": args.path, "layers_resident": n_layers, "step_bytes": int(step_b),
+              "step_flops": int(step_f), "step_roofline_us": round(t_roof_us, 3),
+              "step_hbm_frac": round(t_roof_us / us, 4), "step_gbs": round(step_b / (us * 1e-6) / 1e9, 1)}
+    roofline = {"kernel": kernel, "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None, "avg_launch_us": round(avg_ms * 1e3, 3),
+                "bytes_per_launch": int(avg_b), "launches_timed": len(durs)}
+    cpu = None if args.no_cpu_baseline else cpu_baseline_decode(args.seed, R, mixed, layers_per_unit=per_step,
+                                                                unit=unit)
+    return _line(args, us, unit, ms, config, roofline, cpu)
+
+
+def run_linear(args, torch, np) -> dict:
+    """Config 1: linear.call of one 4-bit EXL3 linear 6144 x 2048 at one row (rot_in + one linear launch)."""
+    from ea_exl3 import device, linear
+    from ea_exl3._lib import Linear as _Linear, check, lib
+    from ea_exl3.resident import DeviceLinear
+
+    K, N = 6144, 2048
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(args.seed)
+    lins = [DeviceLinear(gen, K, N, 8, 1) for _ in range(args.layers)]
+    x = torch.randn((1, K), device="cuda", generator=gen).to(torch.float16)
+    y = torch.zeros((1, N), dtype=torch.float32, device="cuda")
+    sc = linear.Scratch(1, K, lins[0].sk * N)
+    s = device.stream()
+    fn = lib().ea_linear_call
+    arrs = [(C.POINTER(_Linear) * 1)(C.pointer(l.c)) for l in lins]
+    outs = (C.c_uint64 * 1)(y.data_ptr())
+    dts = (C.c_int * 1)(2)
+    scr = C.byref(sc.c)
+    xp = x.data_ptr()
+
+    def step(i):
+        r = fn(s, scr, arrs[i % len(arrs)], 1, xp, 0, 1, outs, dts)
+        if r:
+            check(r, "linear.call")
+
+    ms = time_steps(step, args.steps, args.warmup, torch)
+    b = lins[0].bytes() + K * 2 + N * 4
+    f = 2 * K * N
+    us = ms * 1e3
+    t_roof = max(b / (HBM_PEAK_GBS * 1e9), f / (FP16_PEAK_TFLOPS * 1e12)) * 1e6
+    gbs = b / (us * 1e-6) / 1e9
+    config = {"workload": "config 1: one EXL3 4-bit linear K 6144 x N 2048 at one fp16 row, fp32 out (linear.call: "
+                          "rot_in + linear launch)", "linears_resident": args.layers, "step_bytes": b,
+              "step_roofline_us": round(t_roof, 3), "step_hbm_frac": round(t_roof / us, 4)}
+    roofline = {"kernel": "linear.call (whole call: rot_in + linear_kernel)", "bound": "hbm", "achieved": round(gbs, 1),
+                "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None}
+    return _line(args, us, "us/linear", ms, config, roofline, None)
+
+
+def run_prefill(args, torch, np, R: int) -> dict:
+    """Config 4: prompt_experts.run over R rows, Zipf(1.1) routing, 4-bit experts."""
+    from ea_exl3 import device, prompt_experts, synth
+    from ea_exl3.resident import DeviceRouted
+
+    lay = DeviceRouted(args.seed, E, D, I, k2=8, cb=1)
+
+    class _Ex:
+        def __init__(s, dr):
+            s.c = dr.c
+
+    ex = _Ex(lay)
+    pick = synth.picks_zipf(args.seed + 1, R, 1.1, E, SLOTS)
+    wts = synth.routing_weights(args.seed + 2, R, SLOTS)
+    dp, dw = device.upload(pick), device.upload(wts)
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(args.seed + 3)
+    x = torch.randn((R, D), device="cuda", generator=gen).to(torch.float16)
+    out = torch.zeros((R, D), dtype=torch.float32, device="cuda")
+    sc = prompt_experts.Scratch(ex, R, SLOTS)
+    s = device.stream()
+
+    def step(i):
+        prompt_experts.run(s, x.data_ptr(), D, dp.data_ptr(), dw.data_ptr(), ex, sc, out.data_ptr(), R,
+                           do_round=False, x_dtype=0)
+
+    ms = time_steps(step, args.steps, args.warmup, torch)
+    distinct = sorted(set(int(e) for e in pick.reshape(-1)))
+    b = sum(lay.expert_bytes(e) for e in distinct) + R * D * 2 + R * D * 4 + R * SLOTS * 8
+    f = 2 * R * SLOTS * 3 * D * I
+    us = ms * 1e3
+    t_roof = max(b / (HBM_PEAK_GBS * 1e9), f / (FP16_PEAK_TFLOPS * 1e12)) * 1e6
+    tfs = f / (us * 1e-6) / 1e12
+    config = {"workload": f"config 4: prefill chunk of {R} tokens x 6144 through prompt_experts.run, Zipf(1.1) top-8 "
+                          "routing over 256 4-bit experts", "distinct_experts": len(distinct), "step_bytes": b,
+              "step_flops": f, "step_roofline_us": round(t_roof, 3), "step_roof_frac": round(t_roof / us, 4),
+              "step_gbs": round(b / (us * 1e-6) / 1e9, 1)}
+    roofline = {"kernel": "prompt_experts.run (whole call)", "bound": "mfma", "achieved": round(tfs, 2),
+                "peak": FP16_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(tfs / FP16_PEAK_TFLOPS, 4), "traffic": None}
+    return _line(args, us, "us/layer", ms, config, roofline, None)
+
 
 def main() -> int:
     args = parse()
@@ -273,80 +468,12 @@ def main() -> int:
     device.init(0)
     if args.copy_calibration:
         copy_calibration(torch)
-
-    if args.config not in ("decode",):
-        print(f"config {args.config} is not wired into bench.py yet", file=sys.stderr)
-        return 2
-
-    total = args.warmup + args.steps
-    bench = DecodeLayerBench(1, args.layers, False, args.seed, 2 * total + 8)
-    # the timed region: K whole layers
-    ms = time_steps(bench.step, args.steps, args.warmup, torch)
-
-    # the dominant kernel, live: events around the grouped launches of the same steps issued launch by launch
-    ev = []
-    picks = []
-    for i in range(args.warmup):
-        bench.step_instrumented(total + i, [])
-    torch.cuda.synchronize()
-    for i in range(args.steps):
-        bench.step_instrumented(total + args.warmup + i, ev)
-        if i < 16:
-            picks.append(np.asarray(bench.pick.cpu()))
-    torch.cuda.synchronize()
-    gu_ms = [a.elapsed_time(b) for n, a, b in ev if n == "gateup"]
-    dn_ms = [a.elapsed_time(b) for n, a, b in ev if n == "down"]
-    distinct = sorted(set(int(e) for e in picks[0].reshape(-1)))
-    gu_b, dn_b = bench.grouped_bytes(distinct, 0)
-    avg_launch_ms = (sum(gu_ms) + sum(dn_ms)) / (len(gu_ms) + len(dn_ms))
-    avg_launch_b = (gu_b + dn_b) / 2
-    achieved = avg_launch_b / (avg_launch_ms * 1e-3) / 1e9
-
-    layer_b, layer_f, _ = bench._bytes_of(0, picks[0])
-    us = ms * 1e3
-    t_roof_us = max(layer_b / (HBM_PEAK_GBS * 1e9), layer_f / (FP16_PEAK_TFLOPS * 1e12)) * 1e6
-    result = {
-        "metric": baseline_metric(),
-        "value": round(us, 3),
-        "unit": "us/layer",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(ms, 6),
-        "higher_is_better": False,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "fp16",
-        "data": "synthetic: seeded random EXL3 trellis words (any bit stream is a valid tile), random-sign fp16 "
-                "scales sized for N(0, 0.02) weights, N(0,1) fp16 activations and router logits (fresh each step)",
-        "config": {
-            "workload": "config 2: one GLM-5.3 MoE layer at batch-1 decode, one TP=8 rank's shard (D 6144, 256 "
-                        "routed experts x I 256 + shared expert, EXL3 4-bit mcg), router top-8 from logits",
-            "layers_cycled": args.layers,
-            "layer_bytes": layer_b,
-            "layer_flops": layer_f,
-            "layer_roofline_us": round(t_roof_us, 3),
-            "layer_hbm_frac": round(t_roof_us / us, 4),
-            "layer_gbs": round(layer_b / (us * 1e-6) / 1e9, 1),
-        },
-        "roofline": {
-            "kernel": "grouped_kernel (the routed experts' EXL3 grouped GEMV: gate|up and down launches)",
-            "bound": "hbm",
-            "achieved": round(achieved, 1),
-            "peak": HBM_PEAK_GBS,
-            "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
-            "avg_launch_us": round(avg_launch_ms * 1e3, 3),
-            "bytes_per_launch": int(avg_launch_b),
-            "gateup_us": round(sum(gu_ms) / len(gu_ms) * 1e3, 3),
-            "down_us": round(sum(dn_ms) / len(dn_ms) * 1e3, 3),
-        },
-    }
-    if not args.no_cpu_baseline:
-        result["cpu_baseline"] = cpu_baseline_decode(args.seed)
+    if args.config in WORKLOADS:
+        result = run_decode(args, torch, np)
+    elif args.config == "linear":
+        result = run_linear(args, torch, np)
     else:
-        result["cpu_baseline"] = None
+        result = run_prefill(args, torch, np, 512 if args.config == "prefill512" else 2048)
     print(json.dumps(result))
     return 0
 

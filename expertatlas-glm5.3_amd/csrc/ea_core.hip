@@ -31,7 +31,7 @@ template <int CB, int K2>
 __device__ __forceinline__ void unpack_tile(const uint32_t* __restrict__ tile, uint16_t* __restrict__ W, int N, int kt,
                                             int nt, int lane) {
     const TileLane<K2, CB> tl(lane);
-    const u2v v = tl.decode(tile);
+    const u2v v = tl.decode_at(tile);
     const int n = nt * 16 + (lane & 15), g = (lane >> 4) & 3;
     uint16_t* w = W + (size_t)(kt * 16 + 2 * g) * N + n;
     w[0] = (uint16_t)(v.x & 0xffffu);

@@ -37,13 +37,20 @@ struct TileLane {
         w[1] = gload(tile + w1);
         if constexpr (NW == 3) w[2] = gload(tile + w2);
     }
+    // The same through a buffer resource: the tile starts `soff` bytes into it (a scalar offset), so the addressing
+    // costs no vector registers beyond the lane's word offsets.
+    __device__ __forceinline__ void fetch(__amdgpu_buffer_rsrc_t r, int soff, uint32_t (&w)[NW]) const {
+        w[0] = __builtin_amdgcn_raw_buffer_load_b32(r, 4 * w0, soff, 0);
+        w[1] = __builtin_amdgcn_raw_buffer_load_b32(r, 4 * w1, soff, 0);
+        if constexpr (NW == 3) w[2] = __builtin_amdgcn_raw_buffer_load_b32(r, 4 * w2, soff, 0);
+    }
     // The four values as two packed words (values 0, 1 in .x; 2, 3 in .y).
     __device__ __forceinline__ u2v decode(const uint32_t (&w)[NW]) const {
         if constexpr (K2 <= 10) return decode_quad<K2, CB>(w[0], w[1], sh);
         else return decode_quad3<K2, CB>(w[0], w[1], w[2], sh);
     }
     // This lane's four B values of the tile starting at `tile`.
-    __device__ __forceinline__ u2v decode(const uint32_t* __restrict__ tile) const {
+    __device__ __forceinline__ u2v decode_at(const uint32_t* __restrict__ tile) const {
         uint32_t w[NW];
         fetch(tile, w);
         return decode(w);
@@ -130,7 +137,7 @@ __device__ __forceinline__ void wave_tiles(const uint32_t* __restrict__ base, si
         const uint32_t* t0 = base + (size_t)t * kstride;
 #pragma unroll
         for (int j = 0; j < NTW; ++j) {
-            const h4v b = __builtin_bit_cast(h4v, tl.decode(t0 + j * TW));
+            const h4v b = __builtin_bit_cast(h4v, tl.decode_at(t0 + j * TW));
 #pragma unroll
             for (int m = 0; m < MG; ++m) acc[m][j] = __builtin_amdgcn_mfma_f32_16x16x16f16(a[m], b, acc[m][j], 0, 0, 0);
         }
@@ -138,6 +145,12 @@ __device__ __forceinline__ void wave_tiles(const uint32_t* __restrict__ base, si
 }
 
 __device__ __forceinline__ void record_error(int* status, int code) { atomicCAS(status, 0, code); }
+
+// A raw buffer resource over `bytes` bytes at `base` (gfx9 word 3: 32-bit data, no format conversion). `base` must
+// be wave-uniform.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
 
 // Dispatch a runtime K2 to wave_tiles<..., K2, ...> for K2 in [LO, HI]; false when outside.
 #define EA_K2_SWITCH(k2, LO, HI, CALL)                                        \
