@@ -5,8 +5,8 @@
 
 A step is one pass of the hot path over one batch of synthetic input, with every input already in HBM:
   decode (default): one GLM-5.3 MoE layer of a TP=8 rank at batch 1 -- router top-8 from logits,
-      the routed experts (moe.routed), the shared expert (EXL3 linears + SwiGLU) and their sum, as the one launch of
-      ea_ffn_moe_decode;
+      the routed experts (moe.routed), the shared expert (EXL3 linears + SwiGLU) and their sum: ea_ffn_moe_decode,
+      four launches (gate|up, epilogue, down, combine);
   multi (config 3): the same layer at 16 rows, uniform top-8, 70 % of the experts at 3 bits;
   stack (config 5): 75 resident layers (3-bit for 70 % of the experts), one token through all of them (us / token);
   linear (config 1): one 4-bit EXL3 linear 6144 x 2048 at one row (linear.call);
@@ -50,7 +50,7 @@ def parse():
                     choices=["decode", "multi", "stack", "linear", "prefill512", "prefill2048"])
     ap.add_argument("--layers", type=int, default=8, help="distinct resident layers the decode configs cycle through")
     ap.add_argument("--path", default="fused", choices=["fused", "sequence"],
-                    help="decode configs: the one-launch layer, or the reference's launch sequence (topk, "
+                    help="decode configs: ea_ffn_moe_decode, or the reference's launch sequence (topk, "
                          "moe.routed's six launches, the shared expert's linears, swiglu2, add)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -102,7 +102,7 @@ class DecodeBench:
         self.lscratch = linear.Scratch(R, D, sk_max * R * D)
         self.k = experts.Kernels.load()
         self.s = device.stream()
-        # the one-launch path's arguments, built once: a layer costs the host one foreign call
+        # ea_ffn_moe_decode's arguments, built once: a layer costs the host one foreign call
         self.fn = lib().ea_ffn_moe_decode
         self._sh_arrays = [(C.POINTER(_Linear) * 3)(C.pointer(sh.gate.c), C.pointer(sh.up.c), C.pointer(sh.down.c))
                            for sh in self.shared]
@@ -134,15 +134,17 @@ class DecodeBench:
             self.launch(i * self.per_step + q)
 
     def step_events(self, i: int, ev: list) -> None:
-        torch = self.torch
+        """Step i again, timing its launches: the fused path's four launches from the library's stage events
+        (recorded on the launch stream), the sequence path's grouped launches from torch events on the same stream."""
         for q in range(self.per_step):
             j = i * self.per_step + q
             if self.path == "fused":
-                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-                e0.record()
                 self.launch(j)
-                e1.record()
-                ev.append((j, e0, e1, "layer"))
+                ms = (C.c_float * 4)()
+                from ea_exl3._lib import check, lib
+
+                check(lib().ea_profile_stages(ms, 4), "profile_stages")
+                ev.append((j, list(ms)))
             else:
                 self.sequence(j, ev)
 
@@ -196,6 +198,16 @@ class DecodeBench:
         b += self.R * D * 2 + self.R * E * 4 + E * 4 + self.R * D * 4 + 2 * self.R * SLOTS * 4
         f = 2 * (self.R * SLOTS + self.R) * 3 * D * I
         return b, f
+
+    def gateup_bytes(self, j: int, picks) -> int:
+        """Algorithmic bytes of the gate|up launch of layer launch j: gate and up trellis and suh of every distinct
+        expert it touches, the shared expert's gate and up (words, suh), the activations, logits and bias."""
+        l = self.layer_of(j)
+        lay, sh = self.layers[l], self.shared[l]
+        distinct = sorted(set(int(e) for e in picks[j].reshape(-1)))
+        b = sum(int(lay.bytes[0][e] + lay.bytes[1][e]) + 2 * 2 * D for e in distinct)
+        b += sh.gate.words.numel() * 4 + sh.up.words.numel() * 4 + 2 * 2 * D
+        return b + self.R * D * 2 + self.R * E * 4 + E * 4
 
     def grouped_bytes(self, j: int, picks, which: str) -> int:
         """The sequence path's grouped launches: touched experts' trellis, rotated inputs read, partial sums written."""
@@ -334,21 +346,31 @@ def run_decode(args, torch, np) -> dict:
     bench = DecodeBench(R, n_layers, per_step, mixed, args.seed, 2 * total + 2, args.path)
     # the timed region: K whole steps
     ms = time_steps(bench.step, args.steps, args.warmup, torch)
-    # the same number of steps again with events around each launch of the dominant kernel
+    # the same number of steps again, timing each launch of the dominant kernel on the stream it runs on
     ev = []
     for i in range(args.warmup):
         bench.step(total + i)
     torch.cuda.synchronize()
+    from ea_exl3._lib import check, lib
+
+    if args.path == "fused":
+        check(lib().ea_profile_enable(1), "profile_enable")
     for i in range(args.steps):
         bench.step_events(total + args.warmup + i, ev)
     torch.cuda.synchronize()
-    picks = bench.pick.cpu().numpy()
-    durs = [a.elapsed_time(b) for _, a, b, _ in ev]
     if args.path == "fused":
-        nbytes = [bench.launch_bytes(j, picks)[0] for j, _, _, _ in ev]
-        kernel = ("decode_layer_kernel (ea_ffn_moe_decode: top-8, the routed experts' gate|up and down, the shared "
-                  "expert and the combine in one persistent launch)")
+        check(lib().ea_profile_enable(0), "profile_enable")
+    picks = bench.pick.cpu().numpy()
+    stages = None
+    if args.path == "fused":
+        durs = [ms[0] for _, ms in ev]
+        nbytes = [bench.gateup_bytes(j, picks) for j, _ in ev]
+        kernel = ("gateup_kernel (ea_ffn_moe_decode's first launch: per-block top-8 and grouping, then the gate and "
+                  "up EXL3 GEMV of every touched routed expert and of the shared expert)")
+        stages = {name: round(sum(ms[k] for _, ms in ev) / len(ev) * 1e3, 3)
+                  for k, name in enumerate(("gateup_us", "epilogue_us", "down_us", "combine_us"))}
     else:
+        durs = [a.elapsed_time(b) for _, a, b, _ in ev]
         nbytes = [bench.grouped_bytes(j, picks, w) for j, _, _, w in ev]
         kernel = "grouped_kernel (the routed experts' EXL3 grouped GEMV: gate|up and down launches)"
     avg_ms = sum(durs) / len(durs)
@@ -367,6 +389,8 @@ def run_decode(args, torch, np) -> dict:
     roofline = {"kernel": kernel, "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None, "avg_launch_us": round(avg_ms * 1e3, 3),
                 "bytes_per_launch": int(avg_b), "launches_timed": len(durs)}
+    if stages:
+        roofline["layer_stages"] = stages
     cpu = None if args.no_cpu_baseline else cpu_baseline_decode(args.seed, R, mixed, layers_per_unit=per_step,
                                                                 unit=unit)
     return _line(args, us, unit, ms, config, roofline, cpu)

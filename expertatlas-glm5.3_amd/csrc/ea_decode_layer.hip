@@ -35,7 +35,7 @@ constexpr int DL_MAXI = 256;                 // widest rank-local intermediate (
 constexpr int DL_RS = 264;                   // LDS row stride of the staged activations, halves
 constexpr int DL_MAXKC = 24;                 // k chunks of 256 (D up to 6144)
 
-// Scratch of the two launches, carved on the host for the scratch's row capacity (any R up to it runs).
+// Scratch of the four launches, carved on the host for the scratch's row capacity (any R up to it runs).
 struct DLLayout {
     float* zp;          // [Q, NH, 2, KC, 128] gate|up partial sums, Q = pairs + rows (the shared expert's rows last)
     uint16_t* xd;       // [Q, I] down inputs
@@ -676,8 +676,26 @@ static DLLayout dl_layout(uint64_t base, uint32_t rows, uint32_t D, uint32_t I, 
     return l;
 }
 
+// Stage events for benchmarks (ea_profile_enable): recorded on the call's stream around the four launches.
+constexpr int DL_STAGES = 4;
+struct DLProfile {
+    bool on = false, recorded = false;
+    hipEvent_t ev[DL_STAGES + 1] = {};
+};
+static DLProfile g_prof[64];
+
+static DLProfile* profile_of(int device) { return device >= 0 && device < 64 ? &g_prof[device] : nullptr; }
+
+static void mark_stage(hipStream_t s, int device, int k) {
+    DLProfile* p = profile_of(device);
+    if (p && p->on) {
+        hipEventRecord(p->ev[k], s);
+        if (k == DL_STAGES) p->recorded = true;
+    }
+}
+
 template <int CB, int SCB>
-static int dl_launch(hipStream_t s, const DLArgs& a, int cus) {
+static int dl_launch(hipStream_t s, const DLArgs& a, int cus, int device) {
     static int per_cu = 0;  // resident gate|up blocks a CU, once per instantiation
     if (per_cu == 0) {
         int n = 0;
@@ -690,15 +708,21 @@ static int dl_launch(hipStream_t s, const DLArgs& a, int cus) {
     const int items = a.U * NH * 2 * KC;
     int grid = per_cu * cus;
     if (grid > items) grid = items;
+    mark_stage(s, device, 0);
     gateup_kernel<CB, SCB><<<grid, DL_THREADS, 0, s>>>(a);
     int r = launched();
     if (r) return r;
+    mark_stage(s, device, 1);
     epilogue_kernel<<<a.U * NH, DL_THREADS, 0, s>>>(a);
     if ((r = launched())) return r;
+    mark_stage(s, device, 2);
     down_kernel<CB, SCB><<<a.U * DB, DL_THREADS, 0, s>>>(a);
     if ((r = launched())) return r;
+    mark_stage(s, device, 3);
     combine_kernel<<<(a.R * DB + DL_WAVES - 1) / DL_WAVES, DL_THREADS, 0, s>>>(a);
-    return launched();
+    if ((r = launched())) return r;
+    mark_stage(s, device, 4);
+    return EA_OK;
 }
 
 // The decode layer in four launches: routing from logits (when given), the routed experts of `ex`, the shared expert
@@ -761,10 +785,10 @@ int decode_layer(hipStream_t s, const void* x, int x_dtype, uint32_t x_stride, c
     a.U = a.hs + (int)(P < E ? P : E);
     a.status = c->status;
     const int rcb = (int)ex->cb;
-    if (rcb == 1 && scb == 1) return dl_launch<1, 1>(s, a, c->cus);
-    if (rcb == 1 && scb == 2) return dl_launch<1, 2>(s, a, c->cus);
-    if (rcb == 2 && scb == 2) return dl_launch<2, 2>(s, a, c->cus);
-    if (rcb == 2 && scb == 1) return dl_launch<2, 1>(s, a, c->cus);
+    if (rcb == 1 && scb == 1) return dl_launch<1, 1>(s, a, c->cus, c->device);
+    if (rcb == 1 && scb == 2) return dl_launch<1, 2>(s, a, c->cus, c->device);
+    if (rcb == 2 && scb == 2) return dl_launch<2, 2>(s, a, c->cus, c->device);
+    if (rcb == 2 && scb == 1) return dl_launch<2, 1>(s, a, c->cus, c->device);
     return EA_UNPORTED_GROUPED_VARIANT;
 }
 
@@ -773,6 +797,34 @@ int decode_layer(hipStream_t s, const void* x, int x_dtype, uint32_t x_stride, c
 using namespace ea;
 
 extern "C" {
+
+int ea_profile_enable(int on) {
+    EA_REQUIRE_CTX(c);
+    DLProfile* p = profile_of(c->device);
+    if (!p) return EA_BAD_ARGUMENT;
+    if (on && !p->ev[0])
+        for (int k = 0; k <= DL_STAGES; ++k) {
+            const int r = hip_status(hipEventCreate(&p->ev[k]));
+            if (r) return r;
+        }
+    p->on = on != 0;
+    p->recorded = false;
+    return EA_OK;
+}
+
+int ea_profile_stages(float* ms, uint32_t n) {
+    EA_REQUIRE_CTX(c);
+    DLProfile* p = profile_of(c->device);
+    if (!p || !ms || n < (uint32_t)DL_STAGES) return EA_BAD_ARGUMENT;
+    if (!p->recorded) return EA_INVALID;
+    int r = hip_status(hipEventSynchronize(p->ev[DL_STAGES]));
+    if (r) return r;
+    for (int k = 0; k < DL_STAGES; ++k) {
+        r = hip_status(hipEventElapsedTime(&ms[k], p->ev[k], p->ev[k + 1]));
+        if (r) return r;
+    }
+    return EA_OK;
+}
 
 int ea_ffn_moe_decode(ea_stream_t stream, const void* x, int x_dtype, uint32_t x_stride, const float* logits,
                       const float* bias, float scale, int32_t* pick, float* wts, const ea_routed* ex,

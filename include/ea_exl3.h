@@ -235,6 +235,16 @@ int ea_ffn_moe_decode(ea_stream_t stream, const void* x, int x_dtype, uint32_t x
                       const float* bias, float scale, int32_t* pick, float* wts, const ea_routed* ex,
                       const ea_linear* const* shared, const ea_moe_scratch* s, float* out, uint32_t R);
 
+/* ---- benchmark instrumentation (no counterpart in the reference) ------------------------------------------- */
+
+/* With on != 0, every call that runs the decode layer's four launches (ea_ffn_moe_decode, and ea_moe_routed when it
+ * takes that path) records a HIP event on its stream before each launch (gate|up, epilogue, down, combine) and after
+ * the last. For benchmarks; not under graph capture. */
+int ea_profile_enable(int on);
+/* ms[0..3]: the four launches of the most recent recorded call, in milliseconds (waits for that call); n >= 4.
+ * EA_INVALID when nothing was recorded since ea_profile_enable. */
+int ea_profile_stages(float* ms, uint32_t n);
+
 #ifdef __cplusplus
 }
 #endif

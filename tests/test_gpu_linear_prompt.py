@@ -89,7 +89,8 @@ def test_linear_three_jobs_one_launch(ea):
                                      1, lin.sk, lin.wk))
         outs.append(device.zeros((M, N), torch.float32))
     sc = linear.Scratch(M, K, max(l.sk * M * l.n for l in lins))
-    linear.call(device.stream(), sc, lins, device.upload(x).data_ptr(), 0, M, [o.data_ptr() for o in outs], [2, 2, 2])
+    dx = device.upload(x)
+    linear.call(device.stream(), sc, lins, dx.data_ptr(), 0, M, [o.data_ptr() for o in outs], [2, 2, 2])
     for o, w, l in zip(outs, wants, lins):
         assert_close_rms(device.download(o), w, 1e-4, "job")
         assert int(device.download(l.counters).sum()) == 0
@@ -105,11 +106,12 @@ def test_linear_errors(ea):
     b = linear.Linear(T2, synth.scales(82, 512, 1.0), svh, 512, 128, 8, 1)
     sc = linear.Scratch(1, 512, 4096)
     y = device.zeros((1, 128), torch.float32)
+    dx = device.upload(x)
     with pytest.raises(EaError) as e:  # different K: not groupable (linear.zig:270-275)
-        linear.call(device.stream(), sc, [a, b], device.upload(x).data_ptr(), 1, 1, [y.data_ptr()] * 2, [2, 2])
+        linear.call(device.stream(), sc, [a, b], dx.data_ptr(), 1, 1, [y.data_ptr()] * 2, [2, 2])
     assert e.value.code == 14
     with pytest.raises(EaError) as e:  # 129 rows
-        linear.call(device.stream(), sc, [a], device.upload(x).data_ptr(), 1, 129, [y.data_ptr()], [2])
+        linear.call(device.stream(), sc, [a], dx.data_ptr(), 1, 129, [y.data_ptr()], [2])
     assert e.value.code == 14
 
 
@@ -176,7 +178,8 @@ def test_prompt_half_sums_and_invalid(ea):
     pick2[0, 3] = -1  # a slot that is not an expert adds nothing
     want = orc.prompt_experts(x, pick2, wts, oracle_routed(host), R, 8, bf16=True)
     h = device.zeros((R, D), torch.float16)
-    pe.run(device.stream(), dx.data_ptr(), D, device.upload(pick2).data_ptr(), dw.data_ptr(), ex, sc, h.data_ptr(), R,
+    dp2 = device.upload(pick2)
+    pe.run(device.stream(), dx.data_ptr(), D, dp2.data_ptr(), dw.data_ptr(), ex, sc, h.data_ptr(), R,
            do_round=False, half_sums=True)
     got = device.download(h).view(np.float16).astype(np.float32)
     assert_close_rms(got, want, 2e-3, "half sums")
