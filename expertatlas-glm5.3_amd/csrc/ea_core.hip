@@ -147,7 +147,6 @@ const char* ea_strerror(int s) {
         case EA_NOT_INITIALIZED: return "ea_init was not called on this device";
         case EA_BAD_ARGUMENT: return "bad argument";
         case EA_UNSUPPORTED_WIDTH: return "an expert width (K2) or codebook this build has no decoder for";
-        case EA_WAIT_TIMEOUT: return "a dependency wait of the one-launch layer ran out (overlapping calls on one scratch?)";
         default: return "unknown status";
     }
 }

@@ -39,7 +39,7 @@ __host__ __device__ inline T* dptr(uint64_t a) {
 int fill_words(hipStream_t s, void* p, uint32_t v, size_t n);
 
 // Device-side error codes written into DevCtx::status.
-enum DeviceError : int { DEV_UNSUPPORTED_WIDTH = EA_UNSUPPORTED_WIDTH, DEV_WAIT_TIMEOUT = EA_WAIT_TIMEOUT };
+enum DeviceError : int { DEV_UNSUPPORTED_WIDTH = EA_UNSUPPORTED_WIDTH };
 
 }  // namespace ea
 

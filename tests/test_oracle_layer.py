@@ -194,3 +194,26 @@ def test_exl3_linear_equals_dense(M, K, N, k2, cb):
     y = orc.exl3_linear(xh, S, 8 * tw, (K // 16) * 8 * tw, svh, M, K, N, k2, cb, sk, wk)
     want = synth.bf16_to_f32(x).astype(np.float64) @ dense_weight(T, K, N, k2, cb, suh, svh)
     assert_close_rms(y, want, 2e-3, "oracle exl3 linear vs dense fp64")
+
+
+# ---- the shared expert's activation --------------------------------------------------------------------------------
+
+def test_swiglu2_against_float64_and_closed_forms():
+    """swiglu2 (native_ops.cu:429-441): out = bf16(bf16(silu(g)) * u). Against float64 silu with the same two bf16
+    rounding points the result may differ by one bf16 ulp (the fp32 exp); silu(0) = 0 exactly; for g >= 20,
+    silu(g) rounds to g in bf16, so out = bf16(g * u); a sign flip of u flips the output's sign."""
+    rng = np.random.default_rng(7)
+    g = synth.bf16_bits(rng.standard_normal(4096) * 4)
+    u = synth.bf16_bits(rng.standard_normal(4096))
+    got = synth.bf16_to_f32(orc.swiglu2(g, u)).astype(np.float64)
+    gf, uf = synth.bf16_to_f32(g).astype(np.float64), synth.bf16_to_f32(u).astype(np.float64)
+    s = synth.bf16_to_f32(synth.bf16_bits(gf / (1.0 + np.exp(-gf)))).astype(np.float64)
+    want = synth.bf16_to_f32(synth.bf16_bits(s * uf)).astype(np.float64)
+    ulp = np.abs(want) * 2.0 ** -7 + 1e-30
+    assert np.all(np.abs(got - want) <= ulp)
+    zero = synth.bf16_bits(np.zeros(8))
+    assert np.all(synth.bf16_to_f32(orc.swiglu2(zero, u[:8])) == 0.0)
+    big = synth.bf16_bits(np.full(8, 24.0))
+    np.testing.assert_array_equal(orc.swiglu2(big, u[:8]), synth.bf16_bits(24.0 * synth.bf16_to_f32(u[:8])))
+    neg = synth.bf16_bits(-synth.bf16_to_f32(u))
+    np.testing.assert_array_equal(synth.bf16_to_f32(orc.swiglu2(g, neg)), -synth.bf16_to_f32(orc.swiglu2(g, u)))
