@@ -44,6 +44,8 @@ struct DLLayout {
     int* ucount;        // [1] routed units
     int* members;       // [DL_MAXP, DL_MAXR] pair ids of a routed unit, ascending
     int* mcount;        // [DL_MAXP]
+    uint64_t* dptr;     // [DL_MAXP] a routed unit's down trellis address
+    int* dk2;           // [DL_MAXP] and width
 };
 
 struct DLArgs {
@@ -89,17 +91,40 @@ __device__ __forceinline__ float wave_max(float v) {
     return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
 }
 
+struct RouteSh {
+    int pick[DL_MAXP];
+    float wts[DL_MAXP];
+    int unit[DL_MAXE];  // count of an expert's picks, then its routed unit (-1: not picked)
+    int uids[DL_MAXP];
+    int members[DL_MAXP][DL_MAXR];
+    int mcount[DL_MAXP];
+    int wsum[DL_WAVES];
+    int ucount;
+    uint64_t uptr[DL_MAXP][3];  // a routed unit's gate, up and down trellis addresses and widths
+    int uk2[DL_MAXP][3];
+    uint64_t tptr[3][256];      // one row's path: every expert's addresses and widths, loaded with the logits
+    int tk2[3][256];
+};
+
 // One row's top-8 on one wave (E = 256: expert q * 64 + lane in choice[q]): choice = sigmoid + bias, the larger
 // first, the lower id on a tie; wts = sigmoid / (sum of the picks' sigmoids in pick order + 1e-20) * scale
 // (native_ops.cu:1015-1068). A round: the wave maximum, then the lowest id holding it from four ballots.
 __device__ __forceinline__ void topk8_wave(const float* logits, const float* bias, float scale, int* pick, float* wts,
                                            int lane) {
+    // all eight loads in flight before any is used
+    float lg[4], bs[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        lg[q] = logits[q * 64 + lane];
+        bs[q] = bias[q * 64 + lane];
+    }
+    asm volatile("" : "+v"(lg[0]), "+v"(lg[1]), "+v"(lg[2]), "+v"(lg[3]), "+v"(bs[0]), "+v"(bs[1]), "+v"(bs[2]),
+                 "+v"(bs[3]));
     float score[4], choice[4];
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-        const int e = q * 64 + lane;
-        score[q] = 1.0f / (expf_path(0.0f - logits[e]) + 1.0f);
-        choice[q] = score[q] + bias[e];
+        score[q] = 1.0f / (expf_path(0.0f - lg[q]) + 1.0f);
+        choice[q] = score[q] + bs[q];
     }
     float total = 0.0f, my_w = 0.0f;
     int my_p = 0;
@@ -130,22 +155,58 @@ __device__ __forceinline__ void topk8_wave(const float* logits, const float* bia
     }
 }
 
-struct RouteSh {
-    int pick[DL_MAXP];
-    float wts[DL_MAXP];
-    int unit[DL_MAXE];  // count of an expert's picks, then its routed unit (-1: not picked)
-    int uids[DL_MAXP];
-    int members[DL_MAXP][DL_MAXR];
-    int mcount[DL_MAXP];
-    int wsum[DL_WAVES];
-    int ucount;
-};
+
+// The trellis addresses and widths of every routed unit, into LDS (one round trip for the block, instead of one an
+// item): gate and up, and down for the block that publishes them.
+__device__ __forceinline__ void route_tables(const DLArgs& a, RouteSh& sh, int mats) {
+    for (int u = threadIdx.x; u < sh.ucount; u += DL_THREADS) {
+        const int e = sh.uids[u];
+        for (int m = 0; m < mats; ++m) {
+            sh.uptr[u][m] = (uint64_t)a.ptr[m][e];
+            sh.uk2[u][m] = a.k2t[m][e];
+        }
+    }
+    __syncthreads();
+}
 
 // The window's routing in LDS: picks (top-8 of the logits, or the given picks), the distinct picked experts in id
-// order and each one's pairs in ascending order (exl3_experts.cu:36-90).
-__device__ __forceinline__ void route_block(const DLArgs& a, RouteSh& sh) {
+// order and each one's pairs in ascending order (exl3_experts.cu:36-90), and the units' trellis tables (`mats`
+// matrices of each).
+__device__ __forceinline__ void route_block(const DLArgs& a, RouteSh& sh, int mats) {
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const int n = a.R * DL_SLOTS;
+    if (a.logits && a.R == 1) {
+        // one row: the tables of all 256 experts are loaded with the logits (a thread an expert), so the picks' need
+        // no round trip after the top-8; each pick names a different expert and is a unit of its own
+        uint64_t tp[3];
+        int tk[3];
+#pragma unroll
+        for (int m = 0; m < 3; ++m) {
+            tp[m] = (uint64_t)a.ptr[m][t];
+            tk[m] = a.k2t[m][t];
+        }
+        if (wave == 0) topk8_wave(a.logits, a.bias, a.scale, sh.pick, sh.wts, lane);
+#pragma unroll
+        for (int m = 0; m < 3; ++m) {
+            sh.tptr[m][t] = tp[m];
+            sh.tk2[m][t] = tk[m];
+        }
+        __syncthreads();
+        if (t < DL_SLOTS) {
+            const int e = sh.pick[t];
+            sh.uids[t] = e;
+            sh.mcount[t] = 1;
+            sh.members[t][0] = t;
+#pragma unroll
+            for (int m = 0; m < 3; ++m) {
+                sh.uptr[t][m] = sh.tptr[m][e];
+                sh.uk2[t][m] = sh.tk2[m][e];
+            }
+        }
+        if (t == 0) sh.ucount = DL_SLOTS;
+        __syncthreads();
+        return;
+    }
     if (a.logits) {
         for (int r = wave; r < a.R; r += DL_WAVES)
             topk8_wave(a.logits + (size_t)r * 256, a.bias, a.scale, sh.pick + r * DL_SLOTS, sh.wts + r * DL_SLOTS,
@@ -221,9 +282,10 @@ __device__ __forceinline__ void route_block(const DLArgs& a, RouteSh& sh) {
         }
     }
     __syncthreads();
+    route_tables(a, sh, mats);
 }
 
-// Block 0 hands the routing to the caller (pick, wts) and the grouping to the later launches.
+// One block hands the routing to the caller (pick, wts) and the grouping to the later launches.
 __device__ __forceinline__ void route_publish(const DLArgs& a, const RouteSh& sh) {
     const int t = threadIdx.x;
     const int n = a.R * DL_SLOTS;
@@ -236,6 +298,8 @@ __device__ __forceinline__ void route_publish(const DLArgs& a, const RouteSh& sh
     for (int u = t; u < sh.ucount; u += DL_THREADS) {
         l.uids[u] = sh.uids[u];
         l.mcount[u] = sh.mcount[u];
+        l.dptr[u] = sh.uptr[u][2];
+        l.dk2[u] = sh.uk2[u][2];
         for (int i = 0; i < sh.mcount[u]; ++i) l.members[u * DL_MAXR + i] = sh.members[u][i];
     }
     if (t == 0) *l.ucount = sh.ucount;
@@ -243,11 +307,12 @@ __device__ __forceinline__ void route_publish(const DLArgs& a, const RouteSh& sh
 
 // ---- the MFMA core of an item ------------------------------------------------------------------------------------
 
-// acc[j] += A (16 staged rows in LDS, rows >= nm read as zero) @ tiles (t, j) for t in [0, NKT), j in {0, 1}: the
-// wave's trellis words, all loaded before (w).
-template <int CB, int K2, int NKT, int NW>
-__device__ __forceinline__ void mfma_tiles(const TileLane<K2, CB>& tl, const uint32_t (&w)[2][NKT][NW],
-                                           const uint16_t* xs, int nm, int lane, f4v (&acc)[2]) {
+// The wave's two column tiles times the activation rows in xs over NKT k tiles: acc[j] += A (rows of xs, the MFMA's
+// 16 rows) x B (tile pair (t, t + 1) of column tile j). Each pair decodes right before its MFMA, so the decoded values
+// never all live at once.
+template <int CB, int K2, int NKT>
+__device__ __forceinline__ void mfma_tiles(const uint32_t (&w)[2][NKT][2], int sh, const uint16_t* xs, int nm,
+                                           int lane, f4v (&acc)[2]) {
     const int m = lane & 15, g = (lane >> 4) & 3;
     const bool live = m < nm;
     const uint16_t* xr = xs + m * DL_RS + 2 * g;
@@ -262,12 +327,19 @@ __device__ __forceinline__ void mfma_tiles(const TileLane<K2, CB>& tl, const uin
         }
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
-            const u2v b0 = tl.decode(w[j][t]);
-            const u2v b1 = tl.decode(w[j][t + 1]);
-            const h8v b = __builtin_bit_cast(h8v, (u4v{b0.x, b0.y, b1.x, b1.y}));
-            acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, acc[j], 0, 0, 0);
+            const u2v b0 = decode_quad<K2, CB>(w[j][t][0], w[j][t][1], sh);
+            const u2v b1 = decode_quad<K2, CB>(w[j][t + 1][0], w[j][t + 1][1], sh);
+            const h8v bb = __builtin_bit_cast(h8v, (u4v{b0.x, b0.y, b1.x, b1.y}));
+            acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bb, acc[j], 0, 0, 0);
         }
     }
+}
+
+// The same product for a run-time width in 2..10 (false for any other): only this loop is specialised per width.
+template <int CB, int NKT>
+__device__ __forceinline__ bool mfma_tiles_k2(int k2, const uint32_t (&w)[2][NKT][2], int sh, const uint16_t* xs,
+                                              int nm, int lane, f4v (&acc)[2]) {
+    return EA_K2_SWITCH(k2, 2, 10, (mfma_tiles<CB, K2V, NKT>(w, sh, xs, nm, lane, acc)));
 }
 
 // Where an item's tiles are: a buffer over the whole matrix, the byte offset of tile (0, 0) and the byte stride between
@@ -277,13 +349,33 @@ struct TileSpan {
     int off, kstride;
 };
 
-// This lane's words of tiles (t, j), t in [0, NKT), j in {0, 1}, all issued before any is used.
-template <int CB, int K2, int NKT, int NW>
-__device__ __forceinline__ void fetch_tiles(const TileLane<K2, CB>& tl, const TileSpan& sp, uint32_t (&w)[2][NKT][NW]) {
+// The two words of a tile this lane's four values come from and their bit offset, for a width in 2..10 (zeros for
+// any other: the loads stay inside the buffer and the product then reports the width).
+struct LaneQuad {
+    int w0, w1, sh;
+};
+__device__ __forceinline__ LaneQuad lane_quad(int k2, int lane) {
+    LaneQuad r{0, 0, 0};
+    EA_K2_SWITCH(k2, 2, 10, ([&] {
+                     const Quad q = quad_of<K2V>(mfma_lane_p0(lane));
+                     r = LaneQuad{q.wa, q.wb, q.sh};
+                 }()));
+    return r;
+}
+
+// This lane's words of tiles (t, j), t in [0, NKT), j in {0, 1} (tiles of `tile_bytes`), all issued before any is
+// used.
+template <int NKT>
+__device__ __forceinline__ void fetch_tiles(const TileSpan& sp, int tile_bytes, const LaneQuad& lq,
+                                            uint32_t (&w)[2][NKT][2]) {
 #pragma unroll
     for (int t = 0; t < NKT; ++t)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) tl.fetch(sp.r, sp.off + t * sp.kstride + j * 16 * K2, w[j][t]);
+        for (int j = 0; j < 2; ++j) {
+            const int soff = sp.off + t * sp.kstride + j * tile_bytes;
+            w[j][t][0] = __builtin_amdgcn_raw_buffer_load_b32(sp.r, 4 * lq.w0, soff, 0);
+            w[j][t][1] = __builtin_amdgcn_raw_buffer_load_b32(sp.r, 4 * lq.w1, soff, 0);
+        }
 }
 
 // Wave-uniform values the compiler cannot prove uniform (a wave's index, what a block read from LDS or memory) moved
@@ -320,13 +412,14 @@ __device__ __forceinline__ int member_row(const UnitView& uv, int m) { return uv
 
 // The item's product for one width: prefetch every trellis word, rotate the activations of the k chunk into xs
 // (xs[m][k] = fp16(((x * suh) @ H) * HAD_SCALE), a wave a (row, 128-block)), then the MFMAs.
-template <int CB, int K2>
-__device__ __forceinline__ void gateup_product(const DLArgs& a, const UnitView& uv, const TileSpan& sp, const uint16_t* suh, int c,
-                               uint16_t* xs, f4v (&acc)[2]) {
-    using TL = TileLane<K2, CB>;
+template <int CB>
+__device__ __forceinline__ bool gateup_product(const DLArgs& a, const UnitView& uv, const TileSpan& sp, int k2,
+                                               const uint16_t* suh, int c, uint16_t* xs, f4v (&acc)[2]) {
     const int lane = opaque_lane(threadIdx.x & 63), wave = uniform((int)threadIdx.x >> 6);
-    const TL tl(lane);
-    // activations and suh of this wave's (row, block) tasks first: their loads then complete ahead of the trellis
+    const LaneQuad lq = lane_quad(k2, lane);
+    // activations and suh of this wave's (row, block) tasks, then the trellis: loads complete in order, so the
+    // rotation waits only for the first two while the trellis is in flight; the tiles decode pair by pair between the
+    // MFMAs
     constexpr int MT = 2 * DL_MAXR / DL_WAVES;
     uint32_t xv[MT], sv[MT];
     const int ntask = 2 * uv.nm;
@@ -342,8 +435,8 @@ __device__ __forceinline__ void gateup_product(const DLArgs& a, const UnitView& 
             sv[i] = *reinterpret_cast<const uint32_t*>(suh + k);
         }
     }
-    uint32_t w[2][DL_KT][TL::NW];
-    fetch_tiles<CB, K2, DL_KT, TL::NW>(tl, sp, w);
+    uint32_t w[2][DL_KT][2];
+    fetch_tiles<DL_KT>(sp, 16 * k2, lq, w);
     const bool bf = a.x_dtype == BF16;
 #pragma unroll
     for (int i = 0; i < MT; ++i) {
@@ -361,118 +454,158 @@ __device__ __forceinline__ void gateup_product(const DLArgs& a, const UnitView& 
         }
     }
     __syncthreads();
-    mfma_tiles<CB, K2, DL_KT, TL::NW>(tl, w, xs, uv.nm, lane, acc);
+    return mfma_tiles_k2<CB, DL_KT>(k2, w, lq.sh, xs, uv.nm, lane, acc);
 }
 
-// The unit of block u as the later launches see it: from the grouping block 0 of the gate|up launch wrote.
-__device__ __forceinline__ bool unit_from_layout(const DLArgs& a, int u, UnitView& uv, int* s_mem) {
+// The unit of block u as the later launches see it, from the grouping the gate|up launch published. Every field loads
+// at once (a unit's members past its count are read and not used), and with them the unit's down trellis address and
+// width, so one round trip precedes the trellis.
+struct UnitDown {
+    const uint32_t* ptr;
+    int k2;
+};
+__device__ __forceinline__ bool unit_from_layout(const DLArgs& a, int u, UnitView& uv, int* s_mem,
+                                                 UnitDown* down = nullptr) {
     const DLLayout& l = a.lay;
-    if (u >= a.hs + *l.ucount) return false;
+    const int ur = u > a.hs ? u - a.hs : 0;
+    const int ucount = *l.ucount;
+    const int nm = l.mcount[ur], e = l.uids[ur], dk2 = l.dk2[ur];
+    const uint64_t dptr = l.dptr[ur];
+    if (threadIdx.x < DL_MAXR) s_mem[threadIdx.x] = l.members[ur * DL_MAXR + threadIdx.x];
+    if (u >= a.hs + ucount) return false;
     uv.shared = a.hs && u == 0;
-    const int ur = u - a.hs;
-    uv.nm = uniform(uv.shared ? a.R : l.mcount[ur]);
-    uv.e = uniform(uv.shared ? -1 : l.uids[ur]);
-    if (!uv.shared && threadIdx.x < uv.nm) s_mem[threadIdx.x] = l.members[ur * DL_MAXR + threadIdx.x];
+    uv.nm = uniform(uv.shared ? a.R : nm);
+    uv.e = uniform(uv.shared ? -1 : e);
     uv.mem = s_mem;
+    if (down) {
+        down->ptr = uniform(reinterpret_cast<const uint32_t*>(dptr));
+        down->k2 = uniform(dk2);
+    }
     return true;
 }
 
-// Block (unit, column block nh of 128): the chunks summed in order, FWHT, svh, SwiGLU, suh_d, FWHT -> the unit's down
-// inputs; a wave a member.
-__global__ void __launch_bounds__(DL_THREADS) epilogue_kernel(DLArgs a) {
-    __shared__ int s_mem[DL_MAXR];
+// ---- the SwiGLU epilogue --------------------------------------------------------------------------------------------
+
+// The gate|up partials of member q, column block nh, matrix mat (two columns a lane): every chunk's pair in flight at
+// once.
+__device__ __forceinline__ void zp_load(const DLArgs& a, int q, int nh, int mat, int lane, float2 (&v)[DL_MAXKC]) {
     const int NH = a.I / 128, KC = a.D / 256;
-    const int u = blockIdx.x / NH, nh = blockIdx.x % NH;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    UnitView uv;
-    if (!unit_from_layout(a, u, uv, s_mem)) return;
-    __syncthreads();
-    for (int m = wave; m < uv.nm; m += DL_WAVES) {
-        const int q = member_q(a, uv, m);
-        const float* zg = a.lay.zp + ((size_t)(q * NH + nh) * 2 + 0) * KC * 128 + 2 * lane;
-        const float* zu = zg + (size_t)KC * 128;
-        // every chunk's pair of values in flight at once; summed in chunk order
-        float2 gv[DL_MAXKC], uw[DL_MAXKC];
+    const float* z = a.lay.zp + ((size_t)(q * NH + nh) * 2 + mat) * KC * 128 + 2 * lane;
 #pragma unroll
-        for (int cc = 0; cc < DL_MAXKC; ++cc) {
-            const int ci = cc < KC ? cc : KC - 1;
-            gv[cc] = *reinterpret_cast<const float2*>(zg + ci * 128);
-            uw[cc] = *reinterpret_cast<const float2*>(zu + ci * 128);
-        }
-        float g0 = 0.f, g1 = 0.f, u0 = 0.f, u1 = 0.f;
-#pragma unroll
-        for (int cc = 0; cc < DL_MAXKC; ++cc)
-            if (cc < KC) {
-                g0 += gv[cc].x;
-                g1 += gv[cc].y;
-                u0 += uw[cc].x;
-                u1 += uw[cc].y;
-            }
-        fwht128_w64(g0, g1, lane);
-        fwht128_w64(u0, u1, lane);
-        const int n = nh * 128 + 2 * lane;
-        const float g[2] = {g0, g1}, u[2] = {u0, u1};
-        float v[2];
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            if (uv.shared) {
-                // the shared expert's gate / up linears write bf16 (forward.zig:2330), swiglu2 (native_ops.cu:429-441)
-                // makes act in bf16, and the down linear's rot_in reads it (exl3_linear.cu:152-173)
-                const float gq = bf16r(g[j] * HAD_SCALE * h2f(a.sh_svh[0][n + j]));
-                const float uq = bf16r(u[j] * HAD_SCALE * h2f(a.sh_svh[1][n + j]));
-                const float s = bf16r(gq / (expf_path(0.0f - gq) + 1.0f));
-                v[j] = bf16r(s * uq) * h2f(a.sh_suh[2][n + j]);
-            } else {
-                // act_mode 1 with no limit (moe.zig:290; exl3_experts.cu:142-184)
-                const size_t at = (size_t)uv.e * a.I + n + j;
-                const float gg = g[j] * HAD_SCALE * h2f(a.svh_g[at]);
-                const float ug = u[j] * HAD_SCALE * h2f(a.svh_u[at]);
-                v[j] = gg / (1.f + expf_path(-gg)) * ug * h2f(a.suh_d[at]);
-            }
-        }
-        fwht128_w64(v[0], v[1], lane);
-        *reinterpret_cast<uint32_t*>(a.lay.xd + (size_t)q * a.I + n) =
-            (uint32_t)f2h(v[0] * HAD_SCALE) | ((uint32_t)f2h(v[1] * HAD_SCALE) << 16);
+    for (int cc = 0; cc < DL_MAXKC; ++cc) {
+        const int ci = cc < KC ? cc : KC - 1;
+        v[cc] = *reinterpret_cast<const float2*>(z + ci * 128);
     }
 }
 
-template <int CB, int SCB>
+// Their sum in chunk order.
+__device__ __forceinline__ float2 zp_sum(const DLArgs& a, const float2 (&v)[DL_MAXKC]) {
+    const int KC = a.D / 256;
+    float s0 = 0.f, s1 = 0.f;
+#pragma unroll
+    for (int cc = 0; cc < DL_MAXKC; ++cc)
+        if (cc < KC) {
+            s0 += v[cc].x;
+            s1 += v[cc].y;
+        }
+    return float2{s0, s1};
+}
+
+// A matrix's outputs of a column block: FWHT of the sums, HAD_SCALE, the output scale svh. The shared expert's gate
+// and up linears write bf16 (forward.zig:2330); the routed experts keep fp32 (exl3_experts.cu:142-184).
+__device__ __forceinline__ float2 gu_out(const DLArgs& a, const UnitView& uv, int nh, int mat, float2 v, int lane) {
+    fwht128_w64(v.x, v.y, lane);
+    const int n = nh * 128 + 2 * lane;
+    const uint16_t* svh =
+        uv.shared ? (mat ? a.sh_svh[1] : a.sh_svh[0]) : (mat ? a.svh_u : a.svh_g) + (size_t)uv.e * a.I;
+    float o0 = v.x * HAD_SCALE * h2f(svh[n]);
+    float o1 = v.y * HAD_SCALE * h2f(svh[n + 1]);
+    if (uv.shared) {
+        o0 = bf16r(o0);
+        o1 = bf16r(o1);
+    }
+    return float2{o0, o1};
+}
+
+// SwiGLU of a column block, the down input scale suh, FWHT, HAD_SCALE: the packed fp16 down inputs of columns n, n + 1.
+// Routed experts: act_mode 1 with no limit (moe.zig:290; exl3_experts.cu:142-184). The shared expert: swiglu2 in bf16
+// (native_ops.cu:429-441), read by the down linear's rot_in (exl3_linear.cu:152-173).
+__device__ __forceinline__ uint32_t act_pair(const DLArgs& a, const UnitView& uv, int nh, float2 g, float2 u, int lane) {
+    const int n = nh * 128 + 2 * lane;
+    const float gs[2] = {g.x, g.y}, us[2] = {u.x, u.y};
+    float v[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        if (uv.shared) {
+            const float sg = bf16r(gs[j] / (expf_path(0.0f - gs[j]) + 1.0f));
+            v[j] = bf16r(sg * us[j]) * h2f(a.sh_suh[2][n + j]);
+        } else {
+            v[j] = gs[j] / (1.f + expf_path(-gs[j])) * us[j] * h2f(a.suh_d[(size_t)uv.e * a.I + n + j]);
+        }
+    }
+    fwht128_w64(v[0], v[1], lane);
+    return (uint32_t)f2h(v[0] * HAD_SCALE) | ((uint32_t)f2h(v[1] * HAD_SCALE) << 16);
+}
+
+// Block (unit, column block nh of 128): the unit's down inputs, a wave a member.
+__global__ void __launch_bounds__(DL_THREADS) epilogue_kernel(DLArgs a) {
+    __shared__ int s_mem[DL_MAXR];
+    const int NH = a.I / 128;
+    const int unit = blockIdx.x / NH, nh = blockIdx.x % NH;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    UnitView uv;
+    if (!unit_from_layout(a, unit, uv, s_mem)) return;
+    __syncthreads();
+    for (int m = wave; m < uv.nm; m += DL_WAVES) {
+        const int q = member_q(a, uv, m);
+        float2 zg[DL_MAXKC], zu[DL_MAXKC];
+        zp_load(a, q, nh, 0, lane, zg);
+        zp_load(a, q, nh, 1, lane, zu);
+        const float2 g = gu_out(a, uv, nh, 0, zp_sum(a, zg), lane);
+        const float2 u = gu_out(a, uv, nh, 1, zp_sum(a, zu), lane);
+        *reinterpret_cast<uint32_t*>(a.lay.xd + (size_t)q * a.I + nh * 128 + 2 * lane) = act_pair(a, uv, nh, g, u, lane);
+    }
+}
+
+// Item (unit u, column block nh, matrix mat, k chunk c) of the shared expert (SHARED, codebook CB) or of a routed
+// unit.
+template <int CB, bool SHARED>
 __device__ __forceinline__ void gateup_item(const DLArgs& a, const RouteSh& sh, int u, int nh, int mat, int c,
                                             uint16_t* xs) {
     const int lane = threadIdx.x & 63, wave = uniform((int)threadIdx.x >> 6);
     const int KC = a.D / 256, NH = a.I / 128;
     UnitView uv;
-    uv.shared = a.hs && u == 0;
+    uv.shared = SHARED;
     const int ur = u - a.hs;
-    uv.nm = uniform(uv.shared ? a.R : sh.mcount[ur]);
-    uv.e = uniform(uv.shared ? -1 : sh.uids[ur]);
-    uv.mem = uv.shared ? nullptr : sh.members[ur];
+    uv.nm = SHARED ? a.R : uniform(sh.mcount[ur]);
+    uv.e = SHARED ? -1 : uniform(sh.uids[ur]);
+    uv.mem = SHARED ? nullptr : sh.members[ur];
     // wave w: n tiles nh * 8 + 2w, + 1 over the 16 k tiles of chunk c
     const int nt0 = nh * 8 + 2 * wave, kt0 = c * DL_KT;
     f4v acc[2] = {f4v{0.f, 0.f, 0.f, 0.f}, f4v{0.f, 0.f, 0.f, 0.f}};
-    bool ok;
     // matrix D x I: routed in the expert layout (tile (kt, nt) at (kt * I / 16 + nt) * TW words), the shared expert
     // in strips ([I / 128][D / 16][8][TW])
     const int ns = a.I / 16;
-    if (uv.shared) {
-        const int TWB = 16 * a.sh_k2;  // bytes a tile
-        TileSpan sp;
+    TileSpan sp;
+    int k2;
+    const uint16_t* suh;
+    if constexpr (SHARED) {
+        k2 = a.sh_k2;
+        const int TWB = 16 * k2;  // bytes a tile
         sp.r = buffer_rsrc(mat ? a.sh_w[1] : a.sh_w[0], (uint32_t)((a.D / 16) * ns * TWB));
         sp.off = ((nt0 >> 3) * (a.D / 16) * 8 + kt0 * 8 + (nt0 & 7)) * TWB;
         sp.kstride = 8 * TWB;
-        const uint16_t* suh = mat ? a.sh_suh[1] : a.sh_suh[0];
-        ok = EA_K2_SWITCH(a.sh_k2, 2, 10, (gateup_product<SCB, K2V>(a, uv, sp, suh, c, xs, acc)));
+        suh = mat ? a.sh_suh[1] : a.sh_suh[0];
     } else {
-        const int k2 = uniform((mat ? a.k2t[1] : a.k2t[0])[uv.e]);
-        const uint32_t* T = uniform(reinterpret_cast<const uint32_t*>((mat ? a.ptr[1] : a.ptr[0])[uv.e]));
+        k2 = uniform(sh.uk2[ur][mat]);
+        const uint32_t* T = uniform(reinterpret_cast<const uint32_t*>(sh.uptr[ur][mat]));
         const int TWB = 16 * k2;
-        TileSpan sp;
         sp.r = buffer_rsrc(T, (uint32_t)((a.D / 16) * ns * TWB));
         sp.off = (kt0 * ns + nt0) * TWB;
         sp.kstride = ns * TWB;
-        const uint16_t* suh = (mat ? a.suh_u : a.suh_g) + (size_t)uv.e * a.D;
-        ok = EA_K2_SWITCH(k2, 2, 10, (gateup_product<CB, K2V>(a, uv, sp, suh, c, xs, acc)));
+        suh = (mat ? a.suh_u : a.suh_g) + (size_t)uv.e * a.D;
     }
+    const bool ok = gateup_product<CB>(a, uv, sp, k2, suh, c, xs, acc);
     if (!ok && lane == 0) record_error(a.status, DEV_UNSUPPORTED_WIDTH);
     // partial sums of this chunk: zp[q][nh][mat][c][128]
 #pragma unroll
@@ -490,99 +623,124 @@ __device__ __forceinline__ void gateup_item(const DLArgs& a, const RouteSh& sh, 
 template <int CB, int SCB>
 __global__ void __launch_bounds__(DL_THREADS) __attribute__((amdgpu_waves_per_eu(4)))
 gateup_kernel(DLArgs a) {
+    static_assert(DL_THREADS == 256, "the one-row routing loads an expert a thread");
     __shared__ RouteSh sh;
     __shared__ __attribute__((aligned(16))) uint16_t xs[DL_MAXR * DL_RS];
-    route_block(a, sh);
-    if (blockIdx.x == 0) route_publish(a, sh);
     const int NH = a.I / 128, KC = a.D / 256;
     const int per_unit = NH * 2 * KC;
-    const int units = a.hs + sh.ucount;
     const int items = a.U * per_unit;
-    for (int it = blockIdx.x; it < items; it += gridDim.x) {
+    // the shared expert's items (unit 0, the first per_unit items) need no routing: they run first, their trellis loads
+    // starting with the launch; a block routes before its first routed item, and the block that runs the first
+    // routed item publishes the routing
+    const int first_routed = a.hs * per_unit;
+    int it = blockIdx.x;
+    for (; it < items && it < first_routed; it += gridDim.x) {
+        gateup_item<SCB, true>(a, sh, 0, it / (2 * KC), (it / KC) & 1, it % KC, xs);
+        __syncthreads();
+    }
+    if (it >= items) return;
+    const bool publisher = it == first_routed;
+    route_block(a, sh, publisher ? 3 : 2);
+    if (publisher) route_publish(a, sh);
+    const int units = a.hs + sh.ucount;
+    for (; it < items; it += gridDim.x) {
         const int u = it / per_unit, rem = it % per_unit;
         if (u >= units) break;  // items run in unit order
-        gateup_item<CB, SCB>(a, sh, u, rem / (2 * KC), (rem / KC) & 1, rem % KC, xs);
+        gateup_item<CB, false>(a, sh, u, rem / (2 * KC), (rem / KC) & 1, rem % KC, xs);
         __syncthreads();
     }
 }
 
-// ---- down + combine -------------------------------------------------------------------------------------------------
+// ---- down ---------------------------------------------------------------------------------------------------------
 
-template <int CB, int K2, int NKT>
-__device__ __forceinline__ void down_product(const DLArgs& a, const UnitView& uv, const TileSpan& sp, uint16_t* xs, f4v (&acc)[2]) {
-    using TL = TileLane<K2, CB>;
-    const int lane = opaque_lane(threadIdx.x & 63);
-    const TL tl(lane);
-    // the unit's down inputs, nm rows of NKT * 16 halves: loaded ahead of the trellis, stored to LDS after it
-    constexpr int WPR = NKT * 16 / 2;  // words a row
-    constexpr int MW = DL_MAXR * WPR / DL_THREADS;
-    uint32_t xv[MW];
+// The unit's down inputs into xs, then the product. FOLD (one row: a unit has at most 8 members): the block computes
+// the inputs itself from the gate|up partials, a wave a (member, column block, matrix) task, instead of the epilogue
+// launch; the first task's partials load ahead of the trellis. Otherwise they are the epilogue's, loaded ahead of the
+// trellis. Loads complete in order, so the inputs never wait for the trellis.
+template <int CB, int SCB, int NKT, bool FOLD>
+__device__ __forceinline__ bool down_product(const DLArgs& a, const UnitView& uv, const TileSpan& sp, int k2,
+                                             uint16_t* xs, float* gus, f4v (&acc)[2]) {
+    const int lane = opaque_lane(threadIdx.x & 63), wave = uniform((int)threadIdx.x >> 6);
+    const LaneQuad lq = lane_quad(k2, lane);
+    uint32_t w[2][NKT][2];
+    if constexpr (FOLD) {
+        const int NH = a.I / 128, tasks = uv.nm * NH * 2;
+        float2 zv[DL_MAXKC];
+        if (wave < tasks) zp_load(a, member_q(a, uv, wave / (2 * NH)), (wave >> 1) % NH, wave & 1, lane, zv);
+        fetch_tiles<NKT>(sp, 16 * k2, lq, w);
+        for (int task = wave; task < tasks; task += DL_WAVES) {
+            const int m = task / (2 * NH), nh = (task >> 1) % NH, mat = task & 1;
+            if (task != wave) zp_load(a, member_q(a, uv, m), nh, mat, lane, zv);
+            const float2 o = gu_out(a, uv, nh, mat, zp_sum(a, zv), lane);
+            *reinterpret_cast<float2*>(gus + (m * 2 + mat) * DL_MAXI + nh * 128 + 2 * lane) = o;
+        }
+        __syncthreads();
+        for (int task = wave; task < uv.nm * NH; task += DL_WAVES) {
+            const int m = task / NH, nh = task % NH;
+            const float2 g = *reinterpret_cast<const float2*>(gus + (m * 2) * DL_MAXI + nh * 128 + 2 * lane);
+            const float2 u = *reinterpret_cast<const float2*>(gus + (m * 2 + 1) * DL_MAXI + nh * 128 + 2 * lane);
+            *reinterpret_cast<uint32_t*>(xs + m * DL_RS + nh * 128 + 2 * lane) = act_pair(a, uv, nh, g, u, lane);
+        }
+    } else {
+        constexpr int WPR = NKT * 16 / 2;  // words a row
+        constexpr int MW = DL_MAXR * WPR / DL_THREADS;
+        uint32_t xv[MW];
 #pragma unroll
-    for (int i = 0; i < MW; ++i) {
-        const int idx = threadIdx.x + DL_THREADS * i;
-        const int m = idx / WPR, k = 2 * (idx % WPR);
-        xv[i] = 0;
-        if (m < uv.nm) xv[i] = *reinterpret_cast<const uint32_t*>(a.lay.xd + (size_t)member_q(a, uv, m) * a.I + k);
-    }
-    uint32_t w[2][NKT][TL::NW];
-    fetch_tiles<CB, K2, NKT, TL::NW>(tl, sp, w);
+        for (int i = 0; i < MW; ++i) {
+            const int idx = threadIdx.x + DL_THREADS * i;
+            const int m = idx / WPR, k = 2 * (idx % WPR);
+            xv[i] = 0;
+            if (m < uv.nm)
+                xv[i] = *reinterpret_cast<const uint32_t*>(a.lay.xd + (size_t)member_q(a, uv, m) * a.I + k);
+        }
+        fetch_tiles<NKT>(sp, 16 * k2, lq, w);
 #pragma unroll
-    for (int i = 0; i < MW; ++i) {
-        const int idx = threadIdx.x + DL_THREADS * i;
-        const int m = idx / WPR, k = 2 * (idx % WPR);
-        if (m < uv.nm) *reinterpret_cast<uint32_t*>(xs + m * DL_RS + k) = xv[i];
+        for (int i = 0; i < MW; ++i) {
+            const int idx = threadIdx.x + DL_THREADS * i;
+            const int m = idx / WPR, k = 2 * (idx % WPR);
+            if (m < uv.nm) *reinterpret_cast<uint32_t*>(xs + m * DL_RS + k) = xv[i];
+        }
     }
     __syncthreads();
-    mfma_tiles<CB, K2, NKT, TL::NW>(tl, w, xs, uv.nm, lane, acc);
+    return uv.shared ? mfma_tiles_k2<SCB, NKT>(k2, w, lq.sh, xs, uv.nm, lane, acc)
+                     : mfma_tiles_k2<CB, NKT>(k2, w, lq.sh, xs, uv.nm, lane, acc);
 }
 
-template <int CB, int K2>
-__device__ __forceinline__ void down_product_i(const DLArgs& a, const UnitView& uv, const TileSpan& sp, uint16_t* xs, f4v (&acc)[2]) {
-    if (a.I == 256) down_product<CB, K2, 16>(a, uv, sp, xs, acc);
-    else down_product<CB, K2, 8>(a, uv, sp, xs, acc);
-}
-
-template <int CB, int SCB>
-__global__ void __launch_bounds__(DL_THREADS) __attribute__((amdgpu_waves_per_eu(4)))
-down_kernel(DLArgs a) {
-    __shared__ __attribute__((aligned(16))) uint16_t xs[DL_MAXR * DL_RS];
-    __shared__ __attribute__((aligned(16))) float ys[DL_MAXR * 128];
-    __shared__ int s_mem[DL_MAXR];
+// Block (unit, column block of 128 outputs): the members' down products, FWHT, svh -> the pair's y (or the shared
+// expert's sy).
+template <int CB, int SCB, bool FOLD>
+__device__ __forceinline__ void down_block(const DLArgs& a, uint16_t* xs, float* ys, int* s_mem, float* gus) {
     const int DB = a.D / 128;
     const int u = blockIdx.x / DB, cb = blockIdx.x % DB;
     const int lane = threadIdx.x & 63, wave = uniform((int)threadIdx.x >> 6);
     UnitView uv;
-    if (!unit_from_layout(a, u, uv, s_mem)) return;
+    UnitDown dn;
+    if (!unit_from_layout(a, u, uv, s_mem, &dn)) return;
     __syncthreads();
     const int nt0 = cb * 8 + 2 * wave, KT = a.I / 16;
     f4v acc[2] = {f4v{0.f, 0.f, 0.f, 0.f}, f4v{0.f, 0.f, 0.f, 0.f}};
-    bool ok;
     // matrix I x D: routed in the expert layout, the shared expert in strips ([D / 128][I / 16][8][TW])
     const int ns = a.D / 16;
+    const int k2 = uv.shared ? a.sh_k2 : dn.k2, TWB = 16 * k2;
+    TileSpan sp;
     if (uv.shared) {
-        const int TWB = 16 * a.sh_k2;
-        TileSpan sp;
         sp.r = buffer_rsrc(a.sh_w[2], (uint32_t)(KT * ns * TWB));
         sp.off = ((nt0 >> 3) * KT * 8 + (nt0 & 7)) * TWB;
         sp.kstride = 8 * TWB;
-        ok = EA_K2_SWITCH(a.sh_k2, 2, 10, (down_product_i<SCB, K2V>(a, uv, sp, xs, acc)));
     } else {
-        const int k2 = uniform(a.k2t[2][uv.e]);
-        const uint32_t* T = uniform(reinterpret_cast<const uint32_t*>(a.ptr[2][uv.e]));
-        const int TWB = 16 * k2;
-        TileSpan sp;
-        sp.r = buffer_rsrc(T, (uint32_t)(KT * ns * TWB));
+        sp.r = buffer_rsrc(dn.ptr, (uint32_t)(KT * ns * TWB));
         sp.off = nt0 * TWB;
         sp.kstride = ns * TWB;
-        ok = EA_K2_SWITCH(k2, 2, 10, (down_product_i<CB, K2V>(a, uv, sp, xs, acc)));
     }
+    const bool ok = a.I == 256 ? down_product<CB, SCB, 16, FOLD>(a, uv, sp, k2, xs, gus, acc)
+                               : down_product<CB, SCB, 8, FOLD>(a, uv, sp, k2, xs, gus, acc);
     if (!ok && lane == 0) record_error(a.status, DEV_UNSUPPORTED_WIDTH);
 #pragma unroll
     for (int j = 0; j < 2; ++j)
 #pragma unroll
         for (int i = 0; i < 4; ++i) ys[(4 * (lane >> 4) + i) * 128 + (2 * wave + j) * 16 + (lane & 15)] = acc[j][i];
     __syncthreads();
-    // FWHT of each member's 128 columns, * HAD_SCALE * svh_d: the pair's y (or the shared expert's sy)
+    // FWHT of each member's 128 columns, * HAD_SCALE * svh_d
     const int n = cb * 128 + 2 * lane;
     for (int m = wave; m < uv.nm; m += DL_WAVES) {
         float v0 = ys[m * 128 + 2 * lane], v1 = ys[m * 128 + 2 * lane + 1];
@@ -591,6 +749,25 @@ down_kernel(DLArgs a) {
         float* dst = uv.shared ? a.lay.sy + (size_t)m * a.D : a.yroute + (size_t)member_q(a, uv, m) * a.D;
         *reinterpret_cast<float2*>(dst + n) = float2{v0 * HAD_SCALE * h2f(svh[n]), v1 * HAD_SCALE * h2f(svh[n + 1])};
     }
+}
+
+template <int CB, int SCB>
+__global__ void __launch_bounds__(DL_THREADS) __attribute__((amdgpu_waves_per_eu(4))) down_kernel(DLArgs a) {
+    __shared__ __attribute__((aligned(16))) uint16_t xs[DL_MAXR * DL_RS];
+    __shared__ __attribute__((aligned(16))) float ys[DL_MAXR * 128];
+    __shared__ int s_mem[DL_MAXR];
+    down_block<CB, SCB, false>(a, xs, ys, s_mem, nullptr);
+}
+
+// One row: the epilogue folded in (a unit has at most DL_SLOTS members; the grid covers few blocks, so two waves a
+// SIMD are enough and the partials and the trellis stay in registers together).
+template <int CB, int SCB>
+__global__ void __launch_bounds__(DL_THREADS) __attribute__((amdgpu_waves_per_eu(2))) down_fold_kernel(DLArgs a) {
+    __shared__ __attribute__((aligned(16))) uint16_t xs[DL_SLOTS * DL_RS];
+    __shared__ __attribute__((aligned(16))) float ys[DL_MAXR * 128];
+    __shared__ __attribute__((aligned(16))) float gus[DL_SLOTS * 2 * DL_MAXI];
+    __shared__ int s_mem[DL_MAXR];
+    down_block<CB, SCB, true>(a, xs, ys, s_mem, gus);
 }
 
 // ---- combine -------------------------------------------------------------------------------------------------------
@@ -647,7 +824,7 @@ static DLCarve dl_carve(uint32_t rows, uint32_t D, uint32_t I, uint32_t E) {
     c.zp = take(Q * c.NH * 2 * KC * 128 * 4);
     c.xd = take(Q * I * 2);
     c.sy = take((size_t)rows * D * 4);
-    c.ws = take(((size_t)DL_MAXP + 1 + (size_t)DL_MAXP * DL_MAXR + DL_MAXP) * 4);
+    c.ws = take((size_t)DL_MAXP * 8 + ((size_t)DL_MAXP + 1 + (size_t)DL_MAXP * DL_MAXR + 2 * DL_MAXP) * 4);
     c.total = off;
     return c;
 }
@@ -668,11 +845,13 @@ static DLLayout dl_layout(uint64_t base, uint32_t rows, uint32_t D, uint32_t I, 
     l.zp = dptr<float>(base + c.zp);
     l.xd = dptr<uint16_t>(base + c.xd);
     l.sy = dptr<float>(base + c.sy);
-    int* ws = dptr<int>(base + c.ws);
+    l.dptr = dptr<uint64_t>(base + c.ws);  // 256-byte aligned
+    int* ws = dptr<int>(base + c.ws + (size_t)DL_MAXP * 8);
     l.uids = ws;
     l.ucount = ws + DL_MAXP;
     l.members = l.ucount + 1;
     l.mcount = l.members + DL_MAXP * DL_MAXR;
+    l.dk2 = l.mcount + DL_MAXP;
     return l;
 }
 
@@ -713,11 +892,18 @@ static int dl_launch(hipStream_t s, const DLArgs& a, int cus, int device) {
     int r = launched();
     if (r) return r;
     mark_stage(s, device, 1);
-    epilogue_kernel<<<a.U * NH, DL_THREADS, 0, s>>>(a);
-    if ((r = launched())) return r;
-    mark_stage(s, device, 2);
-    down_kernel<CB, SCB><<<a.U * DB, DL_THREADS, 0, s>>>(a);
-    if ((r = launched())) return r;
+    if (a.R == 1) {
+        // one row: the down launch computes its own inputs (the epilogue stage is empty)
+        mark_stage(s, device, 2);
+        down_fold_kernel<CB, SCB><<<a.U * DB, DL_THREADS, 0, s>>>(a);
+        if ((r = launched())) return r;
+    } else {
+        epilogue_kernel<<<a.U * NH, DL_THREADS, 0, s>>>(a);
+        if ((r = launched())) return r;
+        mark_stage(s, device, 2);
+        down_kernel<CB, SCB><<<a.U * DB, DL_THREADS, 0, s>>>(a);
+        if ((r = launched())) return r;
+    }
     mark_stage(s, device, 3);
     combine_kernel<<<(a.R * DB + DL_WAVES - 1) / DL_WAVES, DL_THREADS, 0, s>>>(a);
     if ((r = launched())) return r;

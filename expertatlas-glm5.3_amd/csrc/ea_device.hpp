@@ -56,12 +56,11 @@ __device__ __forceinline__ void store_act(void* p, int dt, size_t i, float v) {
 
 // The path's exp: Cody & Waite reduction x = n ln2 + r, a degree-7 Taylor polynomial by Horner with fma, 2^n by
 // exponent scaling. Only IEEE fma / add / multiply / ldexp, so the CPU checker computes the same bits.
+// Straight-line code (the special cases are selects), so loads around a call are not serialized by its branches.
 __device__ __forceinline__ float expf_path(float x) {
-    if (x != x) return x;
-    if (x > 88.72283935546875f) return __builtin_inff();
-    if (x < -103.972084045410156f) return 0.0f;
-    const float n = __builtin_rintf(x * 1.44269502162933349609f);
-    float r = __builtin_fmaf(-n, 0.693145751953125f, x);
+    const float xc = __builtin_fminf(__builtin_fmaxf(x, -104.0f), 89.0f);  // keeps n in range; NaN -> -104
+    const float n = __builtin_rintf(xc * 1.44269502162933349609f);
+    float r = __builtin_fmaf(-n, 0.693145751953125f, xc);
     r = __builtin_fmaf(-n, 1.42860682030941723212e-06f, r);
     float p = 1.98412698412698412e-04f;
     p = __builtin_fmaf(p, r, 1.38888888888888889e-03f);
@@ -72,8 +71,11 @@ __device__ __forceinline__ float expf_path(float x) {
     p = __builtin_fmaf(p, r, 1.0f);
     p = __builtin_fmaf(p, r, 1.0f);
     const int ni = (int)n;
-    if (ni < -125) return __builtin_ldexpf(__builtin_ldexpf(p, ni + 64), -64);
-    return __builtin_ldexpf(p, ni);
+    const float lo = __builtin_ldexpf(__builtin_ldexpf(p, ni + 64), -64);  // results below 2^-125: two steps
+    float v = ni < -125 ? lo : __builtin_ldexpf(p, ni);
+    v = x < -103.972084045410156f ? 0.0f : v;
+    v = x > 88.72283935546875f ? __builtin_inff() : v;
+    return x != x ? x : v;
 }
 
 // ---- EXL3 trellis -------------------------------------------------------------------------------------------
@@ -198,17 +200,54 @@ __host__ __device__ constexpr int mfma_lane_p0(int lane) {
 // ---- Walsh-Hadamard over 128 values on a wavefront ------------------------------------------------------------
 // Lane j holds values 2j and 2j + 1. Levels run over index bits 0, 1, .., 6 in that order, each pair becoming
 // (lower + upper, lower - upper) in fp32: the reference's butterflies (decode.cuh:146-161), so the same bits.
+// The value of lane (l ^ M) in lane l, without the LDS crossbar: DPP within a row of 16 (xor 1 and 2 are quad
+// permutes, xor 4 = half-row mirror after quad reverse, xor 8 = row mirror after half-row mirror) and gfx950's
+// permlane swaps across rows (xor 16) and halves (xor 32).
+template <int M>
+__device__ __forceinline__ float lane_xor(float v) {
+    const int x = __builtin_bit_cast(int, v);
+    if constexpr (M == 1) {
+        return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(x, 0xB1, 0xf, 0xf, false));  // quad_perm 1,0,3,2
+    } else if constexpr (M == 2) {
+        return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(x, 0x4E, 0xf, 0xf, false));  // quad_perm 2,3,0,1
+    } else if constexpr (M == 4) {
+        const int r = __builtin_amdgcn_mov_dpp(x, 0x1B, 0xf, 0xf, false);                    // lane ^ 3
+        return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(r, 0x141, 0xf, 0xf, false));  // then ^ 7
+    } else if constexpr (M == 8) {
+        const int r = __builtin_amdgcn_mov_dpp(x, 0x141, 0xf, 0xf, false);                   // lane ^ 7
+        return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(r, 0x140, 0xf, 0xf, false));  // then ^ 15
+    } else if constexpr (M == 16) {
+        // swapping the odd rows of one copy with the even rows of another leaves row r's partner in the copy that
+        // did not keep row r
+        const auto p = __builtin_amdgcn_permlane16_swap((unsigned)x, (unsigned)x, false, false);
+        const bool odd_row = (__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u)) >> 4) & 1;
+        return __builtin_bit_cast(float, odd_row ? p[0] : p[1]);
+    } else {
+        static_assert(M == 32, "lane_xor: 1, 2, 4, 8, 16 or 32");
+        const auto p = __builtin_amdgcn_permlane32_swap((unsigned)x, (unsigned)x, false, false);
+        const bool upper = __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u)) >= 32;
+        return __builtin_bit_cast(float, upper ? p[0] : p[1]);
+    }
+}
+
+template <int M>
+__device__ __forceinline__ void fwht_level(float& v0, float& v1, int lane) {
+    const float o0 = lane_xor<M>(v0), o1 = lane_xor<M>(v1);
+    const bool up = lane & M;
+    v0 = up ? o0 - v0 : v0 + o0;
+    v1 = up ? o1 - v1 : v1 + o1;
+}
+
 __device__ __forceinline__ void fwht128_w64(float& v0, float& v1, int lane) {
     const float a = v0 + v1, b = v0 - v1;
     v0 = a;
     v1 = b;
-#pragma unroll
-    for (int m = 1; m < 64; m <<= 1) {
-        const float o0 = __shfl_xor(v0, m, 64), o1 = __shfl_xor(v1, m, 64);
-        const bool up = lane & m;
-        v0 = up ? o0 - v0 : v0 + o0;
-        v1 = up ? o1 - v1 : v1 + o1;
-    }
+    fwht_level<1>(v0, v1, lane);
+    fwht_level<2>(v0, v1, lane);
+    fwht_level<4>(v0, v1, lane);
+    fwht_level<8>(v0, v1, lane);
+    fwht_level<16>(v0, v1, lane);
+    fwht_level<32>(v0, v1, lane);
 }
 
 // 32-lane half-wave variant: lane j (0..31 within its half) holds values 4j .. 4j + 3.
