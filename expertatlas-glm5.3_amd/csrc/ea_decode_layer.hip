@@ -34,6 +34,8 @@ constexpr int DL_KT = 16;                    // k tiles of a gate|up item: 256 k
 constexpr int DL_MAXI = 256;                 // widest rank-local intermediate (I) the LDS layout holds
 constexpr int DL_RS = 264;                   // LDS row stride of the staged activations, halves
 constexpr int DL_MAXKC = 24;                 // k chunks of 256 (D up to 6144)
+constexpr int DL_MAXK2 = 10;                 // widest trellis (K2) the decode layer runs
+constexpr int DL_STAGE_WORDS = DL_KT * 2 * 4 * DL_MAXK2;  // a wave's staged trellis words: 16 rows of 2 tiles
 
 // Scratch of the four launches, carved on the host for the scratch's row capacity (any R up to it runs).
 struct DLLayout {
@@ -91,19 +93,27 @@ __device__ __forceinline__ float wave_max(float v) {
     return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
 }
 
-struct RouteSh {
+// The routing's working set, dead once the routing is published: the block's trellis staging reuses it.
+struct RouteScratch {
     int pick[DL_MAXP];
     float wts[DL_MAXP];
-    int unit[DL_MAXE];  // count of an expert's picks, then its routed unit (-1: not picked)
-    int uids[DL_MAXP];
-    int members[DL_MAXP][DL_MAXR];
-    int mcount[DL_MAXP];
+    int unit[DL_MAXE];  // count of an expert's picks
     int wsum[DL_WAVES];
+    uint64_t tptr[3][256];  // one row's path: every expert's addresses and widths, loaded with the logits
+    int tk2[3][256];
+};
+
+struct RouteSh {
+    int uids[DL_MAXP];
+    int16_t members[DL_MAXP][DL_MAXR];
+    int mcount[DL_MAXP];
     int ucount;
     uint64_t uptr[DL_MAXP][3];  // a routed unit's gate, up and down trellis addresses and widths
     int uk2[DL_MAXP][3];
-    uint64_t tptr[3][256];      // one row's path: every expert's addresses and widths, loaded with the logits
-    int tk2[3][256];
+    union {
+        RouteScratch r;
+        __attribute__((aligned(16))) uint32_t stage[DL_WAVES][DL_STAGE_WORDS];
+    };
 };
 
 // One row's top-8 on one wave (E = 256: expert q * 64 + lane in choice[q]): choice = sigmoid + bias, the larger
@@ -170,8 +180,8 @@ __device__ __forceinline__ void route_tables(const DLArgs& a, RouteSh& sh, int m
 }
 
 // The window's routing in LDS: picks (top-8 of the logits, or the given picks), the distinct picked experts in id
-// order and each one's pairs in ascending order (exl3_experts.cu:36-90), and the units' trellis tables (`mats`
-// matrices of each).
+// order and each one's first R pairs in ascending order (exl3_experts.cu:36-90), and the units' trellis tables
+// (`mats` matrices of each).
 __device__ __forceinline__ void route_block(const DLArgs& a, RouteSh& sh, int mats) {
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const int n = a.R * DL_SLOTS;
@@ -185,22 +195,22 @@ __device__ __forceinline__ void route_block(const DLArgs& a, RouteSh& sh, int ma
             tp[m] = (uint64_t)a.ptr[m][t];
             tk[m] = a.k2t[m][t];
         }
-        if (wave == 0) topk8_wave(a.logits, a.bias, a.scale, sh.pick, sh.wts, lane);
+        if (wave == 0) topk8_wave(a.logits, a.bias, a.scale, sh.r.pick, sh.r.wts, lane);
 #pragma unroll
         for (int m = 0; m < 3; ++m) {
-            sh.tptr[m][t] = tp[m];
-            sh.tk2[m][t] = tk[m];
+            sh.r.tptr[m][t] = tp[m];
+            sh.r.tk2[m][t] = tk[m];
         }
         __syncthreads();
         if (t < DL_SLOTS) {
-            const int e = sh.pick[t];
+            const int e = sh.r.pick[t];
             sh.uids[t] = e;
             sh.mcount[t] = 1;
             sh.members[t][0] = t;
 #pragma unroll
             for (int m = 0; m < 3; ++m) {
-                sh.uptr[t][m] = sh.tptr[m][e];
-                sh.uk2[t][m] = sh.tk2[m][e];
+                sh.uptr[t][m] = sh.r.tptr[m][e];
+                sh.uk2[t][m] = sh.r.tk2[m][e];
             }
         }
         if (t == 0) sh.ucount = DL_SLOTS;
@@ -209,19 +219,19 @@ __device__ __forceinline__ void route_block(const DLArgs& a, RouteSh& sh, int ma
     }
     if (a.logits) {
         for (int r = wave; r < a.R; r += DL_WAVES)
-            topk8_wave(a.logits + (size_t)r * 256, a.bias, a.scale, sh.pick + r * DL_SLOTS, sh.wts + r * DL_SLOTS,
+            topk8_wave(a.logits + (size_t)r * 256, a.bias, a.scale, sh.r.pick + r * DL_SLOTS, sh.r.wts + r * DL_SLOTS,
                        lane);
     } else {
         for (int i = t; i < n; i += DL_THREADS) {
-            sh.pick[i] = a.pick[i];
-            sh.wts[i] = a.wts[i];
+            sh.r.pick[i] = a.pick[i];
+            sh.r.wts[i] = a.wts[i];
         }
     }
-    for (int e = t; e < a.E; e += DL_THREADS) sh.unit[e] = 0;
+    for (int e = t; e < a.E; e += DL_THREADS) sh.r.unit[e] = 0;
     __syncthreads();
     for (int i = t; i < n; i += DL_THREADS) {
-        const int e = sh.pick[i];
-        if (e >= 0 && e < a.E) atomicAdd(&sh.unit[e], 1);
+        const int e = sh.r.pick[i];
+        if (e >= 0 && e < a.E) atomicAdd(&sh.r.unit[e], 1);
     }
     __syncthreads();
     // units in expert order: an exclusive scan of "picked" over experts 4t .. 4t + 3
@@ -229,7 +239,7 @@ __device__ __forceinline__ void route_block(const DLArgs& a, RouteSh& sh, int ma
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
         const int e = 4 * t + q;
-        used += (e < a.E && sh.unit[e] > 0) ? 1 : 0;
+        used += (e < a.E && sh.r.unit[e] > 0) ? 1 : 0;
     }
     int inc = used;
 #pragma unroll
@@ -237,49 +247,25 @@ __device__ __forceinline__ void route_block(const DLArgs& a, RouteSh& sh, int ma
         const int v = __shfl_up(inc, o, 64);
         if (lane >= o) inc += v;
     }
-    if (lane == 63) sh.wsum[wave] = inc;
+    if (lane == 63) sh.r.wsum[wave] = inc;
     __syncthreads();
     int place = inc - used;
-    for (int w = 0; w < wave; ++w) place += sh.wsum[w];
+    for (int w = 0; w < wave; ++w) place += sh.r.wsum[w];
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
         const int e = 4 * t + q;
-        if (e < a.E) {
-            if (sh.unit[e] > 0) {
-                sh.uids[place] = e;
-                sh.mcount[place] = 0;
-                sh.unit[e] = place++;
-            } else {
-                sh.unit[e] = -1;
-            }
-        }
+        if (e < a.E && sh.r.unit[e] > 0) sh.uids[place++] = e;
     }
     if (t == DL_THREADS - 1) sh.ucount = place;
     __syncthreads();
-    for (int i = t; i < n; i += DL_THREADS) {
-        const int e = sh.pick[i];
-        if (e < 0 || e >= a.E) continue;
-        const int u = sh.unit[e];
-        const int slot = atomicAdd(&sh.mcount[u], 1);
-        if (slot < DL_MAXR) sh.members[u][slot] = i;
-    }
-    __syncthreads();
+    // a unit's members: its first R pairs in pair order (exl3_experts.cu:83-86 with maxm = R, moe.zig:288); a pair
+    // past them keeps its y as it is, as a slot without an expert does
     for (int u = t; u < sh.ucount; u += DL_THREADS) {
-        int c = sh.mcount[u];
-        if (c > DL_MAXR) {  // one expert named by more pairs than a unit holds (repeated picks in rows)
-            record_error(a.status, EA_TOO_MANY_SLOTS);
-            c = DL_MAXR;
-        }
+        const int e = sh.uids[u];
+        int c = 0;
+        for (int i = 0; i < n && c < a.R; ++i)
+            if (sh.r.pick[i] == e) sh.members[u][c++] = (int16_t)i;
         sh.mcount[u] = c;
-        for (int i = 1; i < c; ++i) {  // ascending pair ids: row order, then slot order
-            const int v = sh.members[u][i];
-            int j = i - 1;
-            while (j >= 0 && sh.members[u][j] > v) {
-                sh.members[u][j + 1] = sh.members[u][j];
-                --j;
-            }
-            sh.members[u][j + 1] = v;
-        }
     }
     __syncthreads();
     route_tables(a, sh, mats);
@@ -292,8 +278,8 @@ __device__ __forceinline__ void route_publish(const DLArgs& a, const RouteSh& sh
     const DLLayout& l = a.lay;
     if (a.logits)
         for (int i = t; i < n; i += DL_THREADS) {
-            a.pick[i] = sh.pick[i];
-            a.wts[i] = sh.wts[i];
+            a.pick[i] = sh.r.pick[i];
+            a.wts[i] = sh.r.wts[i];
         }
     for (int u = t; u < sh.ucount; u += DL_THREADS) {
         l.uids[u] = sh.uids[u];
@@ -306,41 +292,6 @@ __device__ __forceinline__ void route_publish(const DLArgs& a, const RouteSh& sh
 }
 
 // ---- the MFMA core of an item ------------------------------------------------------------------------------------
-
-// The wave's two column tiles times the activation rows in xs over NKT k tiles: acc[j] += A (rows of xs, the MFMA's
-// 16 rows) x B (tile pair (t, t + 1) of column tile j). Each pair decodes right before its MFMA, so the decoded values
-// never all live at once.
-template <int CB, int K2, int NKT>
-__device__ __forceinline__ void mfma_tiles(const uint32_t (&w)[2][NKT][2], int sh, const uint16_t* xs, int nm,
-                                           int lane, f4v (&acc)[2]) {
-    const int m = lane & 15, g = (lane >> 4) & 3;
-    const bool live = m < nm;
-    const uint16_t* xr = xs + m * DL_RS + 2 * g;
-#pragma unroll
-    for (int t = 0; t < NKT; t += 2) {
-        h8v a = {0, 0, 0, 0, 0, 0, 0, 0};
-        if (live) {
-            const uint16_t* xk = xr + t * 16;
-            const u4v au = {*reinterpret_cast<const uint32_t*>(xk), *reinterpret_cast<const uint32_t*>(xk + 8),
-                            *reinterpret_cast<const uint32_t*>(xk + 16), *reinterpret_cast<const uint32_t*>(xk + 24)};
-            a = __builtin_bit_cast(h8v, au);
-        }
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const u2v b0 = decode_quad<K2, CB>(w[j][t][0], w[j][t][1], sh);
-            const u2v b1 = decode_quad<K2, CB>(w[j][t + 1][0], w[j][t + 1][1], sh);
-            const h8v bb = __builtin_bit_cast(h8v, (u4v{b0.x, b0.y, b1.x, b1.y}));
-            acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bb, acc[j], 0, 0, 0);
-        }
-    }
-}
-
-// The same product for a run-time width in 2..10 (false for any other): only this loop is specialised per width.
-template <int CB, int NKT>
-__device__ __forceinline__ bool mfma_tiles_k2(int k2, const uint32_t (&w)[2][NKT][2], int sh, const uint16_t* xs,
-                                              int nm, int lane, f4v (&acc)[2]) {
-    return EA_K2_SWITCH(k2, 2, 10, (mfma_tiles<CB, K2V, NKT>(w, sh, xs, nm, lane, acc)));
-}
 
 // Where an item's tiles are: a buffer over the whole matrix, the byte offset of tile (0, 0) and the byte stride between
 // k tiles; tile (t, j) sits at off + t * kstride + j * 16 K2 bytes (j: the wave's two column tiles, adjacent).
@@ -363,19 +314,82 @@ __device__ __forceinline__ LaneQuad lane_quad(int k2, int lane) {
     return r;
 }
 
-// This lane's words of tiles (t, j), t in [0, NKT), j in {0, 1} (tiles of `tile_bytes`), all issued before any is
-// used.
+// A wave's trellis of an item: the NKT rows of its two column tiles (2 * 16 K2 contiguous bytes a row) read with
+// 16-byte loads, ceil(NKT * K2 / 32) a wave; lane l of load i carries chunk 64 i + l (row c / (2 K2), 16-byte column
+// c % (2 K2)). Wide loads keep fewer requests in flight for the same bytes than a word a lane a tile.
 template <int NKT>
-__device__ __forceinline__ void fetch_tiles(const TileSpan& sp, int tile_bytes, const LaneQuad& lq,
-                                            uint32_t (&w)[2][NKT][2]) {
+constexpr int stage_loads() {
+    return (NKT * 2 * DL_MAXK2 + 63) / 64;
+}
+
+template <int NKT>
+__device__ __forceinline__ void stage_issue(const TileSpan& sp, int k2, int lane, u4v (&v)[stage_loads<NKT>()]) {
+    // a width outside 2..10 stages nothing (its product reports the width): the region holds DL_MAXK2 rows
+    const bool fits = k2 >= 2 && k2 <= DL_MAXK2;
+    const int cpr = fits ? 2 * k2 : 1, chunks = fits ? NKT * cpr : 0;
+    const int inv = (65536 + cpr - 1) / cpr;  // c / cpr == (c * inv) >> 16 for every chunk c < 16 * 20
 #pragma unroll
-    for (int t = 0; t < NKT; ++t)
+    for (int i = 0; i < stage_loads<NKT>(); ++i) {
+        const int c = 64 * i + lane;
+        v[i] = u4v{0u, 0u, 0u, 0u};
+        if (c < chunks) {
+            const int t = (c * inv) >> 16, col = c - t * cpr;
+            v[i] = __builtin_bit_cast(u4v, __builtin_amdgcn_raw_buffer_load_b128(sp.r, t * sp.kstride + col * 16,
+                                                                                   sp.off, 0));
+        }
+    }
+}
+
+// The chunks into the wave's LDS region in order: tile (t, j) then starts at word (2 t + j) * 4 K2. Only the wave
+// itself reads its region, and a wave's LDS accesses complete in order, so no barrier follows.
+template <int NKT>
+__device__ __forceinline__ void stage_store(uint32_t* st, int k2, int lane, const u4v (&v)[stage_loads<NKT>()]) {
+    const int chunks = (k2 >= 2 && k2 <= DL_MAXK2) ? NKT * 2 * k2 : 0;
+#pragma unroll
+    for (int i = 0; i < stage_loads<NKT>(); ++i) {
+        const int c = 64 * i + lane;
+        if (c < chunks) *reinterpret_cast<u4v*>(st + 4 * c) = v[i];
+    }
+}
+
+// The wave's two column tiles times the activation rows in xs over NKT k tiles: acc[j] += A (rows of xs, the MFMA's
+// 16 rows) x B (tile pair (t, t + 1) of column tile j). The tiles' words are staged in LDS (st: tile (t, j) at word
+// (2 t + j) * 4 K2); each lane reads the two words its four values come from and decodes the pair right before its
+// MFMA.
+template <int CB, int K2, int NKT>
+__device__ __forceinline__ void mfma_tiles(const uint32_t* st, const LaneQuad& lq, const uint16_t* xs, int nm,
+                                           int lane, f4v (&acc)[2]) {
+    constexpr int TW = 4 * K2;
+    const uint32_t* wa = st + lq.w0;
+    const uint32_t* wb = st + lq.w1;
+    const int m = lane & 15, g = (lane >> 4) & 3;
+    const bool live = m < nm;
+    const uint16_t* xr = xs + m * DL_RS + 2 * g;
+#pragma unroll
+    for (int t = 0; t < NKT; t += 2) {
+        h8v a = {0, 0, 0, 0, 0, 0, 0, 0};
+        if (live) {
+            const uint16_t* xk = xr + t * 16;
+            const u4v au = {*reinterpret_cast<const uint32_t*>(xk), *reinterpret_cast<const uint32_t*>(xk + 8),
+                            *reinterpret_cast<const uint32_t*>(xk + 16), *reinterpret_cast<const uint32_t*>(xk + 24)};
+            a = __builtin_bit_cast(h8v, au);
+        }
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
-            const int soff = sp.off + t * sp.kstride + j * tile_bytes;
-            w[j][t][0] = __builtin_amdgcn_raw_buffer_load_b32(sp.r, 4 * lq.w0, soff, 0);
-            w[j][t][1] = __builtin_amdgcn_raw_buffer_load_b32(sp.r, 4 * lq.w1, soff, 0);
+            const int t0 = (2 * t + j) * TW, t1 = (2 * (t + 1) + j) * TW;
+            const u2v b0 = decode_quad<K2, CB>(wa[t0], wb[t0], lq.sh);
+            const u2v b1 = decode_quad<K2, CB>(wa[t1], wb[t1], lq.sh);
+            const h8v bb = __builtin_bit_cast(h8v, (u4v{b0.x, b0.y, b1.x, b1.y}));
+            acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bb, acc[j], 0, 0, 0);
         }
+    }
+}
+
+// The same product for a run-time width in 2..10 (false for any other): only this loop is specialised per width.
+template <int CB, int NKT>
+__device__ __forceinline__ bool mfma_tiles_k2(int k2, const uint32_t* st, const LaneQuad& lq, const uint16_t* xs,
+                                              int nm, int lane, f4v (&acc)[2]) {
+    return EA_K2_SWITCH(k2, 2, 10, (mfma_tiles<CB, K2V, NKT>(st, lq, xs, nm, lane, acc)));
 }
 
 // Wave-uniform values the compiler cannot prove uniform (a wave's index, what a block read from LDS or memory) moved
@@ -402,7 +416,7 @@ struct UnitView {
     bool shared;
     int nm;          // members (rows) of the unit
     int e;           // routed expert, -1 for the shared expert
-    const int* mem;  // routed members (pair ids)
+    const int16_t* mem;  // routed members (pair ids)
 };
 
 __device__ __forceinline__ int member_q(const DLArgs& a, const UnitView& uv, int m) {
@@ -414,12 +428,13 @@ __device__ __forceinline__ int member_row(const UnitView& uv, int m) { return uv
 // (xs[m][k] = fp16(((x * suh) @ H) * HAD_SCALE), a wave a (row, 128-block)), then the MFMAs.
 template <int CB>
 __device__ __forceinline__ bool gateup_product(const DLArgs& a, const UnitView& uv, const TileSpan& sp, int k2,
-                                               const uint16_t* suh, int c, uint16_t* xs, f4v (&acc)[2]) {
+                                               const uint16_t* suh, int c, uint16_t* xs, uint32_t* st,
+                                               f4v (&acc)[2]) {
     const int lane = opaque_lane(threadIdx.x & 63), wave = uniform((int)threadIdx.x >> 6);
     const LaneQuad lq = lane_quad(k2, lane);
     // activations and suh of this wave's (row, block) tasks, then the trellis: loads complete in order, so the
-    // rotation waits only for the first two while the trellis is in flight; the tiles decode pair by pair between the
-    // MFMAs
+    // rotation waits only for the first two while the trellis is in flight. The trellis goes to the wave's LDS region
+    // after the block barrier, so the barrier never waits for it.
     constexpr int MT = 2 * DL_MAXR / DL_WAVES;
     uint32_t xv[MT], sv[MT];
     const int ntask = 2 * uv.nm;
@@ -435,8 +450,8 @@ __device__ __forceinline__ bool gateup_product(const DLArgs& a, const UnitView& 
             sv[i] = *reinterpret_cast<const uint32_t*>(suh + k);
         }
     }
-    uint32_t w[2][DL_KT][2];
-    fetch_tiles<DL_KT>(sp, 16 * k2, lq, w);
+    u4v v[stage_loads<DL_KT>()];
+    stage_issue<DL_KT>(sp, k2, lane, v);
     const bool bf = a.x_dtype == BF16;
 #pragma unroll
     for (int i = 0; i < MT; ++i) {
@@ -454,7 +469,8 @@ __device__ __forceinline__ bool gateup_product(const DLArgs& a, const UnitView& 
         }
     }
     __syncthreads();
-    return mfma_tiles_k2<CB, DL_KT>(k2, w, lq.sh, xs, uv.nm, lane, acc);
+    stage_store<DL_KT>(st, k2, lane, v);
+    return mfma_tiles_k2<CB, DL_KT>(k2, st, lq, xs, uv.nm, lane, acc);
 }
 
 // The unit of block u as the later launches see it, from the grouping the gate|up launch published. Every field loads
@@ -464,7 +480,7 @@ struct UnitDown {
     const uint32_t* ptr;
     int k2;
 };
-__device__ __forceinline__ bool unit_from_layout(const DLArgs& a, int u, UnitView& uv, int* s_mem,
+__device__ __forceinline__ bool unit_from_layout(const DLArgs& a, int u, UnitView& uv, int16_t* s_mem,
                                                  UnitDown* down = nullptr) {
     const DLLayout& l = a.lay;
     const int ur = u > a.hs ? u - a.hs : 0;
@@ -549,7 +565,7 @@ __device__ __forceinline__ uint32_t act_pair(const DLArgs& a, const UnitView& uv
 
 // Block (unit, column block nh of 128): the unit's down inputs, a wave a member.
 __global__ void __launch_bounds__(DL_THREADS) epilogue_kernel(DLArgs a) {
-    __shared__ int s_mem[DL_MAXR];
+    __shared__ int16_t s_mem[DL_MAXR];
     const int NH = a.I / 128;
     const int unit = blockIdx.x / NH, nh = blockIdx.x % NH;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -570,7 +586,7 @@ __global__ void __launch_bounds__(DL_THREADS) epilogue_kernel(DLArgs a) {
 // Item (unit u, column block nh, matrix mat, k chunk c) of the shared expert (SHARED, codebook CB) or of a routed
 // unit.
 template <int CB, bool SHARED>
-__device__ __forceinline__ void gateup_item(const DLArgs& a, const RouteSh& sh, int u, int nh, int mat, int c,
+__device__ __forceinline__ void gateup_item(const DLArgs& a, RouteSh& sh, int u, int nh, int mat, int c,
                                             uint16_t* xs) {
     const int lane = threadIdx.x & 63, wave = uniform((int)threadIdx.x >> 6);
     const int KC = a.D / 256, NH = a.I / 128;
@@ -605,7 +621,7 @@ __device__ __forceinline__ void gateup_item(const DLArgs& a, const RouteSh& sh, 
         sp.kstride = ns * TWB;
         suh = (mat ? a.suh_u : a.suh_g) + (size_t)uv.e * a.D;
     }
-    const bool ok = gateup_product<CB>(a, uv, sp, k2, suh, c, xs, acc);
+    const bool ok = gateup_product<CB>(a, uv, sp, k2, suh, c, xs, sh.stage[wave], acc);
     if (!ok && lane == 0) record_error(a.status, DEV_UNSUPPORTED_WIDTH);
     // partial sums of this chunk: zp[q][nh][mat][c][128]
 #pragma unroll
@@ -659,15 +675,15 @@ gateup_kernel(DLArgs a) {
 // trellis. Loads complete in order, so the inputs never wait for the trellis.
 template <int CB, int SCB, int NKT, bool FOLD>
 __device__ __forceinline__ bool down_product(const DLArgs& a, const UnitView& uv, const TileSpan& sp, int k2,
-                                             uint16_t* xs, float* gus, f4v (&acc)[2]) {
+                                             uint16_t* xs, float* gus, uint32_t* st, f4v (&acc)[2]) {
     const int lane = opaque_lane(threadIdx.x & 63), wave = uniform((int)threadIdx.x >> 6);
     const LaneQuad lq = lane_quad(k2, lane);
-    uint32_t w[2][NKT][2];
+    u4v v[stage_loads<NKT>()];
     if constexpr (FOLD) {
         const int NH = a.I / 128, tasks = uv.nm * NH * 2;
         float2 zv[DL_MAXKC];
         if (wave < tasks) zp_load(a, member_q(a, uv, wave / (2 * NH)), (wave >> 1) % NH, wave & 1, lane, zv);
-        fetch_tiles<NKT>(sp, 16 * k2, lq, w);
+        stage_issue<NKT>(sp, k2, lane, v);
         for (int task = wave; task < tasks; task += DL_WAVES) {
             const int m = task / (2 * NH), nh = (task >> 1) % NH, mat = task & 1;
             if (task != wave) zp_load(a, member_q(a, uv, m), nh, mat, lane, zv);
@@ -693,7 +709,7 @@ __device__ __forceinline__ bool down_product(const DLArgs& a, const UnitView& uv
             if (m < uv.nm)
                 xv[i] = *reinterpret_cast<const uint32_t*>(a.lay.xd + (size_t)member_q(a, uv, m) * a.I + k);
         }
-        fetch_tiles<NKT>(sp, 16 * k2, lq, w);
+        stage_issue<NKT>(sp, k2, lane, v);
 #pragma unroll
         for (int i = 0; i < MW; ++i) {
             const int idx = threadIdx.x + DL_THREADS * i;
@@ -702,14 +718,23 @@ __device__ __forceinline__ bool down_product(const DLArgs& a, const UnitView& uv
         }
     }
     __syncthreads();
-    return uv.shared ? mfma_tiles_k2<SCB, NKT>(k2, w, lq.sh, xs, uv.nm, lane, acc)
-                     : mfma_tiles_k2<CB, NKT>(k2, w, lq.sh, xs, uv.nm, lane, acc);
+    stage_store<NKT>(st, k2, lane, v);
+    return uv.shared ? mfma_tiles_k2<SCB, NKT>(k2, st, lq, xs, uv.nm, lane, acc)
+                     : mfma_tiles_k2<CB, NKT>(k2, st, lq, xs, uv.nm, lane, acc);
 }
+
+// The down launches' LDS besides the staged activations: the folded epilogue's gate and up values, the trellis staging
+// and the product's column sums are live one after another, so they share one region.
+union DownSh {
+    float gus[DL_SLOTS * 2 * DL_MAXI];
+    __attribute__((aligned(16))) uint32_t stage[DL_WAVES][DL_STAGE_WORDS];
+    float ys[DL_MAXR * 128];
+};
 
 // Block (unit, column block of 128 outputs): the members' down products, FWHT, svh -> the pair's y (or the shared
 // expert's sy).
 template <int CB, int SCB, bool FOLD>
-__device__ __forceinline__ void down_block(const DLArgs& a, uint16_t* xs, float* ys, int* s_mem, float* gus) {
+__device__ __forceinline__ void down_block(const DLArgs& a, uint16_t* xs, DownSh& ds, int16_t* s_mem) {
     const int DB = a.D / 128;
     const int u = blockIdx.x / DB, cb = blockIdx.x % DB;
     const int lane = threadIdx.x & 63, wave = uniform((int)threadIdx.x >> 6);
@@ -732,9 +757,11 @@ __device__ __forceinline__ void down_block(const DLArgs& a, uint16_t* xs, float*
         sp.off = nt0 * TWB;
         sp.kstride = ns * TWB;
     }
-    const bool ok = a.I == 256 ? down_product<CB, SCB, 16, FOLD>(a, uv, sp, k2, xs, gus, acc)
-                               : down_product<CB, SCB, 8, FOLD>(a, uv, sp, k2, xs, gus, acc);
+    const bool ok = a.I == 256 ? down_product<CB, SCB, 16, FOLD>(a, uv, sp, k2, xs, ds.gus, ds.stage[wave], acc)
+                               : down_product<CB, SCB, 8, FOLD>(a, uv, sp, k2, xs, ds.gus, ds.stage[wave], acc);
     if (!ok && lane == 0) record_error(a.status, DEV_UNSUPPORTED_WIDTH);
+    __syncthreads();  // the column sums overwrite the other waves' staging
+    float* ys = ds.ys;
 #pragma unroll
     for (int j = 0; j < 2; ++j)
 #pragma unroll
@@ -754,9 +781,9 @@ __device__ __forceinline__ void down_block(const DLArgs& a, uint16_t* xs, float*
 template <int CB, int SCB>
 __global__ void __launch_bounds__(DL_THREADS) __attribute__((amdgpu_waves_per_eu(4))) down_kernel(DLArgs a) {
     __shared__ __attribute__((aligned(16))) uint16_t xs[DL_MAXR * DL_RS];
-    __shared__ __attribute__((aligned(16))) float ys[DL_MAXR * 128];
-    __shared__ int s_mem[DL_MAXR];
-    down_block<CB, SCB, false>(a, xs, ys, s_mem, nullptr);
+    __shared__ DownSh ds;
+    __shared__ int16_t s_mem[DL_MAXR];
+    down_block<CB, SCB, false>(a, xs, ds, s_mem);
 }
 
 // One row: the epilogue folded in (a unit has at most DL_SLOTS members; the grid covers few blocks, so two waves a
@@ -764,10 +791,9 @@ __global__ void __launch_bounds__(DL_THREADS) __attribute__((amdgpu_waves_per_eu
 template <int CB, int SCB>
 __global__ void __launch_bounds__(DL_THREADS) __attribute__((amdgpu_waves_per_eu(2))) down_fold_kernel(DLArgs a) {
     __shared__ __attribute__((aligned(16))) uint16_t xs[DL_SLOTS * DL_RS];
-    __shared__ __attribute__((aligned(16))) float ys[DL_MAXR * 128];
-    __shared__ __attribute__((aligned(16))) float gus[DL_SLOTS * 2 * DL_MAXI];
-    __shared__ int s_mem[DL_MAXR];
-    down_block<CB, SCB, true>(a, xs, ys, s_mem, gus);
+    __shared__ DownSh ds;
+    __shared__ int16_t s_mem[DL_MAXR];
+    down_block<CB, SCB, true>(a, xs, ds, s_mem);
 }
 
 // ---- combine -------------------------------------------------------------------------------------------------------
@@ -868,7 +894,7 @@ static DLProfile* profile_of(int device) { return device >= 0 && device < 64 ? &
 static void mark_stage(hipStream_t s, int device, int k) {
     DLProfile* p = profile_of(device);
     if (p && p->on) {
-        hipEventRecord(p->ev[k], s);
+        (void)hipEventRecord(p->ev[k], s);
         if (k == DL_STAGES) p->recorded = true;
     }
 }

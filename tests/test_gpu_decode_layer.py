@@ -143,3 +143,43 @@ def test_moe_routed_fused_matches_sequence(ea):
         assert device.device_status() == 0
         assert_close_rms(outs[-1], want, 2e-3, f"moe.routed cap={cap}")
     assert_close_rms(outs[0], outs[1], 2e-3, "fused vs sequence")
+
+
+def test_ffn_decode_one_row_routed_only_i128(ea):
+    """One row (the down launch computes its own SwiGLU inputs from the gate|up partials) with no shared expert,
+    I = 128 and bf16 activations."""
+    _case(ea, [1, 1], 2048, 128, 8, 1, None, None, 1, 600)
+
+
+@pytest.mark.parametrize("repeat,mixed", [(False, False), (True, False), (False, True), (True, True)])
+def test_moe_routed_one_row_given_picks(ea, repeat, mixed):
+    """One row with caller-given picks; with `mixed` one picked expert is 3-bit beside 4-bit ones. With `repeat` the
+    picks name one expert three times: like the reference's grouping (exl3_experts.cu:83-86 with maxm = R,
+    moe.zig:288) a unit keeps its first R pairs, so slots 4 and 6 are not computed and read y as it is (zero in a new
+    scratch). The reference's combine reads its shared z scratch for such a slot instead, which then holds another
+    pair's gate|up partials, so the expected output is the oracle's with those two slots empty."""
+    device, linear, moe, synth = ea
+    R, E, D, I = 1, 64, 1024, 256
+    pick = synth.picks_uniform(700, R, E, 8)
+    if repeat:
+        pick[0, 4] = pick[0, 1]
+        pick[0, 6] = pick[0, 1]
+    wts = synth.routing_weights(701, R, 8)
+    k2 = np.full(E, 8, np.int32)
+    if mixed:
+        k2[pick[0, 2]] = 6
+    host = synth.HostLayer(702, experts=E, dims=D, width=I, k2=k2, only=np.unique(pick))
+    x = synth.activations(703, R, D, "f16")
+    computed = pick.copy()
+    if repeat:
+        computed[0, 4] = computed[0, 6] = -1
+    want = orc.moe_routed(x, computed, wts, oracle_routed(host), R, 8)
+    ex = moe.Routed(host)
+    sc = moe.Scratch(ex, 1, 8)
+    assert sc.c.fused != 0
+    dx, dp, dw = device.upload(x), device.upload(pick), device.upload(wts)
+    out = device.zeros((R, D), torch.float32)
+    moe.routed(device.stream(), dx.data_ptr(), D, dp.data_ptr(), dw.data_ptr(), ex, sc, out.data_ptr(), R, x_dtype=0)
+    got = device.download(out)
+    assert device.device_status() == 0
+    assert_close_rms(got, want, 2e-3, f"moe.routed R=1 repeat={repeat} mixed={mixed}")
