@@ -1,12 +1,12 @@
 """ctypes binding of libea_exl3.so (include/ea_exl3.h). Loading fails loudly when the library is missing: there
-is no fallback path."""
+is no fallback path. EA_EXL3_LIB names another build of the same library to load instead (for A/B timing)."""
 from __future__ import annotations
 
 import ctypes as C
 import os
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(_HERE, "libea_exl3.so")
+LIB_PATH = os.environ.get("EA_EXL3_LIB") or os.path.join(_HERE, "libea_exl3.so")
 
 U64, I64, U32, I32, F32, P = C.c_uint64, C.c_int64, C.c_uint32, C.c_int32, C.c_float, C.c_void_p
 MAX_JOBS = 3
