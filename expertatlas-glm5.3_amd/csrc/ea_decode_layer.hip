@@ -75,22 +75,32 @@ struct DLArgs {
 
 // ---- the router and the grouping, per block ------------------------------------------------------------------------
 
-// The largest value over the wavefront, in every lane: DPP within rows of 16 (quad swaps, rotations by 4 and 8),
-// then row broadcasts 15 and 31 leave the maximum in lane 63.
-template <int CTRL, int ROW_MASK>
-__device__ __forceinline__ float dpp_max(float x) {
-    const int xi = __builtin_bit_cast(int, x);
-    const int yi = __builtin_amdgcn_update_dpp(xi, xi, CTRL, ROW_MASK, 0xf, false);
-    return fmaxf(x, __builtin_bit_cast(float, yi));
+// An order-preserving integer key of a float: a larger float has a larger key, +0 and -0 share one, and NaN sits just
+// above 0, the key of a taken expert.
+__device__ __forceinline__ uint32_t order_key(float f) {
+    const uint32_t b = __builtin_bit_cast(uint32_t, f + 0.0f);
+    const uint32_t k = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+    return f != f ? 1u : k;
 }
-__device__ __forceinline__ float wave_max(float v) {
-    v = dpp_max<0xB1, 0xf>(v);   // quad_perm (1, 0, 3, 2)
-    v = dpp_max<0x4E, 0xf>(v);   // quad_perm (2, 3, 0, 1)
-    v = dpp_max<0x124, 0xf>(v);  // row_ror:4
-    v = dpp_max<0x128, 0xf>(v);  // row_ror:8
-    v = dpp_max<0x142, 0xa>(v);  // row_bcast:15 into rows 1, 3
-    v = dpp_max<0x143, 0xc>(v);  // row_bcast:31 into rows 2, 3
-    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+
+// The largest (MAX) or smallest key over the wavefront, in every lane: DPP within rows of 16 (quad swaps, rotations
+// by 4 and 8), then row broadcasts 15 and 31 leave the result in lane 63. Integer compares fold into the DPP moves.
+template <int CTRL, int ROW_MASK, bool MAX>
+__device__ __forceinline__ uint32_t dpp_step(uint32_t x) {
+    // lanes of a masked row read the identity, so the compare folds into one DPP instruction
+    constexpr int ID = MAX ? 0 : -1;
+    const uint32_t y = (uint32_t)__builtin_amdgcn_update_dpp(ID, (int)x, CTRL, ROW_MASK, 0xf, false);
+    return MAX ? (x > y ? x : y) : (x < y ? x : y);
+}
+template <bool MAX>
+__device__ __forceinline__ uint32_t wave_reduce(uint32_t v) {
+    v = dpp_step<0xB1, 0xf, MAX>(v);   // quad_perm (1, 0, 3, 2)
+    v = dpp_step<0x4E, 0xf, MAX>(v);   // quad_perm (2, 3, 0, 1)
+    v = dpp_step<0x124, 0xf, MAX>(v);  // row_ror:4
+    v = dpp_step<0x128, 0xf, MAX>(v);  // row_ror:8
+    v = dpp_step<0x142, 0xa, MAX>(v);  // row_bcast:15 into rows 1, 3
+    v = dpp_step<0x143, 0xc, MAX>(v);  // row_bcast:31 into rows 2, 3
+    return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
 }
 
 // The routing's working set, dead once the routing is published: the block's trellis staging reuses it.
@@ -118,7 +128,8 @@ struct RouteSh {
 
 // One row's top-8 on one wave (E = 256: expert q * 64 + lane in choice[q]): choice = sigmoid + bias, the larger
 // first, the lower id on a tie; wts = sigmoid / (sum of the picks' sigmoids in pick order + 1e-20) * scale
-// (native_ops.cu:1015-1068). A round: the wave maximum, then the lowest id holding it from four ballots.
+// (native_ops.cu:1015-1068). A round: the wave maximum of the choices' keys, then the lowest id holding it (a wave
+// minimum), with no branches and no scalar round trips beyond the two broadcasts.
 __device__ __forceinline__ void topk8_wave(const float* logits, const float* bias, float scale, int* pick, float* wts,
                                            int lane) {
     // all eight loads in flight before any is used
@@ -130,41 +141,41 @@ __device__ __forceinline__ void topk8_wave(const float* logits, const float* bia
     }
     asm volatile("" : "+v"(lg[0]), "+v"(lg[1]), "+v"(lg[2]), "+v"(lg[3]), "+v"(bs[0]), "+v"(bs[1]), "+v"(bs[2]),
                  "+v"(bs[3]));
-    float score[4], choice[4];
+    float score[4];
+    uint32_t key[4];
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
         score[q] = 1.0f / (expf_path(0.0f - lg[q]) + 1.0f);
-        choice[q] = score[q] + bs[q];
+        key[q] = order_key(score[q] + bs[q]);
     }
     float total = 0.0f, my_w = 0.0f;
     int my_p = 0;
     for (int k = 0; k < 8; ++k) {
-        const float m = wave_max(fmaxf(fmaxf(choice[0], choice[1]), fmaxf(choice[2], choice[3])));
-        const uint64_t b0 = __ballot(choice[0] == m), b1 = __ballot(choice[1] == m);
-        const uint64_t b2 = __ballot(choice[2] == m), b3 = __ballot(choice[3] == m);
-        const int q = b0 ? 0 : (b1 ? 1 : (b2 ? 2 : 3));
-        const uint64_t b = b0 ? b0 : (b1 ? b1 : (b2 ? b2 : b3));
-        const int src = __builtin_ctzll(b);
+        const uint32_t km = key[0] > key[1] ? key[0] : key[1], kn = key[2] > key[3] ? key[2] : key[3];
+        const uint32_t m = wave_reduce<true>(km > kn ? km : kn);
+        const uint32_t cand = key[0] == m   ? (uint32_t)lane
+                              : key[1] == m ? 64u + lane
+                              : key[2] == m ? 128u + lane
+                              : key[3] == m ? 192u + lane
+                                            : 0xffffu;
+        const int e = (int)wave_reduce<false>(cand);
+        const int src = e & 63, q = e >> 6;
         const float sq = q == 0 ? score[0] : (q == 1 ? score[1] : (q == 2 ? score[2] : score[3]));
         const float sw = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sq), src));
         total = total + sw;
-        if (lane == k) {
-            my_w = sw;
-            my_p = q * 64 + src;
-        }
-        if (lane == src) {
-            if (q == 0) choice[0] = -__builtin_inff();
-            if (q == 1) choice[1] = -__builtin_inff();
-            if (q == 2) choice[2] = -__builtin_inff();
-            if (q == 3) choice[3] = -__builtin_inff();
-        }
+        my_w = lane == k ? sw : my_w;
+        my_p = lane == k ? e : my_p;
+        const bool mine = lane == src;
+        key[0] = (mine && q == 0) ? 0u : key[0];
+        key[1] = (mine && q == 1) ? 0u : key[1];
+        key[2] = (mine && q == 2) ? 0u : key[2];
+        key[3] = (mine && q == 3) ? 0u : key[3];
     }
     if (lane < 8) {
         pick[lane] = my_p;
         wts[lane] = my_w / (total + 1e-20f) * scale;
     }
 }
-
 
 // The trellis addresses and widths of every routed unit, into LDS (one round trip for the block, instead of one an
 // item): gate and up, and down for the block that publishes them.
