@@ -129,9 +129,10 @@ struct RouteSh {
 // One row's top-8 on one wave (E = 256: expert q * 64 + lane in choice[q]): choice = sigmoid + bias, the larger
 // first, the lower id on a tie; wts = sigmoid / (sum of the picks' sigmoids in pick order + 1e-20) * scale
 // (native_ops.cu:1015-1068). A round: the wave maximum of the choices' keys, then the lowest id holding it (a wave
-// minimum), with no branches and no scalar round trips beyond the two broadcasts.
+// minimum), with no branches and no scalar round trips beyond the two broadcasts. `rounds` < 8 stops after the first
+// picks (wts are then not written: they need all eight).
 __device__ __forceinline__ void topk8_wave(const float* logits, const float* bias, float scale, int* pick, float* wts,
-                                           int lane) {
+                                           int lane, int rounds = DL_SLOTS) {
     // all eight loads in flight before any is used
     float lg[4], bs[4];
 #pragma unroll
@@ -150,7 +151,7 @@ __device__ __forceinline__ void topk8_wave(const float* logits, const float* bia
     }
     float total = 0.0f, my_w = 0.0f;
     int my_p = 0;
-    for (int k = 0; k < 8; ++k) {
+    for (int k = 0; k < rounds; ++k) {
         const uint32_t km = key[0] > key[1] ? key[0] : key[1], kn = key[2] > key[3] ? key[2] : key[3];
         const uint32_t m = wave_reduce<true>(km > kn ? km : kn);
         const uint32_t cand = key[0] == m   ? (uint32_t)lane
@@ -171,10 +172,8 @@ __device__ __forceinline__ void topk8_wave(const float* logits, const float* bia
         key[2] = (mine && q == 2) ? 0u : key[2];
         key[3] = (mine && q == 3) ? 0u : key[3];
     }
-    if (lane < 8) {
-        pick[lane] = my_p;
-        wts[lane] = my_w / (total + 1e-20f) * scale;
-    }
+    if (lane < rounds) pick[lane] = my_p;
+    if (rounds == DL_SLOTS && lane < DL_SLOTS) wts[lane] = my_w / (total + 1e-20f) * scale;
 }
 
 // The trellis addresses and widths of every routed unit, into LDS (one round trip for the block, instead of one an
@@ -192,8 +191,9 @@ __device__ __forceinline__ void route_tables(const DLArgs& a, RouteSh& sh, int m
 
 // The window's routing in LDS: picks (top-8 of the logits, or the given picks), the distinct picked experts in id
 // order and each one's first R pairs in ascending order (exl3_experts.cu:36-90), and the units' trellis tables
-// (`mats` matrices of each).
-__device__ __forceinline__ void route_block(const DLArgs& a, RouteSh& sh, int mats) {
+// (`mats` matrices of each). One row from logits: the units are the picks in order, and a block that runs only units
+// below `need` stops the top-8 there (its loads then start sooner).
+__device__ __forceinline__ void route_block(const DLArgs& a, RouteSh& sh, int mats, int need = DL_SLOTS) {
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const int n = a.R * DL_SLOTS;
     if (a.logits && a.R == 1) {
@@ -206,14 +206,14 @@ __device__ __forceinline__ void route_block(const DLArgs& a, RouteSh& sh, int ma
             tp[m] = (uint64_t)a.ptr[m][t];
             tk[m] = a.k2t[m][t];
         }
-        if (wave == 0) topk8_wave(a.logits, a.bias, a.scale, sh.r.pick, sh.r.wts, lane);
+        if (wave == 0) topk8_wave(a.logits, a.bias, a.scale, sh.r.pick, sh.r.wts, lane, need);
 #pragma unroll
         for (int m = 0; m < 3; ++m) {
             sh.r.tptr[m][t] = tp[m];
             sh.r.tk2[m][t] = tk[m];
         }
         __syncthreads();
-        if (t < DL_SLOTS) {
+        if (t < need) {
             const int e = sh.r.pick[t];
             sh.uids[t] = e;
             sh.mcount[t] = 1;
@@ -339,16 +339,25 @@ __device__ __forceinline__ void stage_issue(const TileSpan& sp, int k2, int lane
     const bool fits = k2 >= 2 && k2 <= DL_MAXK2;
     const int cpr = fits ? 2 * k2 : 1, chunks = fits ? NKT * cpr : 0;
     const int inv = (65536 + cpr - 1) / cpr;  // c / cpr == (c * inv) >> 16 for every chunk c < 16 * 20
+    // every load is issued (a lane past the last chunk reads the last one again), so no branch hides from the
+    // compiler how many loads are in flight
+    const int last = chunks > 0 ? chunks - 1 : 0;
 #pragma unroll
     for (int i = 0; i < stage_loads<NKT>(); ++i) {
-        const int c = 64 * i + lane;
-        v[i] = u4v{0u, 0u, 0u, 0u};
-        if (c < chunks) {
-            const int t = (c * inv) >> 16, col = c - t * cpr;
-            v[i] = __builtin_bit_cast(u4v, __builtin_amdgcn_raw_buffer_load_b128(sp.r, t * sp.kstride + col * 16,
-                                                                                   sp.off, 0));
-        }
+        const int c = min(64 * i + lane, last);
+        const int t = (c * inv) >> 16, col = c - t * cpr;
+        v[i] = __builtin_bit_cast(u4v, __builtin_amdgcn_raw_buffer_load_b128(sp.r, t * sp.kstride + col * 16, sp.off,
+                                                                               0));
     }
+}
+
+// Issue order: a compiler barrier after a batch of loads, then hold() on each earlier load's value. The values can
+// only be used after the holds, which follow every load of the batch; without them the scheduler may consume an
+// earlier load (and wait for it) before issuing the rest.
+__device__ __forceinline__ void issued() { asm volatile("" ::: "memory"); }
+template <typename T>
+__device__ __forceinline__ void hold(T& v) {
+    asm volatile("" : "+v"(v));
 }
 
 // The chunks into the wave's LDS region in order: tile (t, j) then starts at word (2 t + j) * 4 K2. Only the wave
@@ -364,9 +373,9 @@ __device__ __forceinline__ void stage_store(uint32_t* st, int k2, int lane, cons
 }
 
 // The wave's two column tiles times the activation rows in xs over NKT k tiles: acc[j] += A (rows of xs, the MFMA's
-// 16 rows) x B (tile pair (t, t + 1) of column tile j). The tiles' words are staged in LDS (st: tile (t, j) at word
-// (2 t + j) * 4 K2); each lane reads the two words its four values come from and decodes the pair right before its
-// MFMA.
+// 16 rows; rows past the unit's members hold zeros) x B (tile pair (t, t + 1) of column tile j). The tiles' words are
+// staged in LDS (st: tile (t, j) at word (2 t + j) * 4 K2); each lane reads the two words its four values come from
+// and decodes the pair right before its MFMA.
 template <int CB, int K2, int NKT>
 __device__ __forceinline__ void mfma_tiles(const uint32_t* st, const LaneQuad& lq, const uint16_t* xs, int nm,
                                            int lane, f4v (&acc)[2]) {
@@ -374,17 +383,13 @@ __device__ __forceinline__ void mfma_tiles(const uint32_t* st, const LaneQuad& l
     const uint32_t* wa = st + lq.w0;
     const uint32_t* wb = st + lq.w1;
     const int m = lane & 15, g = (lane >> 4) & 3;
-    const bool live = m < nm;
     const uint16_t* xr = xs + m * DL_RS + 2 * g;
 #pragma unroll
     for (int t = 0; t < NKT; t += 2) {
-        h8v a = {0, 0, 0, 0, 0, 0, 0, 0};
-        if (live) {
-            const uint16_t* xk = xr + t * 16;
-            const u4v au = {*reinterpret_cast<const uint32_t*>(xk), *reinterpret_cast<const uint32_t*>(xk + 8),
-                            *reinterpret_cast<const uint32_t*>(xk + 16), *reinterpret_cast<const uint32_t*>(xk + 24)};
-            a = __builtin_bit_cast(h8v, au);
-        }
+        const uint16_t* xk = xr + t * 16;
+        const u4v au = {*reinterpret_cast<const uint32_t*>(xk), *reinterpret_cast<const uint32_t*>(xk + 8),
+                        *reinterpret_cast<const uint32_t*>(xk + 16), *reinterpret_cast<const uint32_t*>(xk + 24)};
+        const h8v a = __builtin_bit_cast(h8v, au);
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
             const int t0 = (2 * t + j) * TW, t1 = (2 * (t + 1) + j) * TW;
@@ -421,6 +426,13 @@ __device__ __forceinline__ int opaque_lane(int lane) {
     return lane;
 }
 
+// Rows [from, to) of a staged-activation array (DL_RS halves a row) set to zero by the block.
+__device__ __forceinline__ void zero_rows(uint16_t* xs, int from, int to) {
+    uint32_t* w = reinterpret_cast<uint32_t*>(xs + from * DL_RS);
+    const int n = (to - from) * DL_RS / 2;
+    for (int i = threadIdx.x; i < n; i += DL_THREADS) w[i] = 0u;
+}
+
 // ---- gate | up ----------------------------------------------------------------------------------------------------
 
 struct UnitView {
@@ -451,18 +463,21 @@ __device__ __forceinline__ bool gateup_product(const DLArgs& a, const UnitView& 
     const int ntask = 2 * uv.nm;
 #pragma unroll
     for (int i = 0; i < MT; ++i) {
-        const int task = wave + DL_WAVES * i;
-        xv[i] = sv[i] = 0;
-        if (task < ntask) {
-            const int m = task >> 1, blk = task & 1;
-            const int k = c * 256 + blk * 128 + 2 * lane;
-            const uint16_t* xr = static_cast<const uint16_t*>(a.x) + (size_t)member_row(uv, m) * a.x_stride;
-            xv[i] = *reinterpret_cast<const uint32_t*>(xr + k);
-            sv[i] = *reinterpret_cast<const uint32_t*>(suh + k);
-        }
+        const int task = min(wave + DL_WAVES * i, ntask - 1);  // unconditional (see stage_issue); extra lanes repeat
+        const int m = task >> 1, blk = task & 1;
+        const int k = c * 256 + blk * 128 + 2 * lane;
+        const uint16_t* xr = static_cast<const uint16_t*>(a.x) + (size_t)member_row(uv, m) * a.x_stride;
+        xv[i] = *reinterpret_cast<const uint32_t*>(xr + k);
+        sv[i] = *reinterpret_cast<const uint32_t*>(suh + k);
     }
     u4v v[stage_loads<DL_KT>()];
     stage_issue<DL_KT>(sp, k2, lane, v);
+    issued();
+#pragma unroll
+    for (int i = 0; i < MT; ++i) {
+        hold(xv[i]);
+        hold(sv[i]);
+    }
     const bool bf = a.x_dtype == BF16;
 #pragma unroll
     for (int i = 0; i < MT; ++i) {
@@ -660,20 +675,32 @@ gateup_kernel(DLArgs a) {
     // starting with the launch; a block routes before its first routed item, and the block that runs the first
     // routed item publishes the routing
     const int first_routed = a.hs * per_unit;
+    zero_rows(xs, 0, DL_MAXR);  // the MFMAs read all 16 rows; an item writes its members' rows
+    __syncthreads();
+    int dirty = 0;              // rows an earlier item wrote
     int it = blockIdx.x;
     for (; it < items && it < first_routed; it += gridDim.x) {
         gateup_item<SCB, true>(a, sh, 0, it / (2 * KC), (it / KC) & 1, it % KC, xs);
+        dirty = a.R;
         __syncthreads();
     }
     if (it >= items) return;
     const bool publisher = it == first_routed;
-    route_block(a, sh, publisher ? 3 : 2);
+    int need = DL_SLOTS;  // one row: the picks up to the block's last unit (the publisher needs them all)
+    if (a.logits && a.R == 1 && !publisher) {
+        const int last = it + (items - 1 - it) / (int)gridDim.x * (int)gridDim.x;
+        need = min(DL_SLOTS, last / per_unit - a.hs + 1);
+    }
+    route_block(a, sh, publisher ? 3 : 2, need);
     if (publisher) route_publish(a, sh);
     const int units = a.hs + sh.ucount;
     for (; it < items; it += gridDim.x) {
         const int u = it / per_unit, rem = it % per_unit;
         if (u >= units) break;  // items run in unit order
+        const int nm = sh.mcount[u - a.hs];
+        if (nm < dirty) zero_rows(xs, nm, dirty);  // ordered before the reads by the item's rotation barrier
         gateup_item<CB, false>(a, sh, u, rem / (2 * KC), (rem / KC) & 1, rem % KC, xs);
+        dirty = nm;
         __syncthreads();
     }
 }
@@ -693,8 +720,12 @@ __device__ __forceinline__ bool down_product(const DLArgs& a, const UnitView& uv
     if constexpr (FOLD) {
         const int NH = a.I / 128, tasks = uv.nm * NH * 2;
         float2 zv[DL_MAXKC];
-        if (wave < tasks) zp_load(a, member_q(a, uv, wave / (2 * NH)), (wave >> 1) % NH, wave & 1, lane, zv);
+        const int t0 = min(wave, tasks - 1);  // unconditional (see stage_issue); a wave without a task repeats one
+        zp_load(a, member_q(a, uv, t0 / (2 * NH)), (t0 >> 1) % NH, t0 & 1, lane, zv);
         stage_issue<NKT>(sp, k2, lane, v);
+        issued();
+#pragma unroll
+        for (int cc = 0; cc < DL_MAXKC; ++cc) hold(zv[cc]);
         for (int task = wave; task < tasks; task += DL_WAVES) {
             const int m = task / (2 * NH), nh = (task >> 1) % NH, mat = task & 1;
             if (task != wave) zp_load(a, member_q(a, uv, m), nh, mat, lane, zv);
@@ -715,12 +746,13 @@ __device__ __forceinline__ bool down_product(const DLArgs& a, const UnitView& uv
 #pragma unroll
         for (int i = 0; i < MW; ++i) {
             const int idx = threadIdx.x + DL_THREADS * i;
-            const int m = idx / WPR, k = 2 * (idx % WPR);
-            xv[i] = 0;
-            if (m < uv.nm)
-                xv[i] = *reinterpret_cast<const uint32_t*>(a.lay.xd + (size_t)member_q(a, uv, m) * a.I + k);
+            const int m = min(idx / WPR, uv.nm - 1), k = 2 * (idx % WPR);  // unconditional (see stage_issue)
+            xv[i] = *reinterpret_cast<const uint32_t*>(a.lay.xd + (size_t)member_q(a, uv, m) * a.I + k);
         }
         stage_issue<NKT>(sp, k2, lane, v);
+        issued();
+#pragma unroll
+        for (int i = 0; i < MW; ++i) hold(xv[i]);
 #pragma unroll
         for (int i = 0; i < MW; ++i) {
             const int idx = threadIdx.x + DL_THREADS * i;
@@ -752,6 +784,7 @@ __device__ __forceinline__ void down_block(const DLArgs& a, uint16_t* xs, DownSh
     UnitView uv;
     UnitDown dn;
     if (!unit_from_layout(a, u, uv, s_mem, &dn)) return;
+    zero_rows(xs, uv.nm, DL_MAXR);  // the MFMAs read all 16 rows; ordered before them by the inputs' barrier
     __syncthreads();
     const int nt0 = cb * 8 + 2 * wave, KT = a.I / 16;
     f4v acc[2] = {f4v{0.f, 0.f, 0.f, 0.f}, f4v{0.f, 0.f, 0.f, 0.f}};
@@ -801,7 +834,7 @@ __global__ void __launch_bounds__(DL_THREADS) __attribute__((amdgpu_waves_per_eu
 // SIMD are enough and the partials and the trellis stay in registers together).
 template <int CB, int SCB>
 __global__ void __launch_bounds__(DL_THREADS) __attribute__((amdgpu_waves_per_eu(2))) down_fold_kernel(DLArgs a) {
-    __shared__ __attribute__((aligned(16))) uint16_t xs[DL_SLOTS * DL_RS];
+    __shared__ __attribute__((aligned(16))) uint16_t xs[DL_MAXR * DL_RS];
     __shared__ DownSh ds;
     __shared__ int16_t s_mem[DL_MAXR];
     down_block<CB, SCB, true>(a, xs, ds, s_mem);

@@ -105,9 +105,9 @@ __device__ __forceinline__ _Float16 cb_value(uint32_t s) {
 }
 
 // Two codebook values of two clean 16-bit states as a packed fp16 pair (the first in the low half): the same bits
-// as cb_value in 3.5 VALU instructions a value. mcg / 3inst: one multiply (and add) a state, two byte permutes
-// that pair the low halves and the high halves, one v_bitop3 a pair for (x & 0x8FFF8FFF) ^ 0x3B603B60 (truth table
-// 0x6A over (x, mask, pattern)), one packed fp16 add. mul1: multiply, byte sum by v_dot4, one packed fp16 fma.
+// as cb_value in 3 VALU instructions a value. mcg / 3inst: one multiply (and add) a state, one v_bitop3 a state for
+// (x & 0x8FFF8FFF) ^ 0x3B603B60 (truth table 0x6A over (x, mask, pattern)), one fp16 add of its two halves written
+// into its half of the result. mul1: multiply, byte sum by v_dot4, one packed fp16 fma.
 template <int CB>
 __device__ __forceinline__ uint32_t cb_pair(uint32_t s0, uint32_t s1) {
     if constexpr (CB == CB_MUL1) {
@@ -120,13 +120,18 @@ __device__ __forceinline__ uint32_t cb_pair(uint32_t s0, uint32_t s1) {
     } else {
         const uint32_t x0 = (CB == CB_MCG) ? s0 * 0xCBAC1FEDu : s0 * 89226354u + 64248484u;
         const uint32_t x1 = (CB == CB_MCG) ? s1 * 0xCBAC1FEDu : s1 * 89226354u + 64248484u;
-        // the mask and xor are the same in both halves, so pair the low halves and the high halves first: one
-        // bitop3 ((x & m) ^ c, table 0x6A) each, then one packed fp16 add gives both values
-        const uint32_t lo = __builtin_amdgcn_perm(x1, x0, 0x05040100u);  // (x0.lo, x1.lo)
-        const uint32_t hi = __builtin_amdgcn_perm(x1, x0, 0x07060302u);  // (x0.hi, x1.hi)
-        const h2v a = __builtin_bit_cast(h2v, __builtin_amdgcn_bitop3_b32(lo, 0x8FFF8FFFu, 0x3B603B60u, 0x6A));
-        const h2v b = __builtin_bit_cast(h2v, __builtin_amdgcn_bitop3_b32(hi, 0x8FFF8FFFu, 0x3B603B60u, 0x6A));
-        return __builtin_bit_cast(uint32_t, a + b);
+        // the mask and xor are the same in both halves: one bitop3 ((x & m) ^ c, table 0x6A) a state, then one fp16
+        // add of a word's two halves a value (SDWA selects the halves and the destination half)
+        const uint32_t a = __builtin_amdgcn_bitop3_b32(x0, 0x8FFF8FFFu, 0x3B603B60u, 0x6A);
+        const uint32_t b = __builtin_amdgcn_bitop3_b32(x1, 0x8FFF8FFFu, 0x3B603B60u, 0x6A);
+        uint32_t r;
+        asm("v_add_f16_sdwa %0, %1, %1 dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:WORD_0 src1_sel:WORD_1"
+            : "=v"(r)
+            : "v"(a));
+        asm("v_add_f16_sdwa %0, %1, %1 dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:WORD_0 src1_sel:WORD_1"
+            : "+v"(r)
+            : "v"(b));
+        return r;
     }
 }
 
