@@ -675,13 +675,14 @@ gateup_kernel(DLArgs a) {
     // starting with the launch; a block routes before its first routed item, and the block that runs the first
     // routed item publishes the routing
     const int first_routed = a.hs * per_unit;
-    zero_rows(xs, 0, DL_MAXR);  // the MFMAs read all 16 rows; an item writes its members' rows
-    __syncthreads();
-    int dirty = 0;              // rows an earlier item wrote
+    // the MFMAs read all 16 rows and an item writes its members' rows: rows from R on stay zero, rows below R are
+    // zeroed before an item with fewer members (every write is ordered before the reads by the item's rotation
+    // barrier, and no item writes the rows being zeroed)
+    zero_rows(xs, a.R, DL_MAXR);
+    int dirty = a.R;  // rows that may hold an earlier item's activations
     int it = blockIdx.x;
     for (; it < items && it < first_routed; it += gridDim.x) {
         gateup_item<SCB, true>(a, sh, 0, it / (2 * KC), (it / KC) & 1, it % KC, xs);
-        dirty = a.R;
         __syncthreads();
     }
     if (it >= items) return;
@@ -698,7 +699,7 @@ gateup_kernel(DLArgs a) {
         const int u = it / per_unit, rem = it % per_unit;
         if (u >= units) break;  // items run in unit order
         const int nm = sh.mcount[u - a.hs];
-        if (nm < dirty) zero_rows(xs, nm, dirty);  // ordered before the reads by the item's rotation barrier
+        if (nm < dirty) zero_rows(xs, nm, dirty);
         gateup_item<CB, false>(a, sh, u, rem / (2 * KC), (rem / KC) & 1, rem % KC, xs);
         dirty = nm;
         __syncthreads();
@@ -724,6 +725,7 @@ __device__ __forceinline__ bool down_product(const DLArgs& a, const UnitView& uv
         zp_load(a, member_q(a, uv, t0 / (2 * NH)), (t0 >> 1) % NH, t0 & 1, lane, zv);
         stage_issue<NKT>(sp, k2, lane, v);
         issued();
+        zero_rows(xs, uv.nm, DL_MAXR);  // the MFMAs read all 16 rows
 #pragma unroll
         for (int cc = 0; cc < DL_MAXKC; ++cc) hold(zv[cc]);
         for (int task = wave; task < tasks; task += DL_WAVES) {
@@ -751,6 +753,7 @@ __device__ __forceinline__ bool down_product(const DLArgs& a, const UnitView& uv
         }
         stage_issue<NKT>(sp, k2, lane, v);
         issued();
+        zero_rows(xs, uv.nm, DL_MAXR);  // the MFMAs read all 16 rows
 #pragma unroll
         for (int i = 0; i < MW; ++i) hold(xv[i]);
 #pragma unroll
@@ -784,7 +787,6 @@ __device__ __forceinline__ void down_block(const DLArgs& a, uint16_t* xs, DownSh
     UnitView uv;
     UnitDown dn;
     if (!unit_from_layout(a, u, uv, s_mem, &dn)) return;
-    zero_rows(xs, uv.nm, DL_MAXR);  // the MFMAs read all 16 rows; ordered before them by the inputs' barrier
     __syncthreads();
     const int nt0 = cb * 8 + 2 * wave, KT = a.I / 16;
     f4v acc[2] = {f4v{0.f, 0.f, 0.f, 0.f}, f4v{0.f, 0.f, 0.f, 0.f}};
