@@ -6,7 +6,7 @@
 A step is one pass of the hot path over one batch of synthetic input, with every input already in HBM:
   decode (default): one GLM-5.3 MoE layer of a TP=8 rank at batch 1 -- router top-8 from logits,
       the routed experts (moe.routed), the shared expert (EXL3 linears + SwiGLU) and their sum: ea_ffn_moe_decode,
-      four launches (gate|up, epilogue, down, combine);
+      three launches at one row (gate|up, down with the SwiGLU epilogue, combine), four above;
   multi (config 3): the same layer at 16 rows, uniform top-8, 70 % of the experts at 3 bits;
   stack (config 5): 75 resident layers (3-bit for 70 % of the experts), one token through all of them (us / token);
   linear (config 1): one 4-bit EXL3 linear 6144 x 2048 at one row (linear.call);
@@ -16,7 +16,8 @@ touched experts are not sitting in the 256 MB Infinity Cache. Prints one JSON li
 
 The dominant kernel's roofline is measured live: HIP events around each of its launches (on the stream the launches
 go to) over a second pass identical to the timed one; its algorithmic bytes per launch are the trellis + scales of
-every distinct expert the launch touches, the shared expert, the activations, logits and outputs.
+every distinct expert the launch touches, the shared expert, the activations, logits and outputs. Its HBM traffic
+a launch comes from the committed rocprofv3 counter summary (profiles/gateup_kernel_config2_traffic.md).
 """
 from __future__ import annotations
 
@@ -134,7 +135,7 @@ class DecodeBench:
             self.launch(i * self.per_step + q)
 
     def step_events(self, i: int, ev: list) -> None:
-        """Step i again, timing its launches: the fused path's four launches from the library's stage events
+        """Step i again, timing its launches: the fused path's launches from the library's stage events
         (recorded on the launch stream), the sequence path's grouped launches from torch events on the same stream."""
         for q in range(self.per_step):
             j = i * self.per_step + q
@@ -339,6 +340,19 @@ def _line(args, value, unit, ms, config, roofline, cpu) -> dict:
             "cpu_baseline": cpu}
 
 
+def recorded_traffic() -> int | None:
+    """HBM bytes a launch of the gate|up kernel at config 2 from the committed rocprofv3 --pmc summary
+    (FETCH_SIZE + WRITE_SIZE, each scaled by the counter's reading for a plain copy of known size), or None."""
+    try:
+        with open(os.path.join(ROOT, "profiles", "gateup_kernel_config2_traffic.md")) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch ="):
+                    return int(line.split("=")[1])
+    except OSError:
+        pass
+    return None
+
+
 def run_decode(args, torch, np) -> dict:
     workload, R, mixed, per_step, unit = WORKLOADS[args.config]
     n_layers = 75 if args.config == "stack" else args.layers
@@ -391,6 +405,10 @@ def run_decode(args, torch, np) -> dict:
                 "bytes_per_launch": int(avg_b), "launches_timed": len(durs)}
     if stages:
         roofline["layer_stages"] = stages
+    if args.config == "decode" and args.path == "fused":
+        roofline["traffic"] = recorded_traffic()
+        if roofline["traffic"]:
+            roofline["traffic_source"] = "profiles/gateup_kernel_config2_traffic.md (rocprofv3 --pmc, copy-calibrated)"
     cpu = None if args.no_cpu_baseline else cpu_baseline_decode(args.seed, R, mixed, layers_per_unit=per_step,
                                                                 unit=unit)
     return _line(args, us, unit, ms, config, roofline, cpu)

@@ -123,7 +123,7 @@ typedef struct ea_routed {
 typedef struct ea_moe_scratch {
     uint64_t xg, xu, xd, z, y, ids, count, members;
     uint64_t sync;         /* reserved counters (zeroed by ea_moe_scratch_init) */
-    uint64_t fused;        /* the one-launch decode layer's region (rows <= 16), else 0; zeroed by init */
+    uint64_t fused;        /* the decode layer's region (rows <= 16), else 0; zeroed by init */
     uint32_t rows, slots;
 } ea_moe_scratch;
 
@@ -135,8 +135,10 @@ int ea_moe_scratch_init(ea_stream_t stream, ea_moe_scratch* s, void* base, size_
 
 /* out fp32 [R, D] = the R rows' routed experts weighted by wts. Replaces moe.routed (moe.zig:279-293).
  * x: [R, D] rows x_stride apart; pick int32 / wts fp32 [R, slots]. With a scratch of at most 16 rows, widths
- * 2..10, mcg or mul1 and I of 128 or 256, the layer is one persistent launch; otherwise the six-launch sequence of
- * moe.zig:279-293. */
+ * 2..10, mcg or mul1 and I of 128 or 256, the decode layer's launches (three at one row, four above); otherwise the
+ * six-launch sequence of moe.zig:279-293. As the reference groups pairs (maxm = R), an expert computes its first R
+ * pairs in pair order; a slot past them (picks naming one expert more than R times) reads y as it is, as a slot
+ * without an expert does. */
 int ea_moe_routed(ea_stream_t stream, const void* x, int x_dtype, uint32_t x_stride, const int32_t* pick,
                   const float* wts, const ea_routed* ex, const ea_moe_scratch* s, float* out, uint32_t R);
 
@@ -219,9 +221,10 @@ int ea_swiglu2(ea_stream_t stream, const void* g, const void* u, void* out, uint
  * glue.cu:57). */
 int ea_add_f32(ea_stream_t stream, float* a, const float* b, size_t n);
 
-/* ---- the decode layer in one launch ------------------------------------------------------------------------- */
+/* ---- the decode layer in one call --------------------------------------------------------------------------- */
 
-/* ffnMain's expert part for a decode window in one launch: pick / wts [R, 8] = top-8 of logits [R, 256] (as
+/* ffnMain's expert part for a decode window in one call (three launches at one row, four above): pick / wts
+ * [R, 8] = top-8 of logits [R, 256] (as
  * ea_topk8, written out), out [R, D] = moe.routed(x) + the shared expert's mlp(x) (gate and up EXL3 linears with
  * bf16 outputs, swiglu2, the down linear with fp32 output), or the routed part alone when shared is NULL.
  * Replaces the sequence ops.topk -> moe.routed -> forward.mlp -> glue.addF32 of forward.zig:2361-2403 (the
@@ -235,11 +238,12 @@ int ea_ffn_moe_decode(ea_stream_t stream, const void* x, int x_dtype, uint32_t x
 
 /* ---- benchmark instrumentation (no counterpart in the reference) ------------------------------------------- */
 
-/* With on != 0, every call that runs the decode layer's four launches (ea_ffn_moe_decode, and ea_moe_routed when it
- * takes that path) records a HIP event on its stream before each launch (gate|up, epilogue, down, combine) and after
- * the last. For benchmarks; not under graph capture. */
+/* With on != 0, every call that runs the decode layer (ea_ffn_moe_decode, and ea_moe_routed when it takes that
+ * path) records a HIP event on its stream before each of its four stages (gate|up, epilogue, down, combine) and after
+ * the last; a stage run inside another launch (the epilogue and the combine with one row) is the time between two
+ * back-to-back events. For benchmarks; not under graph capture. */
 int ea_profile_enable(int on);
-/* ms[0..3]: the four launches of the most recent recorded call, in milliseconds (waits for that call); n >= 4.
+/* ms[0..3]: the four stages of the most recent recorded call, in milliseconds (waits for that call); n >= 4.
  * EA_INVALID when nothing was recorded since ea_profile_enable. */
 int ea_profile_stages(float* ms, uint32_t n);
 

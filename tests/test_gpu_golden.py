@@ -1,6 +1,6 @@
 """The HIP path against the committed golden fixtures (tests/golden/golden.npz): every tile decodes bit for bit, the
 top-8 matches bit for bit, and the reduced-width layers through ea_moe_routed (both its paths: a scratch of 16 rows
-takes the decode layer's four launches, one of 32 rows the six-launch sequence) stay within 2e-3 * RMS."""
+takes the decode layer's launches, one of 32 rows the six-launch sequence) stay within 2e-3 * RMS."""
 import os
 import sys
 
