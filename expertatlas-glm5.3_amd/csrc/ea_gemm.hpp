@@ -177,4 +177,76 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, 
             return false;                                \
         }
 
+// ---- trellis staging through LDS (the decode layer and the prefill GEMM) ------------------------------------
+
+constexpr int STAGE_MAXK2 = 10;  // widest trellis (K2) the staged paths decode: two words a lane a tile
+
+// Where an item's tiles are: a buffer over the whole matrix, the byte offset of tile (0, 0) and the byte stride between
+// k tiles; tile (t, j) sits at off + t * kstride + j * 16 K2 bytes (j: the wave's two column tiles, adjacent).
+struct TileSpan {
+    __amdgpu_buffer_rsrc_t r;
+    int off, kstride;
+};
+
+// The two words of a tile this lane's four values come from and their bit offset, for a width in 2..10 (zeros for
+// any other: the loads stay inside the buffer and the product then reports the width).
+struct LaneQuad {
+    int w0, w1, sh;
+};
+__device__ __forceinline__ LaneQuad lane_quad(int k2, int lane) {
+    LaneQuad r{0, 0, 0};
+    EA_K2_SWITCH(k2, 2, 10, ([&] {
+                     const Quad q = quad_of<K2V>(mfma_lane_p0(lane));
+                     r = LaneQuad{q.wa, q.wb, q.sh};
+                 }()));
+    return r;
+}
+
+// A wave's trellis of an item: the NKT rows of its two column tiles (2 * 16 K2 contiguous bytes a row) read with
+// 16-byte loads, ceil(NKT * K2 / 32) a wave; lane l of load i carries chunk 64 i + l (row c / (2 K2), 16-byte column
+// c % (2 K2)). Wide loads keep fewer requests in flight for the same bytes than a word a lane a tile.
+template <int NKT>
+constexpr int stage_loads() {
+    return (NKT * 2 * STAGE_MAXK2 + 63) / 64;
+}
+
+template <int NKT>
+__device__ __forceinline__ void stage_issue(const TileSpan& sp, int k2, int lane, u4v (&v)[stage_loads<NKT>()]) {
+    // a width outside 2..10 stages nothing (its product reports the width): the region holds STAGE_MAXK2 rows
+    const bool fits = k2 >= 2 && k2 <= STAGE_MAXK2;
+    const int cpr = fits ? 2 * k2 : 1, chunks = fits ? NKT * cpr : 0;
+    const int inv = (65536 + cpr - 1) / cpr;  // c / cpr == (c * inv) >> 16 for every chunk c < 16 * 20
+    // every load is issued (a lane past the last chunk reads the last one again), so no branch hides from the
+    // compiler how many loads are in flight
+    const int last = chunks > 0 ? chunks - 1 : 0;
+#pragma unroll
+    for (int i = 0; i < stage_loads<NKT>(); ++i) {
+        const int c = min(64 * i + lane, last);
+        const int t = (c * inv) >> 16, col = c - t * cpr;
+        v[i] = __builtin_bit_cast(u4v, __builtin_amdgcn_raw_buffer_load_b128(sp.r, t * sp.kstride + col * 16, sp.off,
+                                                                               0));
+    }
+}
+
+// Issue order: a compiler barrier after a batch of loads, then hold() on each earlier load's value. The values can
+// only be used after the holds, which follow every load of the batch; without them the scheduler may consume an
+// earlier load (and wait for it) before issuing the rest.
+__device__ __forceinline__ void issued() { asm volatile("" ::: "memory"); }
+template <typename T>
+__device__ __forceinline__ void hold(T& v) {
+    asm volatile("" : "+v"(v));
+}
+
+// The chunks into the wave's LDS region in order: tile (t, j) then starts at word (2 t + j) * 4 K2. Only the wave
+// itself reads its region, and a wave's LDS accesses complete in order, so no barrier follows.
+template <int NKT>
+__device__ __forceinline__ void stage_store(uint32_t* st, int k2, int lane, const u4v (&v)[stage_loads<NKT>()]) {
+    const int chunks = (k2 >= 2 && k2 <= STAGE_MAXK2) ? NKT * 2 * k2 : 0;
+#pragma unroll
+    for (int i = 0; i < stage_loads<NKT>(); ++i) {
+        const int c = 64 * i + lane;
+        if (c < chunks) *reinterpret_cast<u4v*>(st + 4 * c) = v[i];
+    }
+}
+
 }  // namespace ea

@@ -155,6 +155,243 @@ __global__ void __launch_bounds__(NW * 64) item_gemm_kernel(
         }
 }
 
+// ---- the staged item GEMM (widths 2..10) -------------------------------------------------------------------
+
+constexpr int PK = 8;                                      // k tiles a chunk: 128 k
+constexpr int PXS = PK * 16 + 8;                           // LDS row stride of a staged A chunk, halves (272 bytes)
+constexpr int PW = 4;                                      // waves a block: 8 column tiles, 128 columns
+constexpr int PSTAGE = PK * 2 * 4 * STAGE_MAXK2;           // a wave's staged trellis words a chunk
+constexpr int PA = IPM * PK * 16 * 2 / 16 / (PW * 64);     // 16-byte A pieces a thread a chunk
+static_assert(PA * PW * 64 * 16 == IPM * PK * 16 * 2, "the block's threads cover an A chunk exactly");
+
+// One chunk (PK k tiles) of a wave: its two column tiles times the item's first mts row tiles. The trellis words
+// are staged in st (tile (t, j) at word (2 t + j) * 4 K2), the activations in xa (row stride xs halves); each tile
+// pair decodes once and feeds all row tiles.
+template <int CB, int K2>
+__device__ __forceinline__ void item_chunk(const uint32_t* st, const LaneQuad& lq, const uint16_t* xa, int mts,
+                                           int lane, f4v (&acc)[IPM_TILES][2], int xs = PXS) {
+    constexpr int TW = 4 * K2;
+    const uint32_t* wa = st + lq.w0;
+    const uint32_t* wb = st + lq.w1;
+    const uint16_t* xr = xa + (lane & 15) * xs + 2 * ((lane >> 4) & 3);
+#pragma unroll
+    for (int t = 0; t < PK; t += 2) {
+        h8v bb[2];
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int t0 = (2 * t + j) * TW, t1 = (2 * (t + 1) + j) * TW;
+            const u2v b0 = decode_quad<K2, CB>(wa[t0], wb[t0], lq.sh);
+            const u2v b1 = decode_quad<K2, CB>(wa[t1], wb[t1], lq.sh);
+            bb[j] = __builtin_bit_cast(h8v, (u4v{b0.x, b0.y, b1.x, b1.y}));
+        }
+#pragma unroll
+        for (int mt = 0; mt < IPM_TILES; ++mt) {
+            if (mt >= mts) break;  // the item's occupied row tiles only (uniform)
+            const uint16_t* xk = xr + mt * 16 * xs + t * 16;
+            const u4v au = {*reinterpret_cast<const uint32_t*>(xk), *reinterpret_cast<const uint32_t*>(xk + 8),
+                            *reinterpret_cast<const uint32_t*>(xk + 16), *reinterpret_cast<const uint32_t*>(xk + 24)};
+            const h8v a = __builtin_bit_cast(h8v, au);
+            acc[mt][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bb[0], acc[mt][0], 0, 0, 0);
+            acc[mt][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bb[1], acc[mt][1], 0, 0, 0);
+        }
+    }
+}
+
+// Block (item, 128 columns, matrix): the item's rows (up to IPM, IPM_TILES MFMA row tiles) times its expert's matrix
+// over all of K in chunks of 128. A chunk's activations go to LDS once for the block's four waves; each wave's two
+// column tiles of the chunk come in as 16-byte loads staged in the wave's own LDS region. The activations are loaded
+// one chunk ahead and the trellis two, while the current chunk decodes and multiplies; only the item's occupied row
+// tiles are loaded and multiplied. Rows past the item's count read the item's first pair and are not stored (MFMA
+// rows do not mix). Z[mat][pair][n] fp32.
+template <int CB>
+__global__ void __launch_bounds__(PW * 64) __attribute__((amdgpu_waves_per_eu(2)))
+item_gemm_staged_kernel(const uint16_t* __restrict__ X0, const uint16_t* __restrict__ X1,
+                        const int64_t* __restrict__ TP0, const int64_t* __restrict__ TP1,
+                        const int* __restrict__ K2_0, const int* __restrict__ K2_1, const int* __restrict__ sorted,
+                        const int* __restrict__ items, const int* __restrict__ item_count, float* __restrict__ Z,
+                        int K, int N, int P, int* __restrict__ status) {
+    const int item = blockIdx.x;
+    if (item >= item_count[0]) return;
+    const int e = items[3 * item], first = items[3 * item + 1], cnt = items[3 * item + 2];
+    const int mat = blockIdx.z;
+    const uint16_t* X = mat ? X1 : X0;
+    const uint32_t* T = reinterpret_cast<const uint32_t*>(mat ? TP1[e] : TP0[e]);
+    const int k2 = mat ? K2_1[e] : K2_0[e];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    __shared__ int pair_sh[IPM];
+    __shared__ __attribute__((aligned(16))) uint16_t xa[IPM * PXS];
+    __shared__ __attribute__((aligned(16))) uint32_t st[PW][PSTAGE];
+    if (tid < IPM) pair_sh[tid] = tid < cnt ? sorted[first + tid] : -1;
+    __syncthreads();
+    // this thread's pieces of every A chunk: piece i is row tile i (row 16 i + (tid >> 4)), halves 8 (tid & 15) .. +7
+    // of the chunk; a piece past the item's row tiles reads row tile 0's address (a cache hit) and is not stored
+    const int mts = (cnt + 15) >> 4;
+    uint32_t aoff[PA];
+    int lofs[PA];
+#pragma unroll
+    for (int i = 0; i < PA; ++i) {
+        const int idx = i * PW * 64 + tid, row = idx >> 4;
+        const int rr = i < mts ? row : (tid >> 4);
+        const int p = pair_sh[rr] >= 0 ? pair_sh[rr] : pair_sh[0];
+        aoff[i] = ((uint32_t)p * (uint32_t)K + 8u * (idx & 15)) * 2u;
+        lofs[i] = row * PXS + 8 * (idx & 15);
+    }
+    const __amdgpu_buffer_rsrc_t xrs = buffer_rsrc(X, (uint32_t)((size_t)P * K * 2));
+    const int nt0 = blockIdx.y * (2 * PW) + 2 * wave;
+    const int ns = N >> 4, TWB = 16 * k2;
+    TileSpan sp;
+    sp.r = buffer_rsrc(T, (uint32_t)((K >> 4) * ns * TWB));
+    sp.off = nt0 * TWB;
+    sp.kstride = ns * TWB;
+    const LaneQuad lq = lane_quad(k2, lane);
+    f4v acc[IPM_TILES][2];
+#pragma unroll
+    for (int mt = 0; mt < IPM_TILES; ++mt) acc[mt][0] = acc[mt][1] = f4v{0.f, 0.f, 0.f, 0.f};
+    const int nch = K / (PK * 16);
+    // loads complete in issue order; every load is issued (a chunk past the last re-reads the last), so the waits
+    // stay exact: the activations one chunk ahead, the trellis two
+    u4v av[PA], ta[stage_loads<PK>()], tb[stage_loads<PK>()];
+    auto issue_a = [&](int c) {
+        c = c < nch ? c : nch - 1;
+#pragma unroll
+        for (int i = 0; i < PA; ++i)
+            av[i] = __builtin_bit_cast(u4v, __builtin_amdgcn_raw_buffer_load_b128(xrs, aoff[i], c * PK * 32, 0));
+    };
+    auto issue_t = [&](int c, u4v (&tv)[stage_loads<PK>()]) {
+        c = c < nch ? c : nch - 1;
+        TileSpan sc = sp;
+        sc.off = sp.off + c * PK * sp.kstride;
+        stage_issue<PK>(sc, k2, lane, tv);
+    };
+    bool ok = true;
+    auto step = [&](int c, u4v (&tv)[stage_loads<PK>()]) {
+        __syncthreads();  // the previous chunk's reads of xa and of the wave's stage are done
+#pragma unroll
+        for (int i = 0; i < PA; ++i)
+            if (i < mts) *reinterpret_cast<u4v*>(xa + lofs[i]) = av[i];
+        stage_store<PK>(st[wave], k2, lane, tv);
+        issue_a(c + 1);
+        issue_t(c + 2, tv);
+        __syncthreads();  // the chunk's activations are in LDS
+        ok = EA_K2_SWITCH(k2, 2, 10, (item_chunk<CB, K2V>(st[wave], lq, xa, mts, lane, acc)));
+    };
+    issue_t(0, ta);
+    issue_t(1, tb);
+    issue_a(0);
+    for (int c = 0; c < nch; c += 2) {
+        step(c, ta);
+        if (c + 1 < nch) step(c + 1, tb);  // uniform
+    }
+    if (!ok) {
+        if (lane == 0) record_error(status, DEV_UNSUPPORTED_WIDTH);
+        return;
+    }
+    float* Zm = Z + (size_t)mat * P * N;
+#pragma unroll
+    for (int mt = 0; mt < IPM_TILES; ++mt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int p = pair_sh[mt * 16 + 4 * (lane >> 4) + i];
+            if (p < 0) continue;
+#pragma unroll
+            for (int j = 0; j < 2; ++j) Zm[(size_t)p * N + (nt0 + j) * 16 + (lane & 15)] = acc[mt][j][i];
+        }
+}
+
+// The down matrix (K = I of 128 or 256: one or two chunks): a block (item, DNG column blocks of 128) loads the item's
+// activations for all of K into LDS once, then runs its column blocks one after another, the trellis of each
+// (column block, chunk) step loaded two steps ahead, and stores each column block's rows when its last chunk is done.
+constexpr int DNG = 8;                        // column blocks a block
+constexpr int DXS = 2 * PK * 16 + 8;          // LDS row stride of the activations, halves (K up to 256)
+
+template <int CB>
+__global__ void __launch_bounds__(PW * 64) __attribute__((amdgpu_waves_per_eu(2)))
+item_down_staged_kernel(const uint16_t* __restrict__ X, const int64_t* __restrict__ TP, const int* __restrict__ K2T,
+                        const int* __restrict__ sorted, const int* __restrict__ items,
+                        const int* __restrict__ item_count, float* __restrict__ Z, int K, int N, int P,
+                        int* __restrict__ status) {
+    const int item = blockIdx.x;
+    if (item >= item_count[0]) return;
+    const int e = items[3 * item], first = items[3 * item + 1], cnt = items[3 * item + 2];
+    const uint32_t* T = reinterpret_cast<const uint32_t*>(TP[e]);
+    const int k2 = K2T[e];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    __shared__ int pair_sh[IPM];
+    __shared__ __attribute__((aligned(16))) uint16_t xa[IPM * DXS];
+    __shared__ __attribute__((aligned(16))) uint32_t st[PW][PSTAGE];
+    if (tid < IPM) pair_sh[tid] = tid < cnt ? sorted[first + tid] : -1;
+    __syncthreads();
+    const int mts = (cnt + 15) >> 4;
+    const int nch = K / (PK * 16);  // 1 or 2
+    // the activations: piece i of a chunk is row tile i (row 16 i + (tid >> 4)), halves 8 (tid & 15) .. +7
+    {
+        const __amdgpu_buffer_rsrc_t xrs = buffer_rsrc(X, (uint32_t)((size_t)P * K * 2));
+        for (int c = 0; c < nch; ++c) {
+            u4v av[PA];
+#pragma unroll
+            for (int i = 0; i < PA; ++i) {
+                const int row = i * 16 + (tid >> 4);
+                const int rr = i < mts ? row : (tid >> 4);
+                const int p = pair_sh[rr] >= 0 ? pair_sh[rr] : pair_sh[0];
+                av[i] = __builtin_bit_cast(
+                    u4v, __builtin_amdgcn_raw_buffer_load_b128(
+                             xrs, ((uint32_t)p * (uint32_t)K + (uint32_t)(c * PK * 16 + 8 * (tid & 15))) * 2u, 0, 0));
+            }
+#pragma unroll
+            for (int i = 0; i < PA; ++i)
+                if (i < mts)
+                    *reinterpret_cast<u4v*>(xa + (i * 16 + (tid >> 4)) * DXS + c * PK * 16 + 8 * (tid & 15)) = av[i];
+        }
+    }
+    const int ns = N >> 4, TWB = 16 * k2;
+    const int nb0 = blockIdx.y * DNG;  // first column block
+    TileSpan sp;
+    sp.r = buffer_rsrc(T, (uint32_t)((K >> 4) * ns * TWB));
+    sp.off = (nb0 * 8 + 2 * wave) * TWB;
+    sp.kstride = ns * TWB;
+    const LaneQuad lq = lane_quad(k2, lane);
+    const int steps = DNG * nch;
+    u4v ta[stage_loads<PK>()], tb[stage_loads<PK>()];
+    auto issue_t = [&](int s2, u4v (&tv)[stage_loads<PK>()]) {  // step s2: column block s2 / nch, chunk s2 % nch
+        s2 = s2 < steps ? s2 : steps - 1;
+        TileSpan sc = sp;
+        sc.off = sp.off + (s2 / nch) * 8 * TWB + (s2 % nch) * PK * sp.kstride;
+        stage_issue<PK>(sc, k2, lane, tv);
+    };
+    f4v acc[IPM_TILES][2];
+    bool ok = true;
+    auto step = [&](int s2, u4v (&tv)[stage_loads<PK>()]) {
+        const int c = s2 % nch;
+        if (c == 0) {
+#pragma unroll
+            for (int mt = 0; mt < IPM_TILES; ++mt) acc[mt][0] = acc[mt][1] = f4v{0.f, 0.f, 0.f, 0.f};
+        }
+        stage_store<PK>(st[wave], k2, lane, tv);  // only this wave reads its region, in order
+        issue_t(s2 + 2, tv);
+        __syncthreads();  // the activations are in LDS (the first step); keeps the waves together
+        ok = EA_K2_SWITCH(k2, 2, 10, (item_chunk<CB, K2V>(st[wave], lq, xa + c * PK * 16, mts, lane, acc, DXS)));
+        if (c == nch - 1 && ok) {
+            const int nt0 = (nb0 + s2 / nch) * 8 + 2 * wave;
+#pragma unroll
+            for (int mt = 0; mt < IPM_TILES; ++mt)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int p = pair_sh[mt * 16 + 4 * (lane >> 4) + i];
+                    if (p < 0) continue;
+#pragma unroll
+                    for (int j = 0; j < 2; ++j) Z[(size_t)p * N + (nt0 + j) * 16 + (lane & 15)] = acc[mt][j][i];
+                }
+        }
+    };
+    issue_t(0, ta);
+    issue_t(1, tb);
+    for (int s2 = 0; s2 < steps; s2 += 2) {
+        step(s2, ta);
+        if (s2 + 1 < steps) step(s2 + 1, tb);  // uniform
+    }
+    if (!ok && lane == 0) record_error(status, DEV_UNSUPPORTED_WIDTH);
+}
+
 // out fp32 -> bf16 -> fp32 in place (prompt_experts.zig:246), or fp32 -> fp16 into a half output.
 __global__ void round_kernel(float* __restrict__ out, size_t n) {
     for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
@@ -206,11 +443,35 @@ static void item_gemm(hipStream_t s, const uint16_t* X0, const uint16_t* X1, con
                                                                    N, P, status);
 }
 
+template <int CB>
+static void item_gemm_staged(hipStream_t s, const uint16_t* X0, const uint16_t* X1, const int64_t* TP0,
+                             const int64_t* TP1, const int* B0, const int* B1, const int* sorted, const int* items,
+                             const int* count, float* Z, int K, int N, int P, int mats, uint32_t max_items,
+                             int* status) {
+    if (mats == 1 && K <= 2 * PK * 16 && (N / 128) % DNG == 0) {  // the down matrix
+        dim3 grid(max_items, N / 128 / DNG, 1);
+        item_down_staged_kernel<CB><<<grid, PW * 64, 0, s>>>(X0, TP0, B0, sorted, items, count, Z, K, N, P, status);
+        return;
+    }
+    dim3 grid(max_items, N / (16 * 2 * PW), mats);
+    item_gemm_staged_kernel<CB><<<grid, PW * 64, 0, s>>>(X0, X1, TP0, TP1, B0, B1, sorted, items, count, Z, K, N, P,
+                                                         status);
+}
+
+// Widths up to 10 take the staged GEMM; wider ones (three trellis words a lane) the register-streaming one.
 static void item_gemm_dispatch(hipStream_t s, uint32_t cb, bool wide, const uint16_t* X0, const uint16_t* X1,
                                const int64_t* TP0, const int64_t* TP1, const int* B0, const int* B1,
                                const int* sorted, const int* items, const int* count, float* Z, int K, int N, int P,
                                int mats, uint32_t max_items, int* status) {
-    (void)wide;
+    if (!wide) {
+        if (cb == 1)
+            item_gemm_staged<1>(s, X0, X1, TP0, TP1, B0, B1, sorted, items, count, Z, K, N, P, mats, max_items, status);
+        else if (cb == 2)
+            item_gemm_staged<2>(s, X0, X1, TP0, TP1, B0, B1, sorted, items, count, Z, K, N, P, mats, max_items, status);
+        else
+            item_gemm_staged<0>(s, X0, X1, TP0, TP1, B0, B1, sorted, items, count, Z, K, N, P, mats, max_items, status);
+        return;
+    }
     if (cb == 1) {
         item_gemm<1, 2, 16>(s, X0, X1, TP0, TP1, B0, B1, sorted, items, count, Z, K, N, P, mats, max_items, status);
     } else if (cb == 2) {
