@@ -206,7 +206,7 @@ __host__ __device__ constexpr int mfma_lane_p0(int lane) {
 // Lane j holds values 2j and 2j + 1. Levels run over index bits 0, 1, .., 6 in that order, each pair becoming
 // (lower + upper, lower - upper) in fp32: the reference's butterflies (decode.cuh:146-161), so the same bits.
 // The value of lane (l ^ M) in lane l, without the LDS crossbar: DPP within a row of 16 (xor 1 and 2 are quad
-// permutes, xor 4 = half-row mirror after quad reverse, xor 8 = row mirror after half-row mirror) and gfx950's
+// permutes, xor 4 = half-row mirror after quad reverse, xor 8 = row rotation by 8) and gfx950's
 // permlane swaps across rows (xor 16) and halves (xor 32).
 template <int M>
 __device__ __forceinline__ float lane_xor(float v) {
@@ -219,8 +219,7 @@ __device__ __forceinline__ float lane_xor(float v) {
         const int r = __builtin_amdgcn_mov_dpp(x, 0x1B, 0xf, 0xf, false);                    // lane ^ 3
         return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(r, 0x141, 0xf, 0xf, false));  // then ^ 7
     } else if constexpr (M == 8) {
-        const int r = __builtin_amdgcn_mov_dpp(x, 0x141, 0xf, 0xf, false);                   // lane ^ 7
-        return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(r, 0x140, 0xf, 0xf, false));  // then ^ 15
+        return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(x, 0x128, 0xf, 0xf, false));  // row_ror:8
     } else if constexpr (M == 16) {
         // swapping the odd rows of one copy with the even rows of another leaves row r's partner in the copy that
         // did not keep row r

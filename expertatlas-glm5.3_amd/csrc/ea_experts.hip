@@ -74,26 +74,73 @@ __global__ void __launch_bounds__(GROUP_THREADS) group_kernel(const int* __restr
 }
 
 // ---- per-pair input rotation ------------------------------------------------------------------------------------
-// Block (pair p, group of four 128-blocks of K, matrix): a wave a 128-block; lane j holds values 2j, 2j + 1.
-// out[p] = fp16((x[row] * suh[e]) @ H * HAD_SCALE) (exl3_experts.cu:116-134).
+// Block (pair p, matrix): 16 lanes a 128-block of K, lane l holding its values 8 (l & 15) .. +7; a thread steps
+// through K 2048 values at a time. out[p] = fp16((x[row] * suh[e]) @ H * HAD_SCALE) (exl3_experts.cu:116-134). The
+// butterflies run over value-index bits 0..6 in that order (three inside a lane, four across lanes), as in a
+// one-lane-pair-a-value layout, so each output is the same fp32 sum rounded the same way.
 __global__ void __launch_bounds__(256) rot_in_kernel(const void* __restrict__ x, int x_dtype, int x_stride,
                                                      const int* __restrict__ pick, const uint16_t* __restrict__ suh0,
                                                      const uint16_t* __restrict__ suh1, uint16_t* __restrict__ out0,
-                                                     uint16_t* __restrict__ out1, int K, int slots, int E) {
-    const int p = blockIdx.x, mat = blockIdx.z;
-    const int blk = blockIdx.y * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
-    if (blk * 128 >= K) return;
+                                                     uint16_t* __restrict__ out1, int K, int slots, int E, int vec) {
+    const int p = blockIdx.x, mat = blockIdx.y;
     const int e = pick[p];
     if (e < 0 || e >= E) return;
-    const int row = p / slots;
-    const int k = blk * 128 + 2 * lane;
-    const uint16_t* suh = (mat ? suh1 : suh0) + (size_t)e * K + k;
-    const size_t xi = (size_t)row * x_stride + k;
-    float v0 = load_act(x, x_dtype, xi) * h2f(suh[0]);
-    float v1 = load_act(x, x_dtype, xi + 1) * h2f(suh[1]);
-    fwht128_w64(v0, v1, lane);
-    uint16_t* o = (mat ? out1 : out0) + (size_t)p * K + k;
-    *reinterpret_cast<uint32_t*>(o) = (uint32_t)f2h(v0 * HAD_SCALE) | ((uint32_t)f2h(v1 * HAD_SCALE) << 16);
+    const int row = p / slots, lane = threadIdx.x & 63;
+    const uint16_t* suh = (mat ? suh1 : suh0) + (size_t)e * K;
+    uint16_t* o = (mat ? out1 : out0) + (size_t)p * K;
+    const size_t xr = (size_t)row * x_stride;
+    // v' = s * v + o: o - v for the lane holding the upper element of a butterfly, v + o otherwise (exact: s = +-1)
+    const float s1 = lane & 1 ? -1.f : 1.f, s2 = lane & 2 ? -1.f : 1.f, s4 = lane & 4 ? -1.f : 1.f,
+                s8 = lane & 8 ? -1.f : 1.f;
+    for (int k = 8 * (int)threadIdx.x; k < K; k += 2048) {  // uniform across each 16-lane group (K % 128 == 0)
+        float v[8];
+        if (vec) {  // 16-byte aligned rows
+            if (x_dtype == F32) {
+                const f4v a = *reinterpret_cast<const f4v*>(static_cast<const float*>(x) + xr + k);
+                const f4v b = *reinterpret_cast<const f4v*>(static_cast<const float*>(x) + xr + k + 4);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    v[j] = a[j];
+                    v[4 + j] = b[j];
+                }
+            } else {
+                const u4v w = *reinterpret_cast<const u4v*>(static_cast<const uint16_t*>(x) + xr + k);
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const uint16_t h = (uint16_t)(w[j >> 1] >> (16 * (j & 1)));
+                    v[j] = x_dtype == BF16 ? bf2f(h) : h2f(h);
+                }
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) v[j] = load_act(x, x_dtype, xr + k + j);
+        }
+        const u4v sw = *reinterpret_cast<const u4v*>(suh + k);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] *= h2f((uint16_t)(sw[j >> 1] >> (16 * (j & 1))));
+#pragma unroll
+        for (int b = 1; b < 8; b <<= 1)
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+                if (!(j & b)) {
+                    const float lo = v[j], hi = v[j | b];
+                    v[j] = lo + hi;
+                    v[j | b] = lo - hi;
+                }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = __builtin_fmaf(s1, v[j], lane_xor<1>(v[j]));
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = __builtin_fmaf(s2, v[j], lane_xor<2>(v[j]));
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = __builtin_fmaf(s4, v[j], lane_xor<4>(v[j]));
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = __builtin_fmaf(s8, v[j], lane_xor<8>(v[j]));
+        u4v w;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            w[j] = (uint32_t)f2h(v[2 * j] * HAD_SCALE) | ((uint32_t)f2h(v[2 * j + 1] * HAD_SCALE) << 16);
+        *reinterpret_cast<u4v*>(o + k) = w;
+    }
 }
 
 // Block (expert u, n block of NTW tiles, (matrix, split, member tile)): NW waves split the split's k tiles in
@@ -284,9 +331,11 @@ int launch_rot_in(hipStream_t s, const void* x, int x_dtype, uint32_t x_stride, 
     if (kdim % 128 != 0) return EA_BAD_ROT_IN;
     if (x_dtype < 0 || x_dtype > 2 || !x || !pick) return EA_BAD_ARGUMENT;
     if (rows * slots == 0) return EA_OK;
-    dim3 grid(rows * slots, (kdim / 128 + 3) / 4, 2);
+    const size_t eb = x_dtype == F32 ? 4 : 2;
+    const int vec = (reinterpret_cast<uintptr_t>(x) & 15) == 0 && ((size_t)x_stride * eb) % 16 == 0;
+    dim3 grid(rows * slots, 2);
     rot_in_kernel<<<grid, 256, 0, s>>>(x, x_dtype, (int)x_stride, pick, suh0, suh1, out0, out1, (int)kdim,
-                                       (int)slots, (int)experts);
+                                       (int)slots, (int)experts, vec);
     return launched();
 }
 
