@@ -249,4 +249,35 @@ __device__ __forceinline__ void stage_store(uint32_t* st, int k2, int lane, cons
     }
 }
 
+// The same for a width known at compile time: the loads a wave issues are exactly ceil(NKT * K2 / 32), and the
+// chunk -> (row, column) split is a multiply by a constant.
+template <int NKT, int K2>
+constexpr int stage_loads_k() {
+    return (NKT * 2 * K2 + 63) / 64;
+}
+template <int NKT, int K2>
+__device__ __forceinline__ void stage_issue_k(const TileSpan& sp, int lane, u4v (&v)[stage_loads_k<NKT, K2>()]) {
+    constexpr int cpr = 2 * K2, last = NKT * cpr - 1;
+#pragma unroll
+    for (int i = 0; i < stage_loads_k<NKT, K2>(); ++i) {
+        const int c = 64 * i + lane < last ? 64 * i + lane : last;
+        const int t = c / cpr, col = c - t * cpr;
+        v[i] = __builtin_bit_cast(u4v, __builtin_amdgcn_raw_buffer_load_b128(sp.r, t * sp.kstride + col * 16, sp.off,
+                                                                               0));
+    }
+}
+template <int NKT, int K2>
+__device__ __forceinline__ void stage_store_k(uint32_t* st, int lane, const u4v (&v)[stage_loads_k<NKT, K2>()]) {
+#pragma unroll
+    for (int i = 0; i < stage_loads_k<NKT, K2>(); ++i) {
+        const int c = 64 * i + lane;
+        if ((NKT * 2 * K2) % 64 == 0 || c < NKT * 2 * K2) *reinterpret_cast<u4v*>(st + 4 * c) = v[i];
+    }
+}
+template <int K2>
+__device__ __forceinline__ LaneQuad lane_quad_k(int lane) {
+    const Quad q = quad_of<K2>(mfma_lane_p0(lane));
+    return LaneQuad{q.wa, q.wb, q.sh};
+}
+
 }  // namespace ea

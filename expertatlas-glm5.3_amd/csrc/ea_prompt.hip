@@ -20,16 +20,34 @@ constexpr int IPM_TILES = IPM / 16;
 constexpr uint32_t CHUNK_ROWS = 4096;  // rows a pass at most (prompt_experts.zig:17)
 constexpr int ROUTE_THREADS = 1024;
 
-// One block: per-expert counts, exclusive scans of counts and items over experts, items (e, first, cnt <= IPM) in
-// expert order, and sorted[] = pair ids grouped by expert (order within an expert: arrival).
-// (prompt_experts.cu:162-244 with by_count off.)
+constexpr int SMALL_ROWS = 32;     // items of at most this many pairs: the kernels holding two row tiles
+
+// Item i of list `big` (0: items of at most SMALL_ROWS pairs, from the front of items[]; 1: the others, from its
+// back), or false past the list's count.
+__device__ __forceinline__ bool item_at(const int* __restrict__ items, const int* __restrict__ count, int big,
+                                        int max_items, int i, int& e, int& first, int& cnt) {
+    if (i >= count[big]) return false;
+    const int at = big ? max_items - 1 - i : i;
+    e = items[3 * at];
+    first = items[3 * at + 1];
+    cnt = items[3 * at + 2];
+    return true;
+}
+
+// One block: per-expert counts; exclusive scans over experts of the counts and of both lists' items; items
+// (e, first, cnt <= IPM) of an expert in pair order, each into its list; sorted[] = pair ids grouped by expert (order
+// within an expert: arrival); pclass[pair] = 1 when the pair's item is in the list of larger items. (prompt_experts.cu:
+// 162-244 with by_count off; the two lists are this library's: they let a launch size its registers for its items'
+// rows, and the larger items split K.)
 __global__ void __launch_bounds__(ROUTE_THREADS) route_kernel(const int* __restrict__ pick, int n, int E,
                                                              int* __restrict__ sorted, int* __restrict__ items,
-                                                             int* __restrict__ item_count, int max_items) {
+                                                             int* __restrict__ item_count, int* __restrict__ pclass,
+                                                             int max_items) {
     extern __shared__ int sh[];
-    int* cnt = sh;        // [E]
-    int* cur = sh + E;    // [E]
-    __shared__ int wsum[ROUTE_THREADS / 64][2];
+    int* cnt = sh;          // [E]
+    int* cur = sh + E;      // [E]
+    int* start = sh + 2 * E;  // [E]
+    __shared__ int wsum[ROUTE_THREADS / 64][3];
     for (int e = threadIdx.x; e < E; e += ROUTE_THREADS) cnt[e] = 0;
     __syncthreads();
     for (int i = threadIdx.x; i < n; i += ROUTE_THREADS) {
@@ -39,65 +57,75 @@ __global__ void __launch_bounds__(ROUTE_THREADS) route_kernel(const int* __restr
     __syncthreads();
     const int per = (E + ROUTE_THREADS - 1) / ROUTE_THREADS;
     const int e0 = threadIdx.x * per;
-    int c_sum = 0, i_sum = 0;
+    int own[3] = {0, 0, 0};  // pairs, small items, large items of this thread's experts
     for (int q = 0; q < per; ++q) {
         const int e = e0 + q;
         if (e < E) {
-            c_sum += cnt[e];
-            i_sum += (cnt[e] + IPM - 1) / IPM;
+            const int c = cnt[e], full = c / IPM, rem = c - full * IPM;
+            own[0] += c;
+            own[1] += rem > 0 && rem <= SMALL_ROWS;
+            own[2] += full + (rem > SMALL_ROWS);
         }
     }
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    int ci = c_sum, ii = i_sum;
+    int inc[3] = {own[0], own[1], own[2]};
 #pragma unroll
     for (int o = 1; o < 64; o <<= 1) {
-        const int a = __shfl_up(ci, o, 64), b = __shfl_up(ii, o, 64);
-        if (lane >= o) {
-            ci += a;
-            ii += b;
+#pragma unroll
+        for (int v = 0; v < 3; ++v) {
+            const int a = __shfl_up(inc[v], o, 64);
+            if (lane >= o) inc[v] += a;
         }
     }
-    if (lane == 63) {
-        wsum[wave][0] = ci;
-        wsum[wave][1] = ii;
-    }
+    if (lane == 63)
+#pragma unroll
+        for (int v = 0; v < 3; ++v) wsum[wave][v] = inc[v];
     __syncthreads();
     if (wave == 0) {
-        const int a = lane < ROUTE_THREADS / 64 ? wsum[lane][0] : 0, b = lane < ROUTE_THREADS / 64 ? wsum[lane][1] : 0;
-        int sa = a, sb = b;
 #pragma unroll
-        for (int o = 1; o < 64; o <<= 1) {
-            const int x = __shfl_up(sa, o, 64), y = __shfl_up(sb, o, 64);
-            if (lane >= o) {
-                sa += x;
-                sb += y;
+        for (int v = 0; v < 3; ++v) {
+            const int a = lane < ROUTE_THREADS / 64 ? wsum[lane][v] : 0;
+            int sa = a;
+#pragma unroll
+            for (int o = 1; o < 64; o <<= 1) {
+                const int x = __shfl_up(sa, o, 64);
+                if (lane >= o) sa += x;
             }
+            if (lane < ROUTE_THREADS / 64) wsum[lane][v] = sa - a;
+            if (v > 0 && lane == ROUTE_THREADS / 64 - 1) item_count[v - 1] = min(sa, max_items);
         }
-        if (lane < ROUTE_THREADS / 64) {
-            wsum[lane][0] = sa - a;
-            wsum[lane][1] = sb - b;
-        }
-        if (lane == ROUTE_THREADS / 64 - 1) item_count[0] = min(sb, max_items);
     }
     __syncthreads();
-    int off = wsum[wave][0] + ci - c_sum, it = wsum[wave][1] + ii - i_sum;
+    int off = wsum[wave][0] + inc[0] - own[0];
+    int si = wsum[wave][1] + inc[1] - own[1], bi = wsum[wave][2] + inc[2] - own[2];
     for (int q = 0; q < per; ++q) {
         const int e = e0 + q;
         if (e >= E) break;
         const int c = cnt[e];
         cur[e] = off;
-        for (int f = 0; f < c; f += IPM, ++it)
-            if (it < max_items) {
-                items[3 * it] = e;
-                items[3 * it + 1] = off + f;
-                items[3 * it + 2] = min(IPM, c - f);
+        start[e] = off;
+        for (int f = 0; f < c; f += IPM) {
+            const int m = min(IPM, c - f);
+            const int at = m <= SMALL_ROWS ? si++ : max_items - 1 - bi++;
+            if (at >= 0 && at < max_items) {
+                items[3 * at] = e;
+                items[3 * at + 1] = off + f;
+                items[3 * at + 2] = m;
             }
+        }
         off += c;
     }
     __syncthreads();
     for (int i = threadIdx.x; i < n; i += ROUTE_THREADS) {
         const int e = pick[i];
-        if (e >= 0 && e < E) sorted[atomicAdd(&cur[e], 1)] = i;
+        int big = 0;
+        if (e >= 0 && e < E) {
+            const int at = atomicAdd(&cur[e], 1);
+            sorted[at] = i;
+            const int f = (at - start[e]) / IPM * IPM;  // the first pair of its item, within the expert
+            big = min(IPM, cnt[e] - f) > SMALL_ROWS;
+        }
+        pclass[i] = big;
     }
 }
 
@@ -108,10 +136,9 @@ __global__ void __launch_bounds__(NW * 64) item_gemm_kernel(
     const uint16_t* __restrict__ X0, const uint16_t* __restrict__ X1, const int64_t* __restrict__ TP0,
     const int64_t* __restrict__ TP1, const int* __restrict__ K2_0, const int* __restrict__ K2_1,
     const int* __restrict__ sorted, const int* __restrict__ items, const int* __restrict__ item_count,
-    float* __restrict__ Z, int K, int N, int P, int* __restrict__ status) {
-    const int item = blockIdx.x;
-    if (item >= item_count[0]) return;
-    const int e = items[3 * item], first = items[3 * item + 1], cnt = items[3 * item + 2];
+    float* __restrict__ Z, int K, int N, int P, int big, int max_items, int* __restrict__ status) {
+    int e, first, cnt;
+    if (!item_at(items, item_count, big, max_items, blockIdx.x, e, first, cnt)) return;
     const int mat = blockIdx.z;
     const uint16_t* X = mat ? X1 : X0;
     const uint32_t* T = reinterpret_cast<const uint32_t*>(mat ? TP1[e] : TP0[e]);
@@ -157,23 +184,36 @@ __global__ void __launch_bounds__(NW * 64) item_gemm_kernel(
 
 // ---- the staged item GEMM (widths 2..10) -------------------------------------------------------------------
 
-constexpr int PK = 8;                                      // k tiles a chunk: 128 k
-constexpr int PXS = PK * 16 + 8;                           // LDS row stride of a staged A chunk, halves (272 bytes)
-constexpr int PW = 4;                                      // waves a block: 8 column tiles, 128 columns
-constexpr int PSTAGE = PK * 2 * 4 * STAGE_MAXK2;           // a wave's staged trellis words a chunk
-constexpr int PA = IPM * PK * 16 * 2 / 16 / (PW * 64);     // 16-byte A pieces a thread a chunk
-static_assert(PA * PW * 64 * 16 == IPM * PK * 16 * 2, "the block's threads cover an A chunk exactly");
+constexpr int PK = 8;                             // k tiles a chunk: 128 k
+constexpr int PXS = PK * 16 + 8;                  // LDS row stride of a staged activation chunk, halves (272 bytes)
+constexpr int PW = 4;                             // waves a block: 8 column tiles, 128 columns
+constexpr int PSTAGE = PK * 2 * 4 * STAGE_MAXK2;  // a wave's staged trellis words a chunk
+constexpr int DNG = 8;                            // down matrix: column blocks of 128 a block (small items)
+constexpr int DNG_BIG = 2;                        // the same for the larger items: more blocks for fewer items
+constexpr int GU_SPLIT = 4;                       // K splits of a larger item's gate|up
+// The number of K splits of a larger item's gate|up over K (at most one a chunk).
+static int gu_splits(int K) { return K / (PK * 16) < GU_SPLIT ? K / (PK * 16) : GU_SPLIT; }
+constexpr int DXS = 2 * PK * 16 + 8;              // down matrix: LDS row stride of the activations (K up to 256)
 
-// One chunk (PK k tiles) of a wave: its two column tiles times the item's first mts row tiles. The trellis words
-// are staged in st (tile (t, j) at word (2 t + j) * 4 K2), the activations in xa (row stride xs halves); each tile
-// pair decodes once and feeds all row tiles.
-template <int CB, int K2>
+// An activation piece (8 halves: column 8 q8 .. +7 of a chunk row) into LDS. Within each 32-k step of the row
+// (16 words) word d goes to 4 (d & 3) + (d >> 2), so the words of a lane's MFMA operand (g, g + 4, g + 8, g + 12 of
+// the step: the k order in which the trellis quads fill the B operand) are one 16-byte read.
+__device__ __forceinline__ void put_a(uint16_t* row, int q8, const u4v& v) {
+    uint32_t* w = reinterpret_cast<uint32_t*>(row) + 16 * (q8 >> 2) + (q8 & 3);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) w[4 * r] = v[r];
+}
+
+// One chunk (PK k tiles) of a wave: its two column tiles times the item's first mts (<= MT) row tiles. The trellis
+// words are staged in st (tile (t, j) at word (2 t + j) * 4 K2), the activations in xa (row stride xs halves, laid
+// out by put_a); each tile pair decodes once and feeds all row tiles.
+template <int CB, int K2, int MT>
 __device__ __forceinline__ void item_chunk(const uint32_t* st, const LaneQuad& lq, const uint16_t* xa, int mts,
-                                           int lane, f4v (&acc)[IPM_TILES][2], int xs = PXS) {
+                                           int lane, f4v (&acc)[MT][2], int xs) {
     constexpr int TW = 4 * K2;
     const uint32_t* wa = st + lq.w0;
     const uint32_t* wb = st + lq.w1;
-    const uint16_t* xr = xa + (lane & 15) * xs + 2 * ((lane >> 4) & 3);
+    const uint16_t* xr = xa + (lane & 15) * xs + 8 * ((lane >> 4) & 3);
 #pragma unroll
     for (int t = 0; t < PK; t += 2) {
         h8v bb[2];
@@ -185,95 +225,62 @@ __device__ __forceinline__ void item_chunk(const uint32_t* st, const LaneQuad& l
             bb[j] = __builtin_bit_cast(h8v, (u4v{b0.x, b0.y, b1.x, b1.y}));
         }
 #pragma unroll
-        for (int mt = 0; mt < IPM_TILES; ++mt) {
+        for (int mt = 0; mt < MT; ++mt) {
             if (mt >= mts) break;  // the item's occupied row tiles only (uniform)
-            const uint16_t* xk = xr + mt * 16 * xs + t * 16;
-            const u4v au = {*reinterpret_cast<const uint32_t*>(xk), *reinterpret_cast<const uint32_t*>(xk + 8),
-                            *reinterpret_cast<const uint32_t*>(xk + 16), *reinterpret_cast<const uint32_t*>(xk + 24)};
-            const h8v a = __builtin_bit_cast(h8v, au);
+            const h8v a = *reinterpret_cast<const h8v*>(xr + mt * 16 * xs + t * 16);
             acc[mt][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bb[0], acc[mt][0], 0, 0, 0);
             acc[mt][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bb[1], acc[mt][1], 0, 0, 0);
         }
     }
 }
 
-// Block (item, 128 columns, matrix): the item's rows (up to IPM, IPM_TILES MFMA row tiles) times its expert's matrix
-// over all of K in chunks of 128. A chunk's activations go to LDS once for the block's four waves; each wave's two
-// column tiles of the chunk come in as 16-byte loads staged in the wave's own LDS region. The activations are loaded
-// one chunk ahead and the trellis two, while the current chunk decodes and multiplies; only the item's occupied row
-// tiles are loaded and multiplied. Rows past the item's count read the item's first pair and are not stored (MFMA
-// rows do not mix). Z[mat][pair][n] fp32.
-template <int CB>
-__global__ void __launch_bounds__(PW * 64) __attribute__((amdgpu_waves_per_eu(2)))
-item_gemm_staged_kernel(const uint16_t* __restrict__ X0, const uint16_t* __restrict__ X1,
-                        const int64_t* __restrict__ TP0, const int64_t* __restrict__ TP1,
-                        const int* __restrict__ K2_0, const int* __restrict__ K2_1, const int* __restrict__ sorted,
-                        const int* __restrict__ items, const int* __restrict__ item_count, float* __restrict__ Z,
-                        int K, int N, int P, int* __restrict__ status) {
-    const int item = blockIdx.x;
-    if (item >= item_count[0]) return;
-    const int e = items[3 * item], first = items[3 * item + 1], cnt = items[3 * item + 2];
-    const int mat = blockIdx.z;
-    const uint16_t* X = mat ? X1 : X0;
-    const uint32_t* T = reinterpret_cast<const uint32_t*>(mat ? TP1[e] : TP0[e]);
-    const int k2 = mat ? K2_1[e] : K2_0[e];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    __shared__ int pair_sh[IPM];
-    __shared__ __attribute__((aligned(16))) uint16_t xa[IPM * PXS];
-    __shared__ __attribute__((aligned(16))) uint32_t st[PW][PSTAGE];
-    if (tid < IPM) pair_sh[tid] = tid < cnt ? sorted[first + tid] : -1;
-    __syncthreads();
-    // this thread's pieces of every A chunk: piece i is row tile i (row 16 i + (tid >> 4)), halves 8 (tid & 15) .. +7
-    // of the chunk; a piece past the item's row tiles reads row tile 0's address (a cache hit) and is not stored
-    const int mts = (cnt + 15) >> 4;
-    uint32_t aoff[PA];
-    int lofs[PA];
-#pragma unroll
-    for (int i = 0; i < PA; ++i) {
-        const int idx = i * PW * 64 + tid, row = idx >> 4;
-        const int rr = i < mts ? row : (tid >> 4);
-        const int p = pair_sh[rr] >= 0 ? pair_sh[rr] : pair_sh[0];
-        aoff[i] = ((uint32_t)p * (uint32_t)K + 8u * (idx & 15)) * 2u;
-        lofs[i] = row * PXS + 8 * (idx & 15);
-    }
-    const __amdgpu_buffer_rsrc_t xrs = buffer_rsrc(X, (uint32_t)((size_t)P * K * 2));
-    const int nt0 = blockIdx.y * (2 * PW) + 2 * wave;
-    const int ns = N >> 4, TWB = 16 * k2;
-    TileSpan sp;
-    sp.r = buffer_rsrc(T, (uint32_t)((K >> 4) * ns * TWB));
-    sp.off = nt0 * TWB;
-    sp.kstride = ns * TWB;
-    const LaneQuad lq = lane_quad(k2, lane);
-    f4v acc[IPM_TILES][2];
-#pragma unroll
-    for (int mt = 0; mt < IPM_TILES; ++mt) acc[mt][0] = acc[mt][1] = f4v{0.f, 0.f, 0.f, 0.f};
-    const int nch = K / (PK * 16);
-    // loads complete in issue order; every load is issued (a chunk past the last re-reads the last), so the waits
-    // stay exact: the activations one chunk ahead, the trellis two
-    u4v av[PA], ta[stage_loads<PK>()], tb[stage_loads<PK>()];
+// The chunk loop of a gate|up block for one width: the activations one chunk ahead, the trellis two. Loads complete
+// in issue order and every load is issued (a chunk past the last re-reads the last), so the waits stay exact.
+// With FOLD the nch chunks are summed as nsum splits ([s nch / nsum, (s + 1) nch / nsum)), each accumulated from zero
+// and added in order into tot (from zero): the bits of a K-split item's sum of its split planes, so a pair's sums do
+// not depend on which list its item is in. Without FOLD the block's chunks accumulate into acc.
+template <int CB, int K2, int MT, bool FOLD>
+__device__ __forceinline__ void gu_loop(__amdgpu_buffer_rsrc_t xrs, const uint32_t (&aoff)[MT], const int (&lofs)[MT],
+                                        const TileSpan& sp, uint16_t* xa, uint32_t* st, int lane, int q8, int mts,
+                                        int c0, int nch, int nsum, f4v (&acc)[MT][2], f4v (&tot)[MT][2]) {
+    constexpr int NL = stage_loads_k<PK, K2>();
+    const LaneQuad lq = lane_quad_k<K2>(lane);
+    u4v av[MT], ta[NL], tb[NL];
+    int sn = 1;  // the next split's index
     auto issue_a = [&](int c) {
-        c = c < nch ? c : nch - 1;
+        c = c0 + (c < nch ? c : nch - 1);
 #pragma unroll
-        for (int i = 0; i < PA; ++i)
+        for (int i = 0; i < MT; ++i)
             av[i] = __builtin_bit_cast(u4v, __builtin_amdgcn_raw_buffer_load_b128(xrs, aoff[i], c * PK * 32, 0));
     };
-    auto issue_t = [&](int c, u4v (&tv)[stage_loads<PK>()]) {
-        c = c < nch ? c : nch - 1;
+    auto issue_t = [&](int c, u4v (&tv)[NL]) {
+        c = c0 + (c < nch ? c : nch - 1);
         TileSpan sc = sp;
         sc.off = sp.off + c * PK * sp.kstride;
-        stage_issue<PK>(sc, k2, lane, tv);
+        stage_issue_k<PK, K2>(sc, lane, tv);
     };
-    bool ok = true;
-    auto step = [&](int c, u4v (&tv)[stage_loads<PK>()]) {
-        __syncthreads();  // the previous chunk's reads of xa and of the wave's stage are done
+    auto step = [&](int c, u4v (&tv)[NL]) {
+        __syncthreads();  // the previous chunk's reads of xa are done
 #pragma unroll
-        for (int i = 0; i < PA; ++i)
-            if (i < mts) *reinterpret_cast<u4v*>(xa + lofs[i]) = av[i];
-        stage_store<PK>(st[wave], k2, lane, tv);
+        for (int i = 0; i < MT; ++i)
+            if (i < mts) put_a(xa + lofs[i], q8, av[i]);
+        stage_store_k<PK, K2>(st, lane, tv);  // only this wave reads its region, in order
         issue_a(c + 1);
         issue_t(c + 2, tv);
         __syncthreads();  // the chunk's activations are in LDS
-        ok = EA_K2_SWITCH(k2, 2, 10, (item_chunk<CB, K2V>(st[wave], lq, xa, mts, lane, acc)));
+        item_chunk<CB, K2, MT>(st, lq, xa, mts, lane, acc, PXS);
+        if constexpr (FOLD) {
+            if (c + 1 == sn * nch / nsum) {  // the end of a split (uniform)
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                    for (int j = 0; j < 2; ++j) {
+                        tot[mt][j] += acc[mt][j];
+                        acc[mt][j] = f4v{0.f, 0.f, 0.f, 0.f};
+                    }
+                ++sn;
+            }
+        }
     };
     issue_t(0, ta);
     issue_t(1, tb);
@@ -282,98 +289,110 @@ item_gemm_staged_kernel(const uint16_t* __restrict__ X0, const uint16_t* __restr
         step(c, ta);
         if (c + 1 < nch) step(c + 1, tb);  // uniform
     }
+}
+
+// Block (item of list MT > 2, 128 columns, (matrix, K split)): the item's rows (up to MT row tiles) times its
+// expert's matrix over split s of K's chunks of 128 (splits [s nch / nsplit, (s + 1) nch / nsplit)); a block of the
+// small items' list (nsplit 1) covers all of K and sums it as nsum splits the same way. A chunk's
+// activations go to LDS once for the block's four waves; each wave's two column tiles of the chunk come in as 16-byte
+// loads staged in the wave's own LDS region. Only the item's occupied row tiles are loaded and multiplied; rows past
+// the item's count read the item's first pair and are not stored (MFMA rows do not mix). Split 0 goes to
+// Z[mat][pair][n], split s > 0 to Zp[s - 1][mat][pair][n] (fp32).
+template <int CB, int MT>
+__global__ void __launch_bounds__(PW * 64) __attribute__((amdgpu_waves_per_eu(MT > 2 ? 2 : 4)))
+item_gu_kernel(const uint16_t* __restrict__ X0, const uint16_t* __restrict__ X1, const int64_t* __restrict__ TP0,
+               const int64_t* __restrict__ TP1, const int* __restrict__ K2_0, const int* __restrict__ K2_1,
+               const int* __restrict__ sorted, const int* __restrict__ items, const int* __restrict__ item_count,
+               float* __restrict__ Z, float* __restrict__ Zp, int K, int N, int P, int nsplit, int nsum,
+               int max_items, int* __restrict__ status) {
+    int e, first, cnt;
+    if (!item_at(items, item_count, MT > 2, max_items, blockIdx.x, e, first, cnt)) return;
+    const int mat = blockIdx.z / nsplit, split = blockIdx.z % nsplit;
+    const uint16_t* X = mat ? X1 : X0;
+    const uint32_t* T = reinterpret_cast<const uint32_t*>(mat ? TP1[e] : TP0[e]);
+    const int k2 = mat ? K2_1[e] : K2_0[e];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    __shared__ int pair_sh[MT * 16];
+    __shared__ __attribute__((aligned(16))) uint16_t xa[MT * 16 * PXS];
+    __shared__ __attribute__((aligned(16))) uint32_t st[PW][PSTAGE];
+    if (tid < MT * 16) pair_sh[tid] = tid < cnt ? sorted[first + tid] : -1;
+    __syncthreads();
+    // this thread's activation pieces of every chunk: piece i is row 16 i + (tid >> 4), halves 8 (tid & 15) .. +7;
+    // a piece past the item's row tiles reads row tile 0's address (a cache hit) and is not stored
+    const int mts = (cnt + 15) >> 4;
+    uint32_t aoff[MT];
+    int lofs[MT];
+#pragma unroll
+    for (int i = 0; i < MT; ++i) {
+        const int row = i * 16 + (tid >> 4);
+        const int rr = i < mts ? row : (tid >> 4);
+        const int p = pair_sh[rr] >= 0 ? pair_sh[rr] : pair_sh[0];
+        aoff[i] = ((uint32_t)p * (uint32_t)K + 8u * (tid & 15)) * 2u;
+        lofs[i] = row * PXS;
+    }
+    const __amdgpu_buffer_rsrc_t xrs = buffer_rsrc(X, (uint32_t)((size_t)P * K * 2));
+    const int nt0 = blockIdx.y * (2 * PW) + 2 * wave;
+    const int ns = N >> 4, TWB = 16 * k2;
+    TileSpan sp;
+    sp.r = buffer_rsrc(T, (uint32_t)((K >> 4) * ns * TWB));
+    sp.off = nt0 * TWB;
+    sp.kstride = ns * TWB;
+    constexpr bool FOLD = MT <= 2;
+    f4v acc[MT][2], tot[MT][2];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) acc[mt][0] = acc[mt][1] = tot[mt][0] = tot[mt][1] = f4v{0.f, 0.f, 0.f, 0.f};
+    const int nch = K / (PK * 16);
+    const int c0 = split * nch / nsplit, nc = (split + 1) * nch / nsplit - c0;  // nsplit <= nch: nc >= 1
+    const bool ok = EA_K2_SWITCH(k2, 2, 10,
+                                 (gu_loop<CB, K2V, MT, FOLD>(xrs, aoff, lofs, sp, xa, st[wave], lane, tid & 15, mts, c0,
+                                                             nc, nsum, acc, tot)));
     if (!ok) {
         if (lane == 0) record_error(status, DEV_UNSUPPORTED_WIDTH);
         return;
     }
-    float* Zm = Z + (size_t)mat * P * N;
+    float* Zm = (split ? Zp + (size_t)(split - 1) * 2 * P * N : Z) + (size_t)mat * P * N;
 #pragma unroll
-    for (int mt = 0; mt < IPM_TILES; ++mt)
+    for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int p = pair_sh[mt * 16 + 4 * (lane >> 4) + i];
             if (p < 0) continue;
 #pragma unroll
-            for (int j = 0; j < 2; ++j) Zm[(size_t)p * N + (nt0 + j) * 16 + (lane & 15)] = acc[mt][j][i];
+            for (int j = 0; j < 2; ++j)
+                Zm[(size_t)p * N + (nt0 + j) * 16 + (lane & 15)] = FOLD ? tot[mt][j][i] : 0.f + acc[mt][j][i];
         }
 }
 
-// The down matrix (K = I of 128 or 256: one or two chunks): a block (item, DNG column blocks of 128) loads the item's
-// activations for all of K into LDS once, then runs its column blocks one after another, the trellis of each
-// (column block, chunk) step loaded two steps ahead, and stores each column block's rows when its last chunk is done.
-constexpr int DNG = 8;                        // column blocks a block
-constexpr int DXS = 2 * PK * 16 + 8;          // LDS row stride of the activations, halves (K up to 256)
-
-template <int CB>
-__global__ void __launch_bounds__(PW * 64) __attribute__((amdgpu_waves_per_eu(2)))
-item_down_staged_kernel(const uint16_t* __restrict__ X, const int64_t* __restrict__ TP, const int* __restrict__ K2T,
-                        const int* __restrict__ sorted, const int* __restrict__ items,
-                        const int* __restrict__ item_count, float* __restrict__ Z, int K, int N, int P,
-                        int* __restrict__ status) {
-    const int item = blockIdx.x;
-    if (item >= item_count[0]) return;
-    const int e = items[3 * item], first = items[3 * item + 1], cnt = items[3 * item + 2];
-    const uint32_t* T = reinterpret_cast<const uint32_t*>(TP[e]);
-    const int k2 = K2T[e];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    __shared__ int pair_sh[IPM];
-    __shared__ __attribute__((aligned(16))) uint16_t xa[IPM * DXS];
-    __shared__ __attribute__((aligned(16))) uint32_t st[PW][PSTAGE];
-    if (tid < IPM) pair_sh[tid] = tid < cnt ? sorted[first + tid] : -1;
-    __syncthreads();
-    const int mts = (cnt + 15) >> 4;
-    const int nch = K / (PK * 16);  // 1 or 2
-    // the activations: piece i of a chunk is row tile i (row 16 i + (tid >> 4)), halves 8 (tid & 15) .. +7
-    {
-        const __amdgpu_buffer_rsrc_t xrs = buffer_rsrc(X, (uint32_t)((size_t)P * K * 2));
-        for (int c = 0; c < nch; ++c) {
-            u4v av[PA];
-#pragma unroll
-            for (int i = 0; i < PA; ++i) {
-                const int row = i * 16 + (tid >> 4);
-                const int rr = i < mts ? row : (tid >> 4);
-                const int p = pair_sh[rr] >= 0 ? pair_sh[rr] : pair_sh[0];
-                av[i] = __builtin_bit_cast(
-                    u4v, __builtin_amdgcn_raw_buffer_load_b128(
-                             xrs, ((uint32_t)p * (uint32_t)K + (uint32_t)(c * PK * 16 + 8 * (tid & 15))) * 2u, 0, 0));
-            }
-#pragma unroll
-            for (int i = 0; i < PA; ++i)
-                if (i < mts)
-                    *reinterpret_cast<u4v*>(xa + (i * 16 + (tid >> 4)) * DXS + c * PK * 16 + 8 * (tid & 15)) = av[i];
-        }
-    }
-    const int ns = N >> 4, TWB = 16 * k2;
-    const int nb0 = blockIdx.y * DNG;  // first column block
-    TileSpan sp;
-    sp.r = buffer_rsrc(T, (uint32_t)((K >> 4) * ns * TWB));
-    sp.off = (nb0 * 8 + 2 * wave) * TWB;
-    sp.kstride = ns * TWB;
-    const LaneQuad lq = lane_quad(k2, lane);
-    const int steps = DNG * nch;
-    u4v ta[stage_loads<PK>()], tb[stage_loads<PK>()];
-    auto issue_t = [&](int s2, u4v (&tv)[stage_loads<PK>()]) {  // step s2: column block s2 / nch, chunk s2 % nch
+// The column blocks of a down block for one width: step s is column block s / nch, chunk s % nch; the trellis two
+// steps ahead; each column block's rows are stored when its last chunk is done.
+template <int CB, int K2, int MT, int NG>
+__device__ __forceinline__ void dn_loop(const TileSpan& sp, const uint16_t* xa, uint32_t* st, int lane, int wave,
+                                        int mts, int nch, int nb0, const int* pair_sh, float* __restrict__ Z, int N) {
+    constexpr int NL = stage_loads_k<PK, K2>();
+    constexpr int TWB = 16 * K2;
+    const LaneQuad lq = lane_quad_k<K2>(lane);
+    const int steps = NG * nch;
+    u4v ta[NL], tb[NL];
+    f4v acc[MT][2];
+    auto issue_t = [&](int s2, u4v (&tv)[NL]) {
         s2 = s2 < steps ? s2 : steps - 1;
         TileSpan sc = sp;
         sc.off = sp.off + (s2 / nch) * 8 * TWB + (s2 % nch) * PK * sp.kstride;
-        stage_issue<PK>(sc, k2, lane, tv);
+        stage_issue_k<PK, K2>(sc, lane, tv);
     };
-    f4v acc[IPM_TILES][2];
-    bool ok = true;
-    auto step = [&](int s2, u4v (&tv)[stage_loads<PK>()]) {
+    auto step = [&](int s2, u4v (&tv)[NL]) {
         const int c = s2 % nch;
         if (c == 0) {
 #pragma unroll
-            for (int mt = 0; mt < IPM_TILES; ++mt) acc[mt][0] = acc[mt][1] = f4v{0.f, 0.f, 0.f, 0.f};
+            for (int mt = 0; mt < MT; ++mt) acc[mt][0] = acc[mt][1] = f4v{0.f, 0.f, 0.f, 0.f};
         }
-        stage_store<PK>(st[wave], k2, lane, tv);  // only this wave reads its region, in order
+        stage_store_k<PK, K2>(st, lane, tv);  // only this wave reads its region, in order
         issue_t(s2 + 2, tv);
-        __syncthreads();  // the activations are in LDS (the first step); keeps the waves together
-        ok = EA_K2_SWITCH(k2, 2, 10, (item_chunk<CB, K2V>(st[wave], lq, xa + c * PK * 16, mts, lane, acc, DXS)));
-        if (c == nch - 1 && ok) {
+        item_chunk<CB, K2, MT>(st, lq, xa + c * PK * 16, mts, lane, acc, DXS);
+        if (c == nch - 1) {
             const int nt0 = (nb0 + s2 / nch) * 8 + 2 * wave;
 #pragma unroll
-            for (int mt = 0; mt < IPM_TILES; ++mt)
+            for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     const int p = pair_sh[mt * 16 + 4 * (lane >> 4) + i];
@@ -389,6 +408,56 @@ item_down_staged_kernel(const uint16_t* __restrict__ X, const int64_t* __restric
         step(s2, ta);
         if (s2 + 1 < steps) step(s2 + 1, tb);  // uniform
     }
+}
+
+// The down matrix (K = I of 128 or 256: one or two chunks): a block (item of list MT > 2, NG column blocks of 128)
+// loads the item's activations for all of K into LDS once, then its waves run the column blocks independently.
+template <int CB, int MT, int NG>
+__global__ void __launch_bounds__(PW * 64) __attribute__((amdgpu_waves_per_eu(MT > 2 ? 2 : 4)))
+item_dn_kernel(const uint16_t* __restrict__ X, const int64_t* __restrict__ TP, const int* __restrict__ K2T,
+               const int* __restrict__ sorted, const int* __restrict__ items, const int* __restrict__ item_count,
+               float* __restrict__ Z, int K, int N, int P, int max_items, int* __restrict__ status) {
+    int e, first, cnt;
+    if (!item_at(items, item_count, MT > 2, max_items, blockIdx.x, e, first, cnt)) return;
+    const uint32_t* T = reinterpret_cast<const uint32_t*>(TP[e]);
+    const int k2 = K2T[e];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    __shared__ int pair_sh[MT * 16];
+    __shared__ __attribute__((aligned(16))) uint16_t xa[MT * 16 * DXS];
+    __shared__ __attribute__((aligned(16))) uint32_t st[PW][PSTAGE];
+    if (tid < MT * 16) pair_sh[tid] = tid < cnt ? sorted[first + tid] : -1;
+    __syncthreads();
+    const int mts = (cnt + 15) >> 4;
+    const int nch = K / (PK * 16);  // 1 or 2
+    {
+        const __amdgpu_buffer_rsrc_t xrs = buffer_rsrc(X, (uint32_t)((size_t)P * K * 2));
+        u4v av[2][MT];
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+#pragma unroll
+            for (int i = 0; i < MT; ++i) {
+                const int rr = i < mts ? i * 16 + (tid >> 4) : (tid >> 4);
+                const int p = pair_sh[rr] >= 0 ? pair_sh[rr] : pair_sh[0];
+                const int cc = c < nch ? c : 0;
+                av[c][i] = __builtin_bit_cast(
+                    u4v, __builtin_amdgcn_raw_buffer_load_b128(
+                             xrs, ((uint32_t)p * (uint32_t)K + (uint32_t)(cc * PK * 16 + 8 * (tid & 15))) * 2u, 0, 0));
+            }
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+#pragma unroll
+            for (int i = 0; i < MT; ++i)
+                if (c < nch && i < mts) put_a(xa + (i * 16 + (tid >> 4)) * DXS + c * PK * 16, tid & 15, av[c][i]);
+    }
+    const int ns = N >> 4, TWB = 16 * k2;
+    const int nb0 = blockIdx.y * NG;  // first column block
+    TileSpan sp;
+    sp.r = buffer_rsrc(T, (uint32_t)((K >> 4) * ns * TWB));
+    sp.off = (nb0 * 8 + 2 * wave) * TWB;
+    sp.kstride = ns * TWB;
+    __syncthreads();  // the activations are in LDS
+    const bool ok =
+        EA_K2_SWITCH(k2, 2, 10, (dn_loop<CB, K2V, MT, NG>(sp, xa, st[wave], lane, wave, mts, nch, nb0, pair_sh, Z, N)));
     if (!ok && lane == 0) record_error(status, DEV_UNSUPPORTED_WIDTH);
 }
 
@@ -405,7 +474,7 @@ __global__ void to_half_kernel(const float* __restrict__ in, uint16_t* __restric
 static size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
 
 struct PromptLayout {
-    size_t sorted, items, count, xd, plane, xg, xu, z, total;
+    size_t sorted, items, count, xd, plane, xg, xu, z, zp, pclass, total;
     uint32_t rows, max_items;
 };
 
@@ -429,6 +498,8 @@ static PromptLayout prompt_layout(const ea_routed* ex, uint32_t rows, uint32_t s
     l.xg = take(n * D * 2);
     l.xu = take(n * D * 2);
     l.z = take(2 * n * I * 4);
+    l.zp = take((size_t)(gu_splits((int)D) - 1) * 2 * n * I * 4);
+    l.pclass = take(n * 4);
     l.total = off;
     return l;
 }
@@ -439,37 +510,49 @@ static void item_gemm(hipStream_t s, const uint16_t* X0, const uint16_t* X1, con
                       int K, int N, int P, int mats, uint32_t max_items, int* status) {
     constexpr int NTW = 2, NW = 4;
     dim3 grid(max_items, (N / 16 + NTW * NW - 1) / (NTW * NW), mats);
-    item_gemm_kernel<CB, LO, HI, NTW, NW><<<grid, NW * 64, 0, s>>>(X0, X1, TP0, TP1, B0, B1, sorted, items, count, Z, K,
-                                                                   N, P, status);
+    for (int big = 1; big >= 0; --big)
+        item_gemm_kernel<CB, LO, HI, NTW, NW><<<grid, NW * 64, 0, s>>>(X0, X1, TP0, TP1, B0, B1, sorted, items, count,
+                                                                       Z, K, N, P, big, (int)max_items, status);
 }
 
+// Both item lists, the larger items first (their blocks run longest).
+// Both item lists, the larger items first. The down matrix takes the resident-activation kernel when its K and N fit,
+// anything else the chunked one, with the larger items' K split into Zp when Zp is given.
 template <int CB>
 static void item_gemm_staged(hipStream_t s, const uint16_t* X0, const uint16_t* X1, const int64_t* TP0,
                              const int64_t* TP1, const int* B0, const int* B1, const int* sorted, const int* items,
-                             const int* count, float* Z, int K, int N, int P, int mats, uint32_t max_items,
+                             const int* count, float* Z, float* Zp, int K, int N, int P, int mats, uint32_t max_items,
                              int* status) {
+    const int mi = (int)max_items;
     if (mats == 1 && K <= 2 * PK * 16 && (N / 128) % DNG == 0) {  // the down matrix
-        dim3 grid(max_items, N / 128 / DNG, 1);
-        item_down_staged_kernel<CB><<<grid, PW * 64, 0, s>>>(X0, TP0, B0, sorted, items, count, Z, K, N, P, status);
+        item_dn_kernel<CB, IPM_TILES, DNG_BIG><<<dim3(max_items, N / 128 / DNG_BIG, 1), PW * 64, 0, s>>>(
+            X0, TP0, B0, sorted, items, count, Z, K, N, P, mi, status);
+        item_dn_kernel<CB, SMALL_ROWS / 16, DNG><<<dim3(max_items, N / 128 / DNG, 1), PW * 64, 0, s>>>(
+            X0, TP0, B0, sorted, items, count, Z, K, N, P, mi, status);
         return;
     }
-    dim3 grid(max_items, N / (16 * 2 * PW), mats);
-    item_gemm_staged_kernel<CB><<<grid, PW * 64, 0, s>>>(X0, X1, TP0, TP1, B0, B1, sorted, items, count, Z, K, N, P,
-                                                         status);
+    const int ns = Zp ? gu_splits(K) : 1;
+    item_gu_kernel<CB, IPM_TILES><<<dim3(max_items, N / (16 * 2 * PW), mats * ns), PW * 64, 0, s>>>(
+        X0, X1, TP0, TP1, B0, B1, sorted, items, count, Z, Zp, K, N, P, ns, 1, mi, status);
+    item_gu_kernel<CB, SMALL_ROWS / 16><<<dim3(max_items, N / (16 * 2 * PW), mats), PW * 64, 0, s>>>(
+        X0, X1, TP0, TP1, B0, B1, sorted, items, count, Z, Zp, K, N, P, 1, ns, mi, status);
 }
 
 // Widths up to 10 take the staged GEMM; wider ones (three trellis words a lane) the register-streaming one.
 static void item_gemm_dispatch(hipStream_t s, uint32_t cb, bool wide, const uint16_t* X0, const uint16_t* X1,
                                const int64_t* TP0, const int64_t* TP1, const int* B0, const int* B1,
-                               const int* sorted, const int* items, const int* count, float* Z, int K, int N, int P,
-                               int mats, uint32_t max_items, int* status) {
+                               const int* sorted, const int* items, const int* count, float* Z, float* Zp, int K,
+                               int N, int P, int mats, uint32_t max_items, int* status) {
     if (!wide) {
         if (cb == 1)
-            item_gemm_staged<1>(s, X0, X1, TP0, TP1, B0, B1, sorted, items, count, Z, K, N, P, mats, max_items, status);
+            item_gemm_staged<1>(s, X0, X1, TP0, TP1, B0, B1, sorted, items, count, Z, Zp, K, N, P, mats, max_items,
+                                status);
         else if (cb == 2)
-            item_gemm_staged<2>(s, X0, X1, TP0, TP1, B0, B1, sorted, items, count, Z, K, N, P, mats, max_items, status);
+            item_gemm_staged<2>(s, X0, X1, TP0, TP1, B0, B1, sorted, items, count, Z, Zp, K, N, P, mats, max_items,
+                                status);
         else
-            item_gemm_staged<0>(s, X0, X1, TP0, TP1, B0, B1, sorted, items, count, Z, K, N, P, mats, max_items, status);
+            item_gemm_staged<0>(s, X0, X1, TP0, TP1, B0, B1, sorted, items, count, Z, Zp, K, N, P, mats, max_items,
+                                status);
         return;
     }
     if (cb == 1) {
@@ -528,6 +611,8 @@ int ea_prompt_scratch_init(ea_stream_t stream, ea_prompt_scratch* s, void* base,
     s->xg = b + l.xg;
     s->xu = b + l.xu;
     s->z = b + l.z;
+    s->zp = b + l.zp;
+    s->pclass = b + l.pclass;
     s->rows = l.rows;
     s->slots = slots;
     s->max_items = l.max_items;
@@ -555,9 +640,9 @@ int ea_prompt_experts_run(ea_stream_t stream, const void* x, int x_dtype, uint32
         const char* xs = static_cast<const char*>(x) + (size_t)r0 * xstride * xb;
         const int32_t* pk = pick + (size_t)r0 * S;
         const float* wt = wts + (size_t)r0 * S;
-        route_kernel<<<1, ROUTE_THREADS, 2 * E * sizeof(int), s>>>(pk, (int)pairs, (int)E, dptr<int>(sc->sorted),
+        route_kernel<<<1, ROUTE_THREADS, 3 * E * sizeof(int), s>>>(pk, (int)pairs, (int)E, dptr<int>(sc->sorted),
                                                                   dptr<int>(sc->items), dptr<int>(sc->count),
-                                                                  (int)max_items);
+                                                                  dptr<int>(sc->pclass), (int)max_items);
         int r = launched();
         if (r) return r;
         r = launch_rot_in(s, xs, x_dtype, xstride, pk, dptr<const uint16_t>(ex->suh_g), dptr<const uint16_t>(ex->suh_u),
@@ -566,19 +651,21 @@ int ea_prompt_experts_run(ea_stream_t stream, const void* x, int x_dtype, uint32
         item_gemm_dispatch(s, ex->cb, wide, dptr<const uint16_t>(sc->xg), dptr<const uint16_t>(sc->xu),
                            dptr<const int64_t>(ex->ptr[0]), dptr<const int64_t>(ex->ptr[1]),
                            dptr<const int>(ex->k2[0]), dptr<const int>(ex->k2[1]), dptr<const int>(sc->sorted),
-                           dptr<const int>(sc->items), dptr<const int>(sc->count), dptr<float>(sc->z), (int)D, (int)I,
-                           (int)pairs, 2, max_items, c->status);
+                           dptr<const int>(sc->items), dptr<const int>(sc->count), dptr<float>(sc->z),
+                           wide ? nullptr : dptr<float>(sc->zp), (int)D, (int)I, (int)pairs, 2, max_items, c->status);
         r = launched();
         if (r) return r;
         r = launch_gateup_epilogue(s, dptr<const float>(sc->z), pk, dptr<const uint16_t>(ex->svh_g),
                                    dptr<const uint16_t>(ex->svh_u), dptr<const uint16_t>(ex->suh_d),
-                                   dptr<uint16_t>(sc->xd), n, pairs, I, 1, S, E, __builtin_inff(), 1);
+                                   dptr<uint16_t>(sc->xd), n, pairs, I, 1, S, E, __builtin_inff(), 1,
+                                   wide ? nullptr : dptr<const int>(sc->pclass), dptr<const float>(sc->zp),
+                                   (uint32_t)gu_splits((int)D));
         if (r) return r;
         item_gemm_dispatch(s, ex->cb, wide, dptr<const uint16_t>(sc->xd), dptr<const uint16_t>(sc->xd),
                            dptr<const int64_t>(ex->ptr[2]), dptr<const int64_t>(ex->ptr[2]),
                            dptr<const int>(ex->k2[2]), dptr<const int>(ex->k2[2]), dptr<const int>(sc->sorted),
-                           dptr<const int>(sc->items), dptr<const int>(sc->count), dptr<float>(sc->plane), (int)I,
-                           (int)D, (int)pairs, 1, max_items, c->status);
+                           dptr<const int>(sc->items), dptr<const int>(sc->count), dptr<float>(sc->plane), nullptr,
+                           (int)I, (int)D, (int)pairs, 1, max_items, c->status);
         r = launched();
         if (r) return r;
         // slots without an expert add nothing (the reference's route skips them); fp16 sums go through an fp32

@@ -39,7 +39,8 @@ class MoeScratch(C.Structure):
 
 class PromptScratch(C.Structure):
     _fields_ = [("sorted", U64), ("items", U64), ("count", U64), ("xd", U64), ("plane", U64), ("xg", U64),
-                ("xu", U64), ("z", U64), ("rows", U32), ("slots", U32), ("max_items", U32)]
+                ("xu", U64), ("z", U64), ("zp", U64), ("pclass", U64), ("rows", U32), ("slots", U32),
+                ("max_items", U32)]
 
 
 class Job(C.Structure):

@@ -148,6 +148,7 @@ int ea_moe_routed(ea_stream_t stream, const void* x, int x_dtype, uint32_t x_str
 typedef struct ea_prompt_scratch {
     uint64_t sorted, items, count, xd, plane;  /* plane 0: no deterministic pair plane */
     uint64_t xg, xu, z;                        /* this build's rotated inputs and partial sums */
+    uint64_t zp, pclass;                       /* this build's K-split sums of large items, each pair's item list */
     uint32_t rows, slots, max_items;
 } ea_prompt_scratch;
 
