@@ -147,6 +147,7 @@ const char* ea_strerror(int s) {
         case EA_NOT_INITIALIZED: return "ea_init was not called on this device";
         case EA_BAD_ARGUMENT: return "bad argument";
         case EA_UNSUPPORTED_WIDTH: return "an expert width (K2) or codebook this build has no decoder for";
+        case EA_SYNC_TIMEOUT: return "a kernel's bounded wait on its block's LDS counters gave up";
         default: return "unknown status";
     }
 }
@@ -170,6 +171,12 @@ int ea_init(int device) {
     if (r) return r;
     r = hip_status(hipMemset(c.status, 0, 256));
     if (r) return r;
+    r = hip_status(hipStreamCreateWithFlags(&c.side, hipStreamNonBlocking));
+    if (r) return r;
+    r = hip_status(hipEventCreateWithFlags(&c.fork, hipEventDisableTiming));
+    if (r) return r;
+    r = hip_status(hipEventCreateWithFlags(&c.join, hipEventDisableTiming));
+    if (r) return r;
     r = hip_status(hipDeviceSynchronize());
     if (r) return r;
     c.ready = true;
@@ -183,10 +190,38 @@ int ea_fini(void) {
             hipSetDevice(c.device);
             hipFree(c.status);
             c.status = nullptr;
+            if (c.side) (void)hipStreamDestroy(c.side);
+            if (c.fork) (void)hipEventDestroy(c.fork);
+            if (c.join) (void)hipEventDestroy(c.join);
+            c.side = nullptr;
+            c.fork = c.join = nullptr;
             c.ready = false;
         }
     return EA_OK;
 }
+
+}  // extern "C"
+
+namespace ea {
+static std::mutex g_fork_mu;
+int fork_join(hipStream_t s, const std::function<int(hipStream_t)>& side_work,
+              const std::function<int(hipStream_t)>& main_work) {
+    DevCtx* c = ctx();
+    if (!c || !c->ready) return EA_NOT_INITIALIZED;
+    std::lock_guard<std::mutex> lk(g_fork_mu);
+    int r = hip_status(hipEventRecord(c->fork, s));
+    if (r) return r;
+    r = hip_status(hipStreamWaitEvent(c->side, c->fork, 0));
+    if (r) return r;
+    r = side_work(c->side);
+    const int r2 = main_work(s);  // always issued, so s never waits on a join that is not recorded
+    const int r3 = hip_status(hipEventRecord(c->join, c->side));
+    const int r4 = r3 ? r3 : hip_status(hipStreamWaitEvent(s, c->join, 0));
+    return r ? r : r2 ? r2 : r4;
+}
+}  // namespace ea
+
+extern "C" {
 
 int ea_device_status(int* code) {
     EA_REQUIRE_CTX(c);

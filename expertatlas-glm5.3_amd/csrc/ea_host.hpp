@@ -2,6 +2,8 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+
+#include <functional>
 #include <stdint.h>
 
 #include "ea_exl3.h"
@@ -14,7 +16,16 @@ struct DevCtx {
     int cus = 0;
     size_t lds_optin = 0;
     int* status = nullptr;  // device int: a kernel's recorded error (unsupported width), 0 = none
+    // A second stream (default priority) and two events for launches that run beside the caller's stream inside
+    // one call: fork (side waits for the caller's work so far), join (the caller waits for the side's launches).
+    hipStream_t side = nullptr;
+    hipEvent_t fork = nullptr, join = nullptr;
 };
+
+// Run `side_work(side stream)` beside `main_work(s)`: both start after everything already on s, and s waits for
+// both before anything later. Serialised per device (the side stream and events are shared).
+int fork_join(hipStream_t s, const std::function<int(hipStream_t)>& side_work,
+              const std::function<int(hipStream_t)>& main_work);
 
 // The context of the current device; nullptr before ea_init on it.
 DevCtx* ctx();
@@ -39,7 +50,7 @@ __host__ __device__ inline T* dptr(uint64_t a) {
 int fill_words(hipStream_t s, void* p, uint32_t v, size_t n);
 
 // Device-side error codes written into DevCtx::status.
-enum DeviceError : int { DEV_UNSUPPORTED_WIDTH = EA_UNSUPPORTED_WIDTH };
+enum DeviceError : int { DEV_UNSUPPORTED_WIDTH = EA_UNSUPPORTED_WIDTH, DEV_SYNC_TIMEOUT = EA_SYNC_TIMEOUT };
 
 }  // namespace ea
 

@@ -20,7 +20,7 @@ constexpr int IPM_TILES = IPM / 16;
 constexpr uint32_t CHUNK_ROWS = 4096;  // rows a pass at most (prompt_experts.zig:17)
 constexpr int ROUTE_THREADS = 1024;
 
-constexpr int SMALL_ROWS = 32;     // items of at most this many pairs: the kernels holding two row tiles
+constexpr int SMALL_ROWS = 16;     // items of at most this many pairs: the kernels holding one row tile
 
 // Item i of list `big` (0: items of at most SMALL_ROWS pairs, from the front of items[]; 1: the others, from its
 // back), or false past the list's count.
@@ -234,24 +234,70 @@ __device__ __forceinline__ void item_chunk(const uint32_t* st, const LaneQuad& l
     }
 }
 
+// One chunk for a single row tile with the LDS reads one k step ahead: the trellis words and the activation operand
+// of k step t + 1 are read before k step t decodes, so each read's latency overlaps a step of decoding.
+template <int CB, int K2>
+__device__ __forceinline__ void item_chunk1(const uint32_t* st, const LaneQuad& lq, const uint16_t* xa, int lane,
+                                            f4v (&acc)[1][2], int xs) {
+    constexpr int TW = 4 * K2;
+    const uint32_t* wa = st + lq.w0;
+    const uint32_t* wb = st + lq.w1;
+    const uint16_t* xr = xa + (lane & 15) * xs + 8 * ((lane >> 4) & 3);
+    uint32_t w[2][4][2];  // [buffer][tile: (t, j0), (t + 1, j0), (t, j1), (t + 1, j1)][word]
+    h8v a[2];
+    auto read = [&](int t, int b) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const int o = (2 * (t + h) + j) * TW;
+                w[b][2 * j + h][0] = wa[o];
+                w[b][2 * j + h][1] = wb[o];
+            }
+        a[b] = *reinterpret_cast<const h8v*>(xr + t * 16);
+    };
+    read(0, 0);
+#pragma unroll
+    for (int t = 0; t < PK; t += 2) {
+        const int b = (t >> 1) & 1;
+        if (t + 2 < PK) read(t + 2, b ^ 1);
+        issued();
+        h8v bb[2];
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const u2v b0 = decode_quad<K2, CB>(w[b][2 * j][0], w[b][2 * j][1], lq.sh);
+            const u2v b1 = decode_quad<K2, CB>(w[b][2 * j + 1][0], w[b][2 * j + 1][1], lq.sh);
+            bb[j] = __builtin_bit_cast(h8v, (u4v{b0.x, b0.y, b1.x, b1.y}));
+        }
+        acc[0][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[b], bb[0], acc[0][0], 0, 0, 0);
+        acc[0][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[b], bb[1], acc[0][1], 0, 0, 0);
+    }
+}
+
 // The chunk loop of a gate|up block for one width: the activations one chunk ahead, the trellis two. Loads complete
 // in issue order and every load is issued (a chunk past the last re-reads the last), so the waits stay exact.
 // With FOLD the nch chunks are summed as nsum splits ([s nch / nsum, (s + 1) nch / nsum)), each accumulated from zero
 // and added in order into tot (from zero): the bits of a K-split item's sum of its split planes, so a pair's sums do
 // not depend on which list its item is in. Without FOLD the block's chunks accumulate into acc.
-template <int CB, int K2, int MT, bool FOLD>
+// NB = 1: one activation buffer, two barriers a chunk, activations loaded one chunk ahead. NB = 3: three buffers and
+// one barrier a chunk: chunk c + 1 goes into its buffer before the barrier of chunk c, and that buffer's previous
+// chunk (c - 2) was read before the barrier of chunk c - 1, which every wave has passed; activations are loaded two
+// chunks before they go to LDS (two register sets), like the trellis.
+template <int CB, int K2, int MT, bool FOLD, int NB>
 __device__ __forceinline__ void gu_loop(__amdgpu_buffer_rsrc_t xrs, const uint32_t (&aoff)[MT], const int (&lofs)[MT],
                                         const TileSpan& sp, uint16_t* xa, uint32_t* st, int lane, int q8, int mts,
                                         int c0, int nch, int nsum, f4v (&acc)[MT][2], f4v (&tot)[MT][2]) {
     constexpr int NL = stage_loads_k<PK, K2>();
+    constexpr int BUF = MT * 16 * PXS;
     const LaneQuad lq = lane_quad_k<K2>(lane);
-    u4v av[MT], ta[NL], tb[NL];
-    int sn = 1;  // the next split's index
-    auto issue_a = [&](int c) {
+    u4v av[MT], aw[MT], ta[NL], tb[NL];
+    int sn = 1;   // the next split's index
+    int cur = 0;  // the buffer of the current chunk (NB = 3)
+    auto issue_a = [&](int c, u4v (&v)[MT]) {
         c = c0 + (c < nch ? c : nch - 1);
 #pragma unroll
         for (int i = 0; i < MT; ++i)
-            av[i] = __builtin_bit_cast(u4v, __builtin_amdgcn_raw_buffer_load_b128(xrs, aoff[i], c * PK * 32, 0));
+            v[i] = __builtin_bit_cast(u4v, __builtin_amdgcn_raw_buffer_load_b128(xrs, aoff[i], c * PK * 32, 0));
     };
     auto issue_t = [&](int c, u4v (&tv)[NL]) {
         c = c0 + (c < nch ? c : nch - 1);
@@ -259,16 +305,29 @@ __device__ __forceinline__ void gu_loop(__amdgpu_buffer_rsrc_t xrs, const uint32
         sc.off = sp.off + c * PK * sp.kstride;
         stage_issue_k<PK, K2>(sc, lane, tv);
     };
-    auto step = [&](int c, u4v (&tv)[NL]) {
-        __syncthreads();  // the previous chunk's reads of xa are done
+    auto step = [&](int c, u4v (&tv)[NL], u4v (&v)[MT]) {
+        if constexpr (NB == 1) {
+            __syncthreads();  // the previous chunk's reads of xa are done
 #pragma unroll
-        for (int i = 0; i < MT; ++i)
-            if (i < mts) put_a(xa + lofs[i], q8, av[i]);
-        stage_store_k<PK, K2>(st, lane, tv);  // only this wave reads its region, in order
-        issue_a(c + 1);
-        issue_t(c + 2, tv);
-        __syncthreads();  // the chunk's activations are in LDS
-        item_chunk<CB, K2, MT>(st, lq, xa, mts, lane, acc, PXS);
+            for (int i = 0; i < MT; ++i)
+                if (i < mts) put_a(xa + lofs[i], q8, av[i]);
+            stage_store_k<PK, K2>(st, lane, tv);  // only this wave reads its region, in order
+            issue_a(c + 1, av);
+            issue_t(c + 2, tv);
+            __syncthreads();  // the chunk's activations are in LDS
+            item_chunk<CB, K2, MT>(st, lq, xa, mts, lane, acc, PXS);
+        } else {
+            const int nxt = cur == NB - 1 ? 0 : cur + 1;
+#pragma unroll
+            for (int i = 0; i < MT; ++i)
+                if (i < mts) put_a(xa + nxt * BUF + lofs[i], q8, v[i]);  // chunk c + 1
+            stage_store_k<PK, K2>(st, lane, tv);
+            issue_a(c + 3, v);
+            issue_t(c + 2, tv);
+            __syncthreads();
+            item_chunk<CB, K2, MT>(st, lq, xa + cur * BUF, mts, lane, acc, PXS);
+            cur = nxt;
+        }
         if constexpr (FOLD) {
             if (c + 1 == sn * nch / nsum) {  // the end of a split (uniform)
 #pragma unroll
@@ -282,13 +341,27 @@ __device__ __forceinline__ void gu_loop(__amdgpu_buffer_rsrc_t xrs, const uint32
             }
         }
     };
-    issue_t(0, ta);
-    issue_t(1, tb);
-    issue_a(0);
-    for (int c = 0; c < nch; c += 2) {
-        step(c, ta);
-        if (c + 1 < nch) step(c + 1, tb);  // uniform
+    if constexpr (NB == 1) {
+        issue_t(0, ta);
+        issue_t(1, tb);
+        issue_a(0, av);
+    } else {
+        issue_a(0, av);
+#pragma unroll
+        for (int i = 0; i < MT; ++i)
+            if (i < mts) put_a(xa + lofs[i], q8, av[i]);  // chunk 0 into buffer 0 (the first barrier publishes it)
+        issue_a(1, av);
+        issue_t(0, ta);
+        issue_a(2, aw);
+        issue_t(1, tb);
     }
+    // two steps an iteration with no exit between them, so every load's wait is counted the same on each pass
+    int c = 0;
+    for (; c + 1 < nch; c += 2) {
+        step(c, ta, av);
+        step(c + 1, tb, aw);
+    }
+    if (c < nch) step(c, ta, av);  // uniform
 }
 
 // Block (item of list MT > 2, 128 columns, (matrix, K split)): the item's rows (up to MT row tiles) times its
@@ -311,9 +384,11 @@ item_gu_kernel(const uint16_t* __restrict__ X0, const uint16_t* __restrict__ X1,
     const uint16_t* X = mat ? X1 : X0;
     const uint32_t* T = reinterpret_cast<const uint32_t*>(mat ? TP1[e] : TP0[e]);
     const int k2 = mat ? K2_1[e] : K2_0[e];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    // the wave index in a scalar register: the trellis offsets built from it are then scalar (a buffer load's soffset)
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     __shared__ int pair_sh[MT * 16];
-    __shared__ __attribute__((aligned(16))) uint16_t xa[MT * 16 * PXS];
+    constexpr int NB = MT <= 2 ? 3 : 1;
+    __shared__ __attribute__((aligned(16))) uint16_t xa[NB * MT * 16 * PXS];
     __shared__ __attribute__((aligned(16))) uint32_t st[PW][PSTAGE];
     if (tid < MT * 16) pair_sh[tid] = tid < cnt ? sorted[first + tid] : -1;
     __syncthreads();
@@ -344,8 +419,8 @@ item_gu_kernel(const uint16_t* __restrict__ X0, const uint16_t* __restrict__ X1,
     const int nch = K / (PK * 16);
     const int c0 = split * nch / nsplit, nc = (split + 1) * nch / nsplit - c0;  // nsplit <= nch: nc >= 1
     const bool ok = EA_K2_SWITCH(k2, 2, 10,
-                                 (gu_loop<CB, K2V, MT, FOLD>(xrs, aoff, lofs, sp, xa, st[wave], lane, tid & 15, mts, c0,
-                                                             nc, nsum, acc, tot)));
+                                 (gu_loop<CB, K2V, MT, FOLD, NB>(xrs, aoff, lofs, sp, xa, st[wave], lane, tid & 15, mts,
+                                                                 c0, nc, nsum, acc, tot)));
     if (!ok) {
         if (lane == 0) record_error(status, DEV_UNSUPPORTED_WIDTH);
         return;
@@ -363,6 +438,171 @@ item_gu_kernel(const uint16_t* __restrict__ X0, const uint16_t* __restrict__ X1,
         }
 }
 
+// Items of at most 16 pairs: a block is NW waves, one a column-tile pair of one matrix, over all of K. The block's
+// waves share each chunk of activations through a ring of RING_S chunk slots in LDS, filled and freed with LDS
+// counters instead of barriers, so a wave can run up to RING_S - RING_L - 1 chunks ahead of the slowest:
+//   filled[s]: pieces stored into slot s, over all the chunks it has held (NW a chunk);
+//   done[s]:   waves that have finished a chunk of slot s, over all its chunks (NW a chunk).
+// At its step c a wave stores its piece of chunk p = c + RING_L into slot p % RING_S once every wave is done with
+// that slot's previous chunk (done >= NW (p / RING_S)), waits until chunk c is complete in its slot
+// (filled >= NW (c / RING_S + 1)), computes it, and counts itself done. The slowest wave can always go on (every
+// chunk it waits for was stored at a step no later than its own, and every slot it stores into was freed before),
+// so every wait ends. Each wave's trellis goes through its own LDS region as in gu_loop; the activation piece of a
+// chunk (1/NW of it) and the trellis are loaded two chunks ahead. The chunks are summed as nsum splits (gu_loop).
+constexpr int RING_S = 6;  // activation chunk slots
+constexpr int RING_L = 2;  // a wave stores its piece of chunk c + RING_L at its step c
+
+template <int NW>
+struct RingPiece {  // a lane's words of a chunk: 16 rows x 64 words over NW waves
+    static constexpr int WORDS = 16 * 64 / (NW * 64);
+};
+
+__device__ __forceinline__ int lds_load_acquire(const int* p) {
+    return __hip_atomic_load(p, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+// One count for the whole wave: only its first lane adds (the wait before the add covers every lane's accesses).
+__device__ __forceinline__ void lds_add_release(int* p, int v, int lane) {
+    if (lane == 0) __hip_atomic_fetch_add(p, v, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+// Wait until *p >= target. Every count waited for is reached (see above); the wait is still bounded (about 2^20
+// sleeps, tens of milliseconds): past the bound it gives up, returns false and the kernel reports EA_SYNC_TIMEOUT.
+__device__ __forceinline__ bool lds_wait_geq(const int* p, int target) {
+    for (int n = 0; lds_load_acquire(p) < target; ++n) {
+        if (n >= (1 << 20)) return false;
+        __builtin_amdgcn_s_sleep(1);
+    }
+    return true;
+}
+
+template <int CB, int K2, int NW>
+__device__ __forceinline__ void ring_loop(__amdgpu_buffer_rsrc_t xrs, uint32_t aoff, int lofs, const TileSpan& sp,
+                                          uint16_t* ring, int* filled, int* done, uint32_t* st, int lane, int nch,
+                                          int nsum, f4v (&acc)[1][2], f4v (&tot)[1][2], bool& synced) {
+    constexpr int NL = stage_loads_k<PK, K2>();
+    constexpr int W = RingPiece<NW>::WORDS;  // 2 or 4
+    constexpr int SLOT = 16 * PXS;
+    using pv = uint32_t __attribute__((ext_vector_type(W)));
+    const LaneQuad lq = lane_quad_k<K2>(lane);
+    pv pa, pb;
+    u4v ta[NL], tb[NL];
+    int sn = 1;  // the next split's index
+    auto issue_p = [&](int c, pv& v) {
+        c = c < nch ? c : nch - 1;
+        if constexpr (W == 4)
+            v = __builtin_bit_cast(pv, __builtin_amdgcn_raw_buffer_load_b128(xrs, aoff, c * PK * 32, 0));
+        else
+            v = __builtin_bit_cast(pv, __builtin_amdgcn_raw_buffer_load_b64(xrs, aoff, c * PK * 32, 0));
+    };
+    auto issue_t = [&](int c, u4v (&tv)[NL]) {
+        c = c < nch ? c : nch - 1;
+        TileSpan sc = sp;
+        sc.off = sp.off + c * PK * sp.kstride;
+        stage_issue_k<PK, K2>(sc, lane, tv);
+    };
+    // the piece's words d .. d + W - 1 of its row (d = lofs & 63) at their transposed places (see put_a)
+    auto put = [&](int p, const pv& v) {
+        const int sl = p % RING_S;
+        synced = synced && lds_wait_geq(&done[sl], NW * (p / RING_S));  // after a give-up no more waits
+        uint32_t* w = reinterpret_cast<uint32_t*>(ring + sl * SLOT + (lofs >> 6) * PXS);
+        const int d = lofs & 63;
+#pragma unroll
+        for (int r = 0; r < W; ++r) {
+            const int dd = (d & 15) + r;  // word within its 32-k step
+            w[16 * (d >> 4) + 4 * (dd & 3) + (dd >> 2)] = v[r];
+        }
+        lds_add_release(&filled[sl], 1, lane);
+    };
+    auto step = [&](int c, u4v (&tv)[NL], pv& v) {
+        if (c + RING_L < nch) put(c + RING_L, v);  // uniform
+        issue_p(c + RING_L + 2, v);
+        stage_store_k<PK, K2>(st, lane, tv);
+        issue_t(c + 2, tv);
+        const int sl = c % RING_S;
+        synced = synced && lds_wait_geq(&filled[sl], NW * (c / RING_S + 1));
+        item_chunk1<CB, K2>(st, lq, ring + sl * SLOT, lane, acc, PXS);
+        lds_add_release(&done[sl], 1, lane);  // after the chunk's reads of the slot have returned
+        if (c + 1 == sn * nch / nsum) {  // the end of a split (uniform)
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                tot[0][j] += acc[0][j];
+                acc[0][j] = f4v{0.f, 0.f, 0.f, 0.f};
+            }
+            ++sn;
+        }
+    };
+    // chunks 0 .. RING_L - 1 go in before the loop; pa / pb then carry chunks RING_L and RING_L + 1
+    for (int p = 0; p < RING_L && p < nch; ++p) {
+        pv v;
+        issue_p(p, v);
+        put(p, v);
+    }
+    issue_p(RING_L, pa);
+    issue_t(0, ta);
+    issue_p(RING_L + 1, pb);
+    issue_t(1, tb);
+    int c = 0;
+    for (; c + 1 < nch; c += 2) {  // two steps an iteration with no exit between them
+        step(c, ta, pa);
+        step(c + 1, tb, pb);
+    }
+    if (c < nch) step(c, ta, pa);  // uniform
+}
+
+template <int CB, int NW>
+__global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(4)))
+item_ring_kernel(const uint16_t* __restrict__ X0, const uint16_t* __restrict__ X1, const int64_t* __restrict__ TP0,
+                 const int64_t* __restrict__ TP1, const int* __restrict__ K2_0, const int* __restrict__ K2_1,
+                 const int* __restrict__ sorted, const int* __restrict__ items, const int* __restrict__ item_count,
+                 float* __restrict__ Z, int K, int N, int P, int nsum, int max_items, int* __restrict__ status) {
+    int e, first, cnt;
+    if (!item_at(items, item_count, 0, max_items, blockIdx.x, e, first, cnt)) return;
+    const int mat = blockIdx.z;
+    const uint16_t* X = mat ? X1 : X0;
+    const uint32_t* T = reinterpret_cast<const uint32_t*>(mat ? TP1[e] : TP0[e]);
+    const int k2 = mat ? K2_1[e] : K2_0[e];
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    __shared__ int pair_sh[16];
+    __shared__ int filled[RING_S], done[RING_S];
+    __shared__ __attribute__((aligned(16))) uint16_t ring[RING_S * 16 * PXS];
+    __shared__ __attribute__((aligned(16))) uint32_t st[NW][PSTAGE];
+    if (threadIdx.x < 16) pair_sh[threadIdx.x] = (int)threadIdx.x < cnt ? sorted[first + threadIdx.x] : -1;
+    if (threadIdx.x < RING_S) filled[threadIdx.x] = done[threadIdx.x] = 0;
+    __syncthreads();
+    // this lane's piece of every chunk: words [d, d + W) of row r (word index lofs = 64 r + d over the chunk);
+    // a row past the count reads the first pair's row
+    constexpr int W = RingPiece<NW>::WORDS;
+    const int lofs = (wave * 64 + lane) * W;
+    const int row = lofs >> 6;
+    const int p = pair_sh[row] >= 0 ? pair_sh[row] : pair_sh[0];
+    const uint32_t aoff = ((uint32_t)p * (uint32_t)K + 2u * (uint32_t)(lofs & 63)) * 2u;
+    const __amdgpu_buffer_rsrc_t xrs = buffer_rsrc(X, (uint32_t)((size_t)P * K * 2));
+    const int nt0 = blockIdx.y * (2 * NW) + 2 * wave;
+    const int ns = N >> 4, TWB = 16 * k2;
+    TileSpan sp;
+    sp.r = buffer_rsrc(T, (uint32_t)((K >> 4) * ns * TWB));
+    sp.off = nt0 * TWB;
+    sp.kstride = ns * TWB;
+    f4v acc[1][2], tot[1][2];
+    acc[0][0] = acc[0][1] = tot[0][0] = tot[0][1] = f4v{0.f, 0.f, 0.f, 0.f};
+    const int nch = K / (PK * 16);
+    bool synced = true;
+    const bool ok = EA_K2_SWITCH(k2, 2, 10,
+                                 (ring_loop<CB, K2V, NW>(xrs, aoff, lofs, sp, ring, filled, done, st[wave], lane, nch,
+                                                         nsum, acc, tot, synced)));
+    if (!ok || !synced) {
+        if (lane == 0) record_error(status, ok ? DEV_SYNC_TIMEOUT : DEV_UNSUPPORTED_WIDTH);
+        return;
+    }
+    float* Zm = Z + (size_t)mat * P * N;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int pp = pair_sh[4 * (lane >> 4) + i];
+        if (pp < 0) continue;
+#pragma unroll
+        for (int j = 0; j < 2; ++j) Zm[(size_t)pp * N + (nt0 + j) * 16 + (lane & 15)] = tot[0][j][i];
+    }
+}
+
 // The column blocks of a down block for one width: step s is column block s / nch, chunk s % nch; the trellis two
 // steps ahead; each column block's rows are stored when its last chunk is done.
 template <int CB, int K2, int MT, int NG>
@@ -372,6 +612,7 @@ __device__ __forceinline__ void dn_loop(const TileSpan& sp, const uint16_t* xa, 
     constexpr int TWB = 16 * K2;
     const LaneQuad lq = lane_quad_k<K2>(lane);
     const int steps = NG * nch;
+    static_assert(NG % 2 == 0, "two steps an iteration");
     u4v ta[NL], tb[NL];
     f4v acc[MT][2];
     auto issue_t = [&](int s2, u4v (&tv)[NL]) {
@@ -404,9 +645,9 @@ __device__ __forceinline__ void dn_loop(const TileSpan& sp, const uint16_t* xa, 
     };
     issue_t(0, ta);
     issue_t(1, tb);
-    for (int s2 = 0; s2 < steps; s2 += 2) {
+    for (int s2 = 0; s2 < steps; s2 += 2) {  // steps = NG nch is even: two steps an iteration, no exit between
         step(s2, ta);
-        if (s2 + 1 < steps) step(s2 + 1, tb);  // uniform
+        step(s2 + 1, tb);
     }
 }
 
@@ -421,7 +662,8 @@ item_dn_kernel(const uint16_t* __restrict__ X, const int64_t* __restrict__ TP, c
     if (!item_at(items, item_count, MT > 2, max_items, blockIdx.x, e, first, cnt)) return;
     const uint32_t* T = reinterpret_cast<const uint32_t*>(TP[e]);
     const int k2 = K2T[e];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    // the wave index in a scalar register: the trellis offsets built from it are then scalar (a buffer load's soffset)
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     __shared__ int pair_sh[MT * 16];
     __shared__ __attribute__((aligned(16))) uint16_t xa[MT * 16 * DXS];
     __shared__ __attribute__((aligned(16))) uint32_t st[PW][PSTAGE];
@@ -515,45 +757,63 @@ static void item_gemm(hipStream_t s, const uint16_t* X0, const uint16_t* X1, con
                                                                        Z, K, N, P, big, (int)max_items, status);
 }
 
-// Both item lists, the larger items first (their blocks run longest).
-// Both item lists, the larger items first. The down matrix takes the resident-activation kernel when its K and N fit,
-// anything else the chunked one, with the larger items' K split into Zp when Zp is given.
+// Both item lists at once: the larger items on the side stream, the small ones on s (the two kernels fill each
+// other's idle CUs: the small items' blocks leave room on many CUs, the larger items' blocks are few and long). The
+// down matrix takes the resident-activation kernels when its K and N fit, anything else the chunked ones, with the
+// larger items' K split into Zp when Zp is given.
 template <int CB>
-static void item_gemm_staged(hipStream_t s, const uint16_t* X0, const uint16_t* X1, const int64_t* TP0,
-                             const int64_t* TP1, const int* B0, const int* B1, const int* sorted, const int* items,
-                             const int* count, float* Z, float* Zp, int K, int N, int P, int mats, uint32_t max_items,
-                             int* status) {
+static int item_gemm_staged(hipStream_t s, const uint16_t* X0, const uint16_t* X1, const int64_t* TP0,
+                            const int64_t* TP1, const int* B0, const int* B1, const int* sorted, const int* items,
+                            const int* count, float* Z, float* Zp, int K, int N, int P, int mats, uint32_t max_items,
+                            int* status) {
     const int mi = (int)max_items;
     if (mats == 1 && K <= 2 * PK * 16 && (N / 128) % DNG == 0) {  // the down matrix
-        item_dn_kernel<CB, IPM_TILES, DNG_BIG><<<dim3(max_items, N / 128 / DNG_BIG, 1), PW * 64, 0, s>>>(
-            X0, TP0, B0, sorted, items, count, Z, K, N, P, mi, status);
-        item_dn_kernel<CB, SMALL_ROWS / 16, DNG><<<dim3(max_items, N / 128 / DNG, 1), PW * 64, 0, s>>>(
-            X0, TP0, B0, sorted, items, count, Z, K, N, P, mi, status);
-        return;
+        return fork_join(
+            s,
+            [&](hipStream_t q) {
+                item_dn_kernel<CB, IPM_TILES, DNG_BIG><<<dim3(max_items, N / 128 / DNG_BIG, 1), PW * 64, 0, q>>>(
+                    X0, TP0, B0, sorted, items, count, Z, K, N, P, mi, status);
+                return launched();
+            },
+            [&](hipStream_t q) {
+                item_dn_kernel<CB, SMALL_ROWS / 16, DNG><<<dim3(max_items, N / 128 / DNG, 1), PW * 64, 0, q>>>(
+                    X0, TP0, B0, sorted, items, count, Z, K, N, P, mi, status);
+                return launched();
+            });
     }
     const int ns = Zp ? gu_splits(K) : 1;
-    item_gu_kernel<CB, IPM_TILES><<<dim3(max_items, N / (16 * 2 * PW), mats * ns), PW * 64, 0, s>>>(
-        X0, X1, TP0, TP1, B0, B1, sorted, items, count, Z, Zp, K, N, P, ns, 1, mi, status);
-    item_gu_kernel<CB, SMALL_ROWS / 16><<<dim3(max_items, N / (16 * 2 * PW), mats), PW * 64, 0, s>>>(
-        X0, X1, TP0, TP1, B0, B1, sorted, items, count, Z, Zp, K, N, P, 1, ns, mi, status);
+    return fork_join(
+        s,
+        [&](hipStream_t q) {
+            item_gu_kernel<CB, IPM_TILES><<<dim3(max_items, N / (16 * 2 * PW), mats * ns), PW * 64, 0, q>>>(
+                X0, X1, TP0, TP1, B0, B1, sorted, items, count, Z, Zp, K, N, P, ns, 1, mi, status);
+            return launched();
+        },
+        [&](hipStream_t q) {
+            if (N % 256 == 0)
+                item_ring_kernel<CB, 8><<<dim3(max_items, N / 256, mats), 8 * 64, 0, q>>>(
+                    X0, X1, TP0, TP1, B0, B1, sorted, items, count, Z, K, N, P, ns, mi, status);
+            else  // N a multiple of 128
+                item_ring_kernel<CB, 4><<<dim3(max_items, N / 128, mats), 4 * 64, 0, q>>>(
+                    X0, X1, TP0, TP1, B0, B1, sorted, items, count, Z, K, N, P, ns, mi, status);
+            return launched();
+        });
 }
 
 // Widths up to 10 take the staged GEMM; wider ones (three trellis words a lane) the register-streaming one.
-static void item_gemm_dispatch(hipStream_t s, uint32_t cb, bool wide, const uint16_t* X0, const uint16_t* X1,
-                               const int64_t* TP0, const int64_t* TP1, const int* B0, const int* B1,
-                               const int* sorted, const int* items, const int* count, float* Z, float* Zp, int K,
-                               int N, int P, int mats, uint32_t max_items, int* status) {
+static int item_gemm_dispatch(hipStream_t s, uint32_t cb, bool wide, const uint16_t* X0, const uint16_t* X1,
+                              const int64_t* TP0, const int64_t* TP1, const int* B0, const int* B1, const int* sorted,
+                              const int* items, const int* count, float* Z, float* Zp, int K, int N, int P, int mats,
+                              uint32_t max_items, int* status) {
     if (!wide) {
         if (cb == 1)
-            item_gemm_staged<1>(s, X0, X1, TP0, TP1, B0, B1, sorted, items, count, Z, Zp, K, N, P, mats, max_items,
-                                status);
-        else if (cb == 2)
-            item_gemm_staged<2>(s, X0, X1, TP0, TP1, B0, B1, sorted, items, count, Z, Zp, K, N, P, mats, max_items,
-                                status);
-        else
-            item_gemm_staged<0>(s, X0, X1, TP0, TP1, B0, B1, sorted, items, count, Z, Zp, K, N, P, mats, max_items,
-                                status);
-        return;
+            return item_gemm_staged<1>(s, X0, X1, TP0, TP1, B0, B1, sorted, items, count, Z, Zp, K, N, P, mats,
+                                       max_items, status);
+        if (cb == 2)
+            return item_gemm_staged<2>(s, X0, X1, TP0, TP1, B0, B1, sorted, items, count, Z, Zp, K, N, P, mats,
+                                       max_items, status);
+        return item_gemm_staged<0>(s, X0, X1, TP0, TP1, B0, B1, sorted, items, count, Z, Zp, K, N, P, mats, max_items,
+                                   status);
     }
     if (cb == 1) {
         item_gemm<1, 2, 16>(s, X0, X1, TP0, TP1, B0, B1, sorted, items, count, Z, K, N, P, mats, max_items, status);
@@ -562,6 +822,7 @@ static void item_gemm_dispatch(hipStream_t s, uint32_t cb, bool wide, const uint
     } else {
         item_gemm<0, 2, 16>(s, X0, X1, TP0, TP1, B0, B1, sorted, items, count, Z, K, N, P, mats, max_items, status);
     }
+    return launched();
 }
 
 }  // namespace ea
@@ -648,12 +909,11 @@ int ea_prompt_experts_run(ea_stream_t stream, const void* x, int x_dtype, uint32
         r = launch_rot_in(s, xs, x_dtype, xstride, pk, dptr<const uint16_t>(ex->suh_g), dptr<const uint16_t>(ex->suh_u),
                           dptr<uint16_t>(sc->xg), dptr<uint16_t>(sc->xu), n, D, S, E);
         if (r) return r;
-        item_gemm_dispatch(s, ex->cb, wide, dptr<const uint16_t>(sc->xg), dptr<const uint16_t>(sc->xu),
+        r = item_gemm_dispatch(s, ex->cb, wide, dptr<const uint16_t>(sc->xg), dptr<const uint16_t>(sc->xu),
                            dptr<const int64_t>(ex->ptr[0]), dptr<const int64_t>(ex->ptr[1]),
                            dptr<const int>(ex->k2[0]), dptr<const int>(ex->k2[1]), dptr<const int>(sc->sorted),
                            dptr<const int>(sc->items), dptr<const int>(sc->count), dptr<float>(sc->z),
                            wide ? nullptr : dptr<float>(sc->zp), (int)D, (int)I, (int)pairs, 2, max_items, c->status);
-        r = launched();
         if (r) return r;
         r = launch_gateup_epilogue(s, dptr<const float>(sc->z), pk, dptr<const uint16_t>(ex->svh_g),
                                    dptr<const uint16_t>(ex->svh_u), dptr<const uint16_t>(ex->suh_d),
@@ -661,12 +921,11 @@ int ea_prompt_experts_run(ea_stream_t stream, const void* x, int x_dtype, uint32
                                    wide ? nullptr : dptr<const int>(sc->pclass), dptr<const float>(sc->zp),
                                    (uint32_t)gu_splits((int)D));
         if (r) return r;
-        item_gemm_dispatch(s, ex->cb, wide, dptr<const uint16_t>(sc->xd), dptr<const uint16_t>(sc->xd),
+        r = item_gemm_dispatch(s, ex->cb, wide, dptr<const uint16_t>(sc->xd), dptr<const uint16_t>(sc->xd),
                            dptr<const int64_t>(ex->ptr[2]), dptr<const int64_t>(ex->ptr[2]),
                            dptr<const int>(ex->k2[2]), dptr<const int>(ex->k2[2]), dptr<const int>(sc->sorted),
                            dptr<const int>(sc->items), dptr<const int>(sc->count), dptr<float>(sc->plane), nullptr,
                            (int)I, (int)D, (int)pairs, 1, max_items, c->status);
-        r = launched();
         if (r) return r;
         // slots without an expert add nothing (the reference's route skips them); fp16 sums go through an fp32
         // staging buffer (xg, free by now)

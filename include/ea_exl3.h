@@ -44,7 +44,8 @@ typedef enum ea_status {
     EA_OUT_OF_DEVICE_MEMORY = 16,     /* driver.zig error.OutOfDeviceMemory */
     EA_NOT_INITIALIZED = 17,          /* a call before ea_init on this device */
     EA_BAD_ARGUMENT = 18,             /* a null pointer or a size outside the documented range */
-    EA_UNSUPPORTED_WIDTH = 19         /* a K2 / codebook this build has no decoder for */
+    EA_UNSUPPORTED_WIDTH = 19,        /* a K2 / codebook this build has no decoder for */
+    EA_SYNC_TIMEOUT = 20              /* a kernel's bounded wait on its block's LDS counters gave up */
 } ea_status;
 
 enum { EA_F16 = 0, EA_BF16 = 1, EA_F32 = 2 };
