@@ -74,50 +74,53 @@ __global__ void __launch_bounds__(GROUP_THREADS) group_kernel(const int* __restr
 }
 
 // ---- per-pair input rotation ------------------------------------------------------------------------------------
-// Block (pair p, matrix): 16 lanes a 128-block of K, lane l holding its values 8 (l & 15) .. +7; a thread steps
-// through K 2048 values at a time. out[p] = fp16((x[row] * suh[e]) @ H * HAD_SCALE) (exl3_experts.cu:116-134). The
-// butterflies run over value-index bits 0..6 in that order (three inside a lane, four across lanes), as in a
-// one-lane-pair-a-value layout, so each output is the same fp32 sum rounded the same way.
+// Block (row, matrix, 2048 columns of K): 16 lanes a 128-block, lane l holding its values 8 (l & 15) .. +7; the row's
+// activations are read once and rotated for each of its slots in turn. out[p] = fp16((x[row] * suh[e]) @ H *
+// HAD_SCALE) for each pair p of the row with an expert (exl3_experts.cu:116-134). The butterflies run over value-index
+// bits 0..6 in that order (three inside a lane, four across lanes), as in a one-lane-pair-a-value layout, so each
+// output is the same fp32 sum rounded the same way.
 __global__ void __launch_bounds__(256) rot_in_kernel(const void* __restrict__ x, int x_dtype, int x_stride,
                                                      const int* __restrict__ pick, const uint16_t* __restrict__ suh0,
                                                      const uint16_t* __restrict__ suh1, uint16_t* __restrict__ out0,
                                                      uint16_t* __restrict__ out1, int K, int slots, int E, int vec) {
-    const int p = blockIdx.x, mat = blockIdx.y;
-    const int e = pick[p];
-    if (e < 0 || e >= E) return;
-    const int row = p / slots, lane = threadIdx.x & 63;
-    const uint16_t* suh = (mat ? suh1 : suh0) + (size_t)e * K;
-    uint16_t* o = (mat ? out1 : out0) + (size_t)p * K;
+    const int row = blockIdx.x, mat = blockIdx.y, lane = threadIdx.x & 63;
+    const int k = blockIdx.z * 2048 + 8 * (int)threadIdx.x;
+    if (k >= K) return;  // whole 16-lane groups (K % 128 == 0)
+    const uint16_t* suh = mat ? suh1 : suh0;
+    uint16_t* out = mat ? out1 : out0;
     const size_t xr = (size_t)row * x_stride;
     // v' = s * v + o: o - v for the lane holding the upper element of a butterfly, v + o otherwise (exact: s = +-1)
     const float s1 = lane & 1 ? -1.f : 1.f, s2 = lane & 2 ? -1.f : 1.f, s4 = lane & 4 ? -1.f : 1.f,
                 s8 = lane & 8 ? -1.f : 1.f;
-    for (int k = 8 * (int)threadIdx.x; k < K; k += 2048) {  // uniform across each 16-lane group (K % 128 == 0)
-        float v[8];
-        if (vec) {  // 16-byte aligned rows
-            if (x_dtype == F32) {
-                const f4v a = *reinterpret_cast<const f4v*>(static_cast<const float*>(x) + xr + k);
-                const f4v b = *reinterpret_cast<const f4v*>(static_cast<const float*>(x) + xr + k + 4);
+    float xv[8];
+    if (vec) {  // 16-byte aligned rows
+        if (x_dtype == F32) {
+            const f4v a = *reinterpret_cast<const f4v*>(static_cast<const float*>(x) + xr + k);
+            const f4v b = *reinterpret_cast<const f4v*>(static_cast<const float*>(x) + xr + k + 4);
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    v[j] = a[j];
-                    v[4 + j] = b[j];
-                }
-            } else {
-                const u4v w = *reinterpret_cast<const u4v*>(static_cast<const uint16_t*>(x) + xr + k);
-#pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    const uint16_t h = (uint16_t)(w[j >> 1] >> (16 * (j & 1)));
-                    v[j] = x_dtype == BF16 ? bf2f(h) : h2f(h);
-                }
+            for (int j = 0; j < 4; ++j) {
+                xv[j] = a[j];
+                xv[4 + j] = b[j];
             }
         } else {
+            const u4v w = *reinterpret_cast<const u4v*>(static_cast<const uint16_t*>(x) + xr + k);
 #pragma unroll
-            for (int j = 0; j < 8; ++j) v[j] = load_act(x, x_dtype, xr + k + j);
+            for (int j = 0; j < 8; ++j) {
+                const uint16_t h = (uint16_t)(w[j >> 1] >> (16 * (j & 1)));
+                xv[j] = x_dtype == BF16 ? bf2f(h) : h2f(h);
+            }
         }
-        const u4v sw = *reinterpret_cast<const u4v*>(suh + k);
+    } else {
 #pragma unroll
-        for (int j = 0; j < 8; ++j) v[j] *= h2f((uint16_t)(sw[j >> 1] >> (16 * (j & 1))));
+        for (int j = 0; j < 8; ++j) xv[j] = load_act(x, x_dtype, xr + k + j);
+    }
+    for (int q = 0; q < slots; ++q) {
+        const int p = row * slots + q, e = pick[p];
+        if (e < 0 || e >= E) continue;  // uniform over the block
+        const u4v sw = *reinterpret_cast<const u4v*>(suh + (size_t)e * K + k);
+        float v[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = xv[j] * h2f((uint16_t)(sw[j >> 1] >> (16 * (j & 1))));
 #pragma unroll
         for (int b = 1; b < 8; b <<= 1)
 #pragma unroll
@@ -139,7 +142,7 @@ __global__ void __launch_bounds__(256) rot_in_kernel(const void* __restrict__ x,
 #pragma unroll
         for (int j = 0; j < 4; ++j)
             w[j] = (uint32_t)f2h(v[2 * j] * HAD_SCALE) | ((uint32_t)f2h(v[2 * j + 1] * HAD_SCALE) << 16);
-        *reinterpret_cast<u4v*>(o + k) = w;
+        *reinterpret_cast<u4v*>(out + (size_t)p * K + k) = w;
     }
 }
 
@@ -339,7 +342,7 @@ int launch_rot_in(hipStream_t s, const void* x, int x_dtype, uint32_t x_stride, 
     if (rows * slots == 0) return EA_OK;
     const size_t eb = x_dtype == F32 ? 4 : 2;
     const int vec = (reinterpret_cast<uintptr_t>(x) & 15) == 0 && ((size_t)x_stride * eb) % 16 == 0;
-    dim3 grid(rows * slots, 2);
+    dim3 grid(rows, 2, (kdim + 2047) / 2048);
     rot_in_kernel<<<grid, 256, 0, s>>>(x, x_dtype, (int)x_stride, pick, suh0, suh1, out0, out1, (int)kdim,
                                        (int)slots, (int)experts, vec);
     return launched();

@@ -703,6 +703,68 @@ item_dn_kernel(const uint16_t* __restrict__ X, const int64_t* __restrict__ TP, c
     if (!ok && lane == 0) record_error(status, DEV_UNSUPPORTED_WIDTH);
 }
 
+// The down epilogue and slot combine of a prompt pass. Block (row r, 2048 columns): a thread holds 8 consecutive
+// columns of one 128-block (16 lanes a block); for each slot in order y = FWHT(plane[pair]) * HAD_SCALE * svh_d[e],
+// then out = fma(w, y, out) from zero, a slot without an expert adding w * 0. These are the operations and the order of
+// down_combine_kernel with one split (the butterflies over value-index bits 0..6, three inside a lane and four
+// across lanes), so the same bits; the rotated plane is not written back (nothing reads it after the combine).
+// (prompt_experts.cu's deterministic combine; exl3_experts.cu:186-214 for the epilogue.)
+__global__ void __launch_bounds__(256) prompt_combine_kernel(const float* __restrict__ Z, const int* __restrict__ pick,
+                                                             const uint16_t* __restrict__ svh_d,
+                                                             const float* __restrict__ wts, float* __restrict__ out,
+                                                             int D, int E, int slots) {
+    const int r = blockIdx.x, lane = threadIdx.x & 63;
+    const int k = blockIdx.y * 2048 + 8 * (int)threadIdx.x;
+    if (k >= D) return;  // whole 16-lane groups (D % 128 == 0)
+    const float s1 = lane & 1 ? -1.f : 1.f, s2 = lane & 2 ? -1.f : 1.f, s4 = lane & 4 ? -1.f : 1.f,
+                s8 = lane & 8 ? -1.f : 1.f;
+    float a[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) a[j] = 0.f;
+    for (int q = 0; q < slots; ++q) {
+        const int p = r * slots + q, e = pick[p];
+        const float w = wts[p];
+        float o[8];
+        if (e >= 0 && e < E) {  // uniform over the block
+            const f4v z0 = *reinterpret_cast<const f4v*>(Z + (size_t)p * D + k);
+            const f4v z1 = *reinterpret_cast<const f4v*>(Z + (size_t)p * D + k + 4);
+            const u4v sv = *reinterpret_cast<const u4v*>(svh_d + (size_t)e * D + k);
+            float v[8];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                v[j] = 0.f + z0[j];  // the split sum from zero
+                v[4 + j] = 0.f + z1[j];
+            }
+#pragma unroll
+            for (int b = 1; b < 8; b <<= 1)
+#pragma unroll
+                for (int j = 0; j < 8; ++j)
+                    if (!(j & b)) {
+                        const float lo = v[j], hi = v[j | b];
+                        v[j] = lo + hi;
+                        v[j | b] = lo - hi;
+                    }
+#pragma unroll
+            for (int j = 0; j < 8; ++j) v[j] = __builtin_fmaf(s1, v[j], lane_xor<1>(v[j]));
+#pragma unroll
+            for (int j = 0; j < 8; ++j) v[j] = __builtin_fmaf(s2, v[j], lane_xor<2>(v[j]));
+#pragma unroll
+            for (int j = 0; j < 8; ++j) v[j] = __builtin_fmaf(s4, v[j], lane_xor<4>(v[j]));
+#pragma unroll
+            for (int j = 0; j < 8; ++j) v[j] = __builtin_fmaf(s8, v[j], lane_xor<8>(v[j]));
+#pragma unroll
+            for (int j = 0; j < 8; ++j) o[j] = v[j] * HAD_SCALE * h2f((uint16_t)(sv[j >> 1] >> (16 * (j & 1))));
+        } else {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) o[j] = 0.f;
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) a[j] = __builtin_fmaf(w, o[j], a[j]);
+    }
+    *reinterpret_cast<f4v*>(out + (size_t)r * D + k) = f4v{a[0], a[1], a[2], a[3]};
+    *reinterpret_cast<f4v*>(out + (size_t)r * D + k + 4) = f4v{a[4], a[5], a[6], a[7]};
+}
+
 // out fp32 -> bf16 -> fp32 in place (prompt_experts.zig:246), or fp32 -> fp16 into a half output.
 __global__ void round_kernel(float* __restrict__ out, size_t n) {
     for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
@@ -930,8 +992,15 @@ int ea_prompt_experts_run(ea_stream_t stream, const void* x, int x_dtype, uint32
         // slots without an expert add nothing (the reference's route skips them); fp16 sums go through an fp32
         // staging buffer (xg, free by now)
         float* o32 = half_sums ? dptr<float>(sc->xg) : static_cast<float*>(out) + (size_t)r0 * D;
-        r = launch_down_combine(s, dptr<const float>(sc->plane), pk, dptr<const uint16_t>(ex->svh_d),
-                                dptr<float>(sc->plane), wt, o32, n, pairs, D, 1, S, E, true);
+        if ((reinterpret_cast<uintptr_t>(o32) & 15) == 0) {  // 16-byte stores
+            prompt_combine_kernel<<<dim3(n, (D + 2047) / 2048), 256, 0, s>>>(dptr<const float>(sc->plane), pk,
+                                                                             dptr<const uint16_t>(ex->svh_d), wt, o32,
+                                                                             (int)D, (int)E, (int)S);
+            r = launched();
+        } else {
+            r = launch_down_combine(s, dptr<const float>(sc->plane), pk, dptr<const uint16_t>(ex->svh_d),
+                                    dptr<float>(sc->plane), wt, o32, n, pairs, D, 1, S, E, true);
+        }
         if (r) return r;
         const size_t cnt = (size_t)n * D;
         if (half_sums) {

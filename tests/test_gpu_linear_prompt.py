@@ -164,6 +164,20 @@ def test_prompt_experts_full_shape_512(ea):
     assert_close_rms(device.download(out), want, 2e-3, "prompt experts R=512")
 
 
+def test_prompt_unaligned_output_same_bits(ea):
+    """An output 4 bytes off a 16-byte boundary takes the scalar combine: the same bits as the vector one."""
+    device, _, _, pe, synth = ea
+    R, D = 40, 512
+    host, ex, sc, x, pick, wts, dx, dp, dw = _prompt_case(ea, R, 32, D, 128, 8, 400)
+    a = device.zeros((R, D), torch.float32)
+    pe.run(device.stream(), dx.data_ptr(), D, dp.data_ptr(), dw.data_ptr(), ex, sc, a.data_ptr(), R, do_round=False)
+    b = device.zeros((R * D + 4,), torch.float32)
+    pe.run(device.stream(), dx.data_ptr(), D, dp.data_ptr(), dw.data_ptr(), ex, sc, b.data_ptr() + 4, R,
+           do_round=False)
+    np.testing.assert_array_equal(device.download(b)[1:1 + R * D].reshape(R, D), device.download(a))
+    assert device.device_status() == 0
+
+
 def test_prompt_half_sums_and_invalid(ea):
     device, _, _, pe, synth = ea
     from ea_exl3._lib import EaError
