@@ -117,12 +117,12 @@ def test_linear_errors(ea):
 
 # ---- prefill -------------------------------------------------------------------------------------------------------
 
-def _prompt_case(ea, R, E, D, I, k2, seed, x_dtype=1, zipf=True):
+def _prompt_case(ea, R, E, D, I, k2, seed, x_dtype=1, zipf=True, cb=1):
     device, _, moe, pe, synth = ea
     slots = 8
     pick = synth.picks_zipf(seed, R, 1.1, E, slots) if zipf else synth.picks_uniform(seed, R, E, slots)
     wts = synth.routing_weights(seed + 1, R, slots)
-    host = synth.HostLayer(seed + 2, experts=E, dims=D, width=I, k2=k2, only=np.unique(pick))
+    host = synth.HostLayer(seed + 2, experts=E, dims=D, width=I, k2=k2, cb=cb, only=np.unique(pick))
     x = synth.activations(seed + 3, R, D, ["f16", "bf16", "f32"][x_dtype])
     ex = moe.Routed(host)
     assert pe.supported(ex)
@@ -162,6 +162,20 @@ def test_prompt_experts_full_shape_512(ea):
     pe.run(device.stream(), dx.data_ptr(), D, dp.data_ptr(), dw.data_ptr(), ex, sc, out.data_ptr(), R,
            do_round=False, x_dtype=0)
     assert_close_rms(device.download(out), want, 2e-3, "prompt experts R=512")
+
+
+@pytest.mark.parametrize("cb,I", [(0, 256), (2, 256), (2, 128), (0, 128)])
+def test_prompt_experts_codebooks(ea, cb, I):
+    """3inst and mul1 through both item lists (the small items' ring kernel and the larger items' kernel), both
+    ring widths (8 waves at I = 256, 4 at I = 128)."""
+    device, _, _, pe, synth = ea
+    R, E, D = 160, 48, 512
+    host, ex, sc, x, pick, wts, dx, dp, dw = _prompt_case(ea, R, E, D, I, 8, 500 + cb + I, cb=cb)
+    want = orc.prompt_experts(x, pick, wts, oracle_routed(host), R, 8, bf16=True)
+    out = device.zeros((R, D), torch.float32)
+    pe.run(device.stream(), dx.data_ptr(), D, dp.data_ptr(), dw.data_ptr(), ex, sc, out.data_ptr(), R, do_round=False)
+    assert_close_rms(device.download(out), want, 2e-3, f"prompt experts cb={cb}")
+    assert device.device_status() == 0
 
 
 def test_prompt_unaligned_output_same_bits(ea):
