@@ -86,7 +86,7 @@ __device__ __forceinline__ void wave_tiles(const uint32_t* __restrict__ base, si
     constexpr int NWD = TL::NW;
     const TL tl(lane);
     uint32_t wa[NTW][2][NWD], wb[NTW][2][NWD];
-    auto fetch = [&](uint32_t (&w)[NTW][2][NWD], int t) {
+    auto fetch = [&](uint32_t (&w)[NTW][2][NWD], int t) __attribute__((always_inline)) {
         const uint32_t* t0 = base + (size_t)t * kstride;
 #pragma unroll
         for (int j = 0; j < NTW; ++j) {
@@ -96,11 +96,11 @@ __device__ __forceinline__ void wave_tiles(const uint32_t* __restrict__ base, si
     };
     // the activations of a step are loaded before the next step's trellis words, so waiting for them leaves the
     // trellis prefetch in flight (loads complete in issue order)
-    auto load_a = [&](h8v (&a)[MG], int t) {
+    auto load_a = [&](h8v (&a)[MG], int t) __attribute__((always_inline)) {
 #pragma unroll
         for (int m = 0; m < MG; ++m) a[m] = load_a8(xrow[m], k0 + t * 16, lane);
     };
-    auto compute = [&](uint32_t (&w)[NTW][2][NWD], const h8v (&a)[MG]) {
+    auto compute = [&](uint32_t (&w)[NTW][2][NWD], const h8v (&a)[MG]) __attribute__((always_inline)) {
 #pragma unroll
         for (int j = 0; j < NTW; ++j) {
             const u2v b0 = tl.decode(w[j][0]);

@@ -245,7 +245,7 @@ __device__ __forceinline__ void item_chunk1(const uint32_t* st, const LaneQuad& 
     const uint16_t* xr = xa + (lane & 15) * xs + 8 * ((lane >> 4) & 3);
     uint32_t w[2][4][2];  // [buffer][tile: (t, j0), (t + 1, j0), (t, j1), (t + 1, j1)][word]
     h8v a[2];
-    auto read = [&](int t, int b) {
+    auto read = [&](int t, int b) __attribute__((always_inline)) {
 #pragma unroll
         for (int j = 0; j < 2; ++j)
 #pragma unroll
@@ -293,19 +293,19 @@ __device__ __forceinline__ void gu_loop(__amdgpu_buffer_rsrc_t xrs, const uint32
     u4v av[MT], aw[MT], ta[NL], tb[NL];
     int sn = 1;   // the next split's index
     int cur = 0;  // the buffer of the current chunk (NB = 3)
-    auto issue_a = [&](int c, u4v (&v)[MT]) {
+    auto issue_a = [&](int c, u4v (&v)[MT]) __attribute__((always_inline)) {
         c = c0 + (c < nch ? c : nch - 1);
 #pragma unroll
         for (int i = 0; i < MT; ++i)
             v[i] = __builtin_bit_cast(u4v, __builtin_amdgcn_raw_buffer_load_b128(xrs, aoff[i], c * PK * 32, 0));
     };
-    auto issue_t = [&](int c, u4v (&tv)[NL]) {
+    auto issue_t = [&](int c, u4v (&tv)[NL]) __attribute__((always_inline)) {
         c = c0 + (c < nch ? c : nch - 1);
         TileSpan sc = sp;
         sc.off = sp.off + c * PK * sp.kstride;
         stage_issue_k<PK, K2>(sc, lane, tv);
     };
-    auto step = [&](int c, u4v (&tv)[NL], u4v (&v)[MT]) {
+    auto step = [&](int c, u4v (&tv)[NL], u4v (&v)[MT]) __attribute__((always_inline)) {
         if constexpr (NB == 1) {
             __syncthreads();  // the previous chunk's reads of xa are done
 #pragma unroll
@@ -486,21 +486,21 @@ __device__ __forceinline__ void ring_loop(__amdgpu_buffer_rsrc_t xrs, uint32_t a
     pv pa, pb;
     u4v ta[NL], tb[NL];
     int sn = 1;  // the next split's index
-    auto issue_p = [&](int c, pv& v) {
+    auto issue_p = [&](int c, pv& v) __attribute__((always_inline)) {
         c = c < nch ? c : nch - 1;
         if constexpr (W == 4)
             v = __builtin_bit_cast(pv, __builtin_amdgcn_raw_buffer_load_b128(xrs, aoff, c * PK * 32, 0));
         else
             v = __builtin_bit_cast(pv, __builtin_amdgcn_raw_buffer_load_b64(xrs, aoff, c * PK * 32, 0));
     };
-    auto issue_t = [&](int c, u4v (&tv)[NL]) {
+    auto issue_t = [&](int c, u4v (&tv)[NL]) __attribute__((always_inline)) {
         c = c < nch ? c : nch - 1;
         TileSpan sc = sp;
         sc.off = sp.off + c * PK * sp.kstride;
         stage_issue_k<PK, K2>(sc, lane, tv);
     };
     // the piece's words d .. d + W - 1 of its row (d = lofs & 63) at their transposed places (see put_a)
-    auto put = [&](int p, const pv& v) {
+    auto put = [&](int p, const pv& v) __attribute__((always_inline)) {
         const int sl = p % RING_S;
         synced = synced && lds_wait_geq(&done[sl], NW * (p / RING_S));  // after a give-up no more waits
         uint32_t* w = reinterpret_cast<uint32_t*>(ring + sl * SLOT + (lofs >> 6) * PXS);
@@ -512,7 +512,7 @@ __device__ __forceinline__ void ring_loop(__amdgpu_buffer_rsrc_t xrs, uint32_t a
         }
         lds_add_release(&filled[sl], 1, lane);
     };
-    auto step = [&](int c, u4v (&tv)[NL], pv& v) {
+    auto step = [&](int c, u4v (&tv)[NL], pv& v) __attribute__((always_inline)) {
         if (c + RING_L < nch) put(c + RING_L, v);  // uniform
         issue_p(c + RING_L + 2, v);
         stage_store_k<PK, K2>(st, lane, tv);
@@ -615,13 +615,13 @@ __device__ __forceinline__ void dn_loop(const TileSpan& sp, const uint16_t* xa, 
     static_assert(NG % 2 == 0, "two steps an iteration");
     u4v ta[NL], tb[NL];
     f4v acc[MT][2];
-    auto issue_t = [&](int s2, u4v (&tv)[NL]) {
+    auto issue_t = [&](int s2, u4v (&tv)[NL]) __attribute__((always_inline)) {
         s2 = s2 < steps ? s2 : steps - 1;
         TileSpan sc = sp;
         sc.off = sp.off + (s2 / nch) * 8 * TWB + (s2 % nch) * PK * sp.kstride;
         stage_issue_k<PK, K2>(sc, lane, tv);
     };
-    auto step = [&](int s2, u4v (&tv)[NL]) {
+    auto step = [&](int s2, u4v (&tv)[NL]) __attribute__((always_inline)) {
         const int c = s2 % nch;
         if (c == 0) {
 #pragma unroll
