@@ -274,30 +274,21 @@ __device__ __forceinline__ void item_chunk1(const uint32_t* st, const LaneQuad& 
     }
 }
 
-// The chunk loop of a gate|up block for one width: the activations one chunk ahead, the trellis two. Loads complete
-// in issue order and every load is issued (a chunk past the last re-reads the last), so the waits stay exact.
-// With FOLD the nch chunks are summed as nsum splits ([s nch / nsum, (s + 1) nch / nsum)), each accumulated from zero
-// and added in order into tot (from zero): the bits of a K-split item's sum of its split planes, so a pair's sums do
-// not depend on which list its item is in. Without FOLD the block's chunks accumulate into acc.
-// NB = 1: one activation buffer, two barriers a chunk, activations loaded one chunk ahead. NB = 3: three buffers and
-// one barrier a chunk: chunk c + 1 goes into its buffer before the barrier of chunk c, and that buffer's previous
-// chunk (c - 2) was read before the barrier of chunk c - 1, which every wave has passed; activations are loaded two
-// chunks before they go to LDS (two register sets), like the trellis.
-template <int CB, int K2, int MT, bool FOLD, int NB>
+// The chunk loop of a gate|up block for one width: the activations one chunk ahead, the trellis two, two barriers a
+// chunk (the activations are shared by the block's waves). Loads complete in issue order and every load is issued (a
+// chunk past the last re-reads the last), so the waits stay exact.
+template <int CB, int K2, int MT>
 __device__ __forceinline__ void gu_loop(__amdgpu_buffer_rsrc_t xrs, const uint32_t (&aoff)[MT], const int (&lofs)[MT],
                                         const TileSpan& sp, uint16_t* xa, uint32_t* st, int lane, int q8, int mts,
-                                        int c0, int nch, int nsum, f4v (&acc)[MT][2], f4v (&tot)[MT][2]) {
+                                        int c0, int nch, f4v (&acc)[MT][2]) {
     constexpr int NL = stage_loads_k<PK, K2>();
-    constexpr int BUF = MT * 16 * PXS;
     const LaneQuad lq = lane_quad_k<K2>(lane);
-    u4v av[MT], aw[MT], ta[NL], tb[NL];
-    int sn = 1;   // the next split's index
-    int cur = 0;  // the buffer of the current chunk (NB = 3)
-    auto issue_a = [&](int c, u4v (&v)[MT]) __attribute__((always_inline)) {
+    u4v av[MT], ta[NL], tb[NL];
+    auto issue_a = [&](int c) __attribute__((always_inline)) {
         c = c0 + (c < nch ? c : nch - 1);
 #pragma unroll
         for (int i = 0; i < MT; ++i)
-            v[i] = __builtin_bit_cast(u4v, __builtin_amdgcn_raw_buffer_load_b128(xrs, aoff[i], c * PK * 32, 0));
+            av[i] = __builtin_bit_cast(u4v, __builtin_amdgcn_raw_buffer_load_b128(xrs, aoff[i], c * PK * 32, 0));
     };
     auto issue_t = [&](int c, u4v (&tv)[NL]) __attribute__((always_inline)) {
         c = c0 + (c < nch ? c : nch - 1);
@@ -305,81 +296,45 @@ __device__ __forceinline__ void gu_loop(__amdgpu_buffer_rsrc_t xrs, const uint32
         sc.off = sp.off + c * PK * sp.kstride;
         stage_issue_k<PK, K2>(sc, lane, tv);
     };
-    auto step = [&](int c, u4v (&tv)[NL], u4v (&v)[MT]) __attribute__((always_inline)) {
-        if constexpr (NB == 1) {
-            __syncthreads();  // the previous chunk's reads of xa are done
-#pragma unroll
-            for (int i = 0; i < MT; ++i)
-                if (i < mts) put_a(xa + lofs[i], q8, av[i]);
-            stage_store_k<PK, K2>(st, lane, tv);  // only this wave reads its region, in order
-            issue_a(c + 1, av);
-            issue_t(c + 2, tv);
-            __syncthreads();  // the chunk's activations are in LDS
-            item_chunk<CB, K2, MT>(st, lq, xa, mts, lane, acc, PXS);
-        } else {
-            const int nxt = cur == NB - 1 ? 0 : cur + 1;
-#pragma unroll
-            for (int i = 0; i < MT; ++i)
-                if (i < mts) put_a(xa + nxt * BUF + lofs[i], q8, v[i]);  // chunk c + 1
-            stage_store_k<PK, K2>(st, lane, tv);
-            issue_a(c + 3, v);
-            issue_t(c + 2, tv);
-            __syncthreads();
-            item_chunk<CB, K2, MT>(st, lq, xa + cur * BUF, mts, lane, acc, PXS);
-            cur = nxt;
-        }
-        if constexpr (FOLD) {
-            if (c + 1 == sn * nch / nsum) {  // the end of a split (uniform)
-#pragma unroll
-                for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-                    for (int j = 0; j < 2; ++j) {
-                        tot[mt][j] += acc[mt][j];
-                        acc[mt][j] = f4v{0.f, 0.f, 0.f, 0.f};
-                    }
-                ++sn;
-            }
-        }
-    };
-    if constexpr (NB == 1) {
-        issue_t(0, ta);
-        issue_t(1, tb);
-        issue_a(0, av);
-    } else {
-        issue_a(0, av);
+    auto step = [&](int c, u4v (&tv)[NL]) __attribute__((always_inline)) {
+        __syncthreads();  // the previous chunk's reads of xa are done
 #pragma unroll
         for (int i = 0; i < MT; ++i)
-            if (i < mts) put_a(xa + lofs[i], q8, av[i]);  // chunk 0 into buffer 0 (the first barrier publishes it)
-        issue_a(1, av);
-        issue_t(0, ta);
-        issue_a(2, aw);
-        issue_t(1, tb);
-    }
+            if (i < mts) put_a(xa + lofs[i], q8, av[i]);
+        stage_store_k<PK, K2>(st, lane, tv);  // only this wave reads its region, in order
+        issue_a(c + 1);
+        issue_t(c + 2, tv);
+        __syncthreads();  // the chunk's activations are in LDS
+        item_chunk<CB, K2, MT>(st, lq, xa, mts, lane, acc, PXS);
+    };
+    issue_t(0, ta);
+    issue_t(1, tb);
+    issue_a(0);
     // two steps an iteration with no exit between them, so every load's wait is counted the same on each pass
     int c = 0;
     for (; c + 1 < nch; c += 2) {
-        step(c, ta, av);
-        step(c + 1, tb, aw);
+        step(c, ta);
+        step(c + 1, tb);
     }
-    if (c < nch) step(c, ta, av);  // uniform
+    if (c < nch) step(c, ta);  // uniform
 }
 
-// Block (item of list MT > 2, 128 columns, (matrix, K split)): the item's rows (up to MT row tiles) times its
-// expert's matrix over split s of K's chunks of 128 (splits [s nch / nsplit, (s + 1) nch / nsplit)); a block of the
-// small items' list (nsplit 1) covers all of K and sums it as nsum splits the same way. A chunk's
-// activations go to LDS once for the block's four waves; each wave's two column tiles of the chunk come in as 16-byte
-// loads staged in the wave's own LDS region. Only the item's occupied row tiles are loaded and multiplied; rows past
-// the item's count read the item's first pair and are not stored (MFMA rows do not mix). Split 0 goes to
-// Z[mat][pair][n], split s > 0 to Zp[s - 1][mat][pair][n] (fp32).
-template <int CB, int MT>
-__global__ void __launch_bounds__(PW * 64) __attribute__((amdgpu_waves_per_eu(MT > 2 ? 2 : 4)))
+// Block (item of the larger items' list, 128 columns, (matrix, K split)): the item's rows (up to IPM_TILES row
+// tiles) times its expert's matrix over split s of K's chunks of 128 (splits [s nch / nsplit, (s + 1) nch / nsplit)).
+// A chunk's activations go to LDS once for the block's four waves; each wave's two column tiles of the chunk come in
+// as 16-byte loads staged in the wave's own LDS region. Only the item's occupied row tiles are loaded and multiplied;
+// rows past the item's count read the item's first pair and are not stored (MFMA rows do not mix). Split 0 goes to
+// Z[mat][pair][n], split s > 0 to Zp[s - 1][mat][pair][n] (fp32), each accumulated from zero (stored as 0 + sum).
+template <int CB>
+__global__ void __launch_bounds__(PW * 64) __attribute__((amdgpu_waves_per_eu(2)))
 item_gu_kernel(const uint16_t* __restrict__ X0, const uint16_t* __restrict__ X1, const int64_t* __restrict__ TP0,
                const int64_t* __restrict__ TP1, const int* __restrict__ K2_0, const int* __restrict__ K2_1,
                const int* __restrict__ sorted, const int* __restrict__ items, const int* __restrict__ item_count,
-               float* __restrict__ Z, float* __restrict__ Zp, int K, int N, int P, int nsplit, int nsum,
-               int max_items, int* __restrict__ status) {
+               float* __restrict__ Z, float* __restrict__ Zp, int K, int N, int P, int nsplit, int max_items,
+               int* __restrict__ status) {
+    constexpr int MT = IPM_TILES;
     int e, first, cnt;
-    if (!item_at(items, item_count, MT > 2, max_items, blockIdx.x, e, first, cnt)) return;
+    if (!item_at(items, item_count, 1, max_items, blockIdx.x, e, first, cnt)) return;
     const int mat = blockIdx.z / nsplit, split = blockIdx.z % nsplit;
     const uint16_t* X = mat ? X1 : X0;
     const uint32_t* T = reinterpret_cast<const uint32_t*>(mat ? TP1[e] : TP0[e]);
@@ -387,8 +342,7 @@ item_gu_kernel(const uint16_t* __restrict__ X0, const uint16_t* __restrict__ X1,
     // the wave index in a scalar register: the trellis offsets built from it are then scalar (a buffer load's soffset)
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     __shared__ int pair_sh[MT * 16];
-    constexpr int NB = MT <= 2 ? 3 : 1;
-    __shared__ __attribute__((aligned(16))) uint16_t xa[NB * MT * 16 * PXS];
+    __shared__ __attribute__((aligned(16))) uint16_t xa[MT * 16 * PXS];
     __shared__ __attribute__((aligned(16))) uint32_t st[PW][PSTAGE];
     if (tid < MT * 16) pair_sh[tid] = tid < cnt ? sorted[first + tid] : -1;
     __syncthreads();
@@ -412,15 +366,13 @@ item_gu_kernel(const uint16_t* __restrict__ X0, const uint16_t* __restrict__ X1,
     sp.r = buffer_rsrc(T, (uint32_t)((K >> 4) * ns * TWB));
     sp.off = nt0 * TWB;
     sp.kstride = ns * TWB;
-    constexpr bool FOLD = MT <= 2;
-    f4v acc[MT][2], tot[MT][2];
+    f4v acc[MT][2];
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) acc[mt][0] = acc[mt][1] = tot[mt][0] = tot[mt][1] = f4v{0.f, 0.f, 0.f, 0.f};
+    for (int mt = 0; mt < MT; ++mt) acc[mt][0] = acc[mt][1] = f4v{0.f, 0.f, 0.f, 0.f};
     const int nch = K / (PK * 16);
     const int c0 = split * nch / nsplit, nc = (split + 1) * nch / nsplit - c0;  // nsplit <= nch: nc >= 1
-    const bool ok = EA_K2_SWITCH(k2, 2, 10,
-                                 (gu_loop<CB, K2V, MT, FOLD, NB>(xrs, aoff, lofs, sp, xa, st[wave], lane, tid & 15, mts,
-                                                                 c0, nc, nsum, acc, tot)));
+    const bool ok = EA_K2_SWITCH(
+        k2, 2, 10, (gu_loop<CB, K2V, MT>(xrs, aoff, lofs, sp, xa, st[wave], lane, tid & 15, mts, c0, nc, acc)));
     if (!ok) {
         if (lane == 0) record_error(status, DEV_UNSUPPORTED_WIDTH);
         return;
@@ -433,8 +385,7 @@ item_gu_kernel(const uint16_t* __restrict__ X0, const uint16_t* __restrict__ X1,
             const int p = pair_sh[mt * 16 + 4 * (lane >> 4) + i];
             if (p < 0) continue;
 #pragma unroll
-            for (int j = 0; j < 2; ++j)
-                Zm[(size_t)p * N + (nt0 + j) * 16 + (lane & 15)] = FOLD ? tot[mt][j][i] : 0.f + acc[mt][j][i];
+            for (int j = 0; j < 2; ++j) Zm[(size_t)p * N + (nt0 + j) * 16 + (lane & 15)] = 0.f + acc[mt][j][i];
         }
 }
 
@@ -448,7 +399,10 @@ item_gu_kernel(const uint16_t* __restrict__ X0, const uint16_t* __restrict__ X1,
 // (filled >= NW (c / RING_S + 1)), computes it, and counts itself done. The slowest wave can always go on (every
 // chunk it waits for was stored at a step no later than its own, and every slot it stores into was freed before),
 // so every wait ends. Each wave's trellis goes through its own LDS region as in gu_loop; the activation piece of a
-// chunk (1/NW of it) and the trellis are loaded two chunks ahead. The chunks are summed as nsum splits (gu_loop).
+// chunk (1/NW of it) and the trellis are loaded two chunks ahead. The nch chunks are summed as nsum splits
+// ([s nch / nsum, (s + 1) nch / nsum)), each accumulated from zero and added in order into tot (from zero): the bits
+// of a K-split item's sum of its split planes (item_gu_kernel, summed by the epilogue), so a pair's sums do not
+// depend on which list its item is in.
 constexpr int RING_S = 6;  // activation chunk slots
 constexpr int RING_L = 2;  // a wave stores its piece of chunk c + RING_L at its step c
 
@@ -847,8 +801,8 @@ static int item_gemm_staged(hipStream_t s, const uint16_t* X0, const uint16_t* X
     return fork_join(
         s,
         [&](hipStream_t q) {
-            item_gu_kernel<CB, IPM_TILES><<<dim3(max_items, N / (16 * 2 * PW), mats * ns), PW * 64, 0, q>>>(
-                X0, X1, TP0, TP1, B0, B1, sorted, items, count, Z, Zp, K, N, P, ns, 1, mi, status);
+            item_gu_kernel<CB><<<dim3(max_items, N / (16 * 2 * PW), mats * ns), PW * 64, 0, q>>>(
+                X0, X1, TP0, TP1, B0, B1, sorted, items, count, Z, Zp, K, N, P, ns, mi, status);
             return launched();
         },
         [&](hipStream_t q) {
