@@ -128,11 +128,14 @@ struct RouteSh {
 
 // One row's top-8 on one wave (E = 256: expert q * 64 + lane in choice[q]): choice = sigmoid + bias, the larger
 // first, the lower id on a tie; wts = sigmoid / (sum of the picks' sigmoids in pick order + 1e-20) * scale
-// (native_ops.cu:1015-1068). A round: the wave maximum of the choices' keys, then the lowest id holding it (a wave
-// minimum), with no branches and no scalar round trips beyond the two broadcasts. `rounds` < 8 stops after the first
-// picks (wts are then not written: they need all eight).
+// (native_ops.cu:1015-1068). A round: the wave maximum of the choices' keys (one broadcast), then the lowest id holding
+// it from four ballots, one a key register: the first non-empty ballot names q and its lowest set bit the lane, in
+// scalar registers. The routing is the serial head of every routed item and its wave shares a SIMD with other blocks'
+// decoding waves, so it runs at the highest wave priority. `rounds` < 8 stops after the first picks (wts are then
+// not written: they need all eight).
 __device__ __forceinline__ void topk8_wave(const float* logits, const float* bias, float scale, int* pick, float* wts,
                                            int lane, int rounds = DL_SLOTS) {
+    __builtin_amdgcn_s_setprio(3);
     // all eight loads in flight before any is used
     float lg[4], bs[4];
 #pragma unroll
@@ -154,13 +157,12 @@ __device__ __forceinline__ void topk8_wave(const float* logits, const float* bia
     for (int k = 0; k < rounds; ++k) {
         const uint32_t km = key[0] > key[1] ? key[0] : key[1], kn = key[2] > key[3] ? key[2] : key[3];
         const uint32_t m = wave_reduce<true>(km > kn ? km : kn);
-        const uint32_t cand = key[0] == m   ? (uint32_t)lane
-                              : key[1] == m ? 64u + lane
-                              : key[2] == m ? 128u + lane
-                              : key[3] == m ? 192u + lane
-                                            : 0xffffu;
-        const int e = (int)wave_reduce<false>(cand);
-        const int src = e & 63, q = e >> 6;
+        // some key equals the maximum, so one ballot is non-empty
+        const uint64_t b0 = __builtin_amdgcn_ballot_w64(key[0] == m), b1 = __builtin_amdgcn_ballot_w64(key[1] == m);
+        const uint64_t b2 = __builtin_amdgcn_ballot_w64(key[2] == m), b3 = __builtin_amdgcn_ballot_w64(key[3] == m);
+        const int q = b0 ? 0 : (b1 ? 1 : (b2 ? 2 : 3));
+        const uint64_t bq = b0 ? b0 : (b1 ? b1 : (b2 ? b2 : b3));
+        const int src = (int)__builtin_ctzll(bq), e = q * 64 + src;
         const float sq = q == 0 ? score[0] : (q == 1 ? score[1] : (q == 2 ? score[2] : score[3]));
         const float sw = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sq), src));
         total = total + sw;
@@ -174,6 +176,7 @@ __device__ __forceinline__ void topk8_wave(const float* logits, const float* bia
     }
     if (lane < rounds) pick[lane] = my_p;
     if (rounds == DL_SLOTS && lane < DL_SLOTS) wts[lane] = my_w / (total + 1e-20f) * scale;
+    __builtin_amdgcn_s_setprio(0);
 }
 
 // The trellis addresses and widths of every routed unit, into LDS (one round trip for the block, instead of one an
@@ -358,11 +361,12 @@ __device__ __forceinline__ int opaque_lane(int lane) {
     return lane;
 }
 
-// Rows [from, to) of a staged-activation array (DL_RS halves a row) set to zero by the block.
+// Rows [from, to) of a staged-activation array (DL_RS halves a row) set to zero by the block of NT threads.
+template <int NT = DL_THREADS>
 __device__ __forceinline__ void zero_rows(uint16_t* xs, int from, int to) {
     uint32_t* w = reinterpret_cast<uint32_t*>(xs + from * DL_RS);
     const int n = (to - from) * DL_RS / 2;
-    for (int i = threadIdx.x; i < n; i += DL_THREADS) w[i] = 0u;
+    for (int i = threadIdx.x; i < n; i += NT) w[i] = 0u;
 }
 
 // ---- gate | up ----------------------------------------------------------------------------------------------------
@@ -485,15 +489,25 @@ __device__ __forceinline__ float2 zp_sum(const DLArgs& a, const float2 (&v)[DL_M
     return float2{s0, s1};
 }
 
-// A matrix's outputs of a column block: FWHT of the sums, HAD_SCALE, the output scale svh. The shared expert's gate
-// and up linears write bf16 (forward.zig:2330); the routed experts keep fp32 (exl3_experts.cu:142-184).
-__device__ __forceinline__ float2 gu_out(const DLArgs& a, const UnitView& uv, int nh, int mat, float2 v, int lane) {
-    fwht128_w64(v.x, v.y, lane);
-    const int n = nh * 128 + 2 * lane;
+// The two fp16 scales of columns n, n + 1 of a column block (packed, as loaded): the gate or up output scale svh,
+// and the down input scale suh_d. Callers load them with the partial sums, ahead of any trellis load, since a load
+// issued after the trellis completes only after it.
+__device__ __forceinline__ uint32_t svh_pair(const DLArgs& a, const UnitView& uv, int nh, int mat, int lane) {
     const uint16_t* svh =
         uv.shared ? (mat ? a.sh_svh[1] : a.sh_svh[0]) : (mat ? a.svh_u : a.svh_g) + (size_t)uv.e * a.I;
-    float o0 = v.x * HAD_SCALE * h2f(svh[n]);
-    float o1 = v.y * HAD_SCALE * h2f(svh[n + 1]);
+    return *reinterpret_cast<const uint32_t*>(svh + nh * 128 + 2 * lane);
+}
+__device__ __forceinline__ uint32_t suhd_pair(const DLArgs& a, const UnitView& uv, int nh, int lane) {
+    const uint16_t* suh = uv.shared ? a.sh_suh[2] : a.suh_d + (size_t)uv.e * a.I;
+    return *reinterpret_cast<const uint32_t*>(suh + nh * 128 + 2 * lane);
+}
+
+// A matrix's outputs of a column block: FWHT of the sums, HAD_SCALE, the output scale svh (the pair sv). The shared
+// expert's gate and up linears write bf16 (forward.zig:2330); the routed experts keep fp32 (exl3_experts.cu:142-184).
+__device__ __forceinline__ float2 gu_out(const UnitView& uv, float2 v, uint32_t sv, int lane) {
+    fwht128_w64(v.x, v.y, lane);
+    float o0 = v.x * HAD_SCALE * h2f((uint16_t)(sv & 0xffffu));
+    float o1 = v.y * HAD_SCALE * h2f((uint16_t)(sv >> 16));
     if (uv.shared) {
         o0 = bf16r(o0);
         o1 = bf16r(o1);
@@ -501,20 +515,20 @@ __device__ __forceinline__ float2 gu_out(const DLArgs& a, const UnitView& uv, in
     return float2{o0, o1};
 }
 
-// SwiGLU of a column block, the down input scale suh, FWHT, HAD_SCALE: the packed fp16 down inputs of columns n, n + 1.
-// Routed experts: act_mode 1 with no limit (moe.zig:290; exl3_experts.cu:142-184). The shared expert: swiglu2 in bf16
-// (native_ops.cu:429-441), read by the down linear's rot_in (exl3_linear.cu:152-173).
-__device__ __forceinline__ uint32_t act_pair(const DLArgs& a, const UnitView& uv, int nh, float2 g, float2 u, int lane) {
-    const int n = nh * 128 + 2 * lane;
+// SwiGLU of a column block, the down input scale suh (the pair sd), FWHT, HAD_SCALE: the packed fp16 down inputs of
+// columns n, n + 1. Routed experts: act_mode 1 with no limit (moe.zig:290; exl3_experts.cu:142-184). The shared
+// expert: swiglu2 in bf16 (native_ops.cu:429-441), read by the down linear's rot_in (exl3_linear.cu:152-173).
+__device__ __forceinline__ uint32_t act_pair(const UnitView& uv, float2 g, float2 u, uint32_t sd, int lane) {
     const float gs[2] = {g.x, g.y}, us[2] = {u.x, u.y};
+    const float ss[2] = {h2f((uint16_t)(sd & 0xffffu)), h2f((uint16_t)(sd >> 16))};
     float v[2];
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
         if (uv.shared) {
             const float sg = bf16r(gs[j] / (expf_path(0.0f - gs[j]) + 1.0f));
-            v[j] = bf16r(sg * us[j]) * h2f(a.sh_suh[2][n + j]);
+            v[j] = bf16r(sg * us[j]) * ss[j];
         } else {
-            v[j] = gs[j] / (1.f + expf_path(-gs[j])) * us[j] * h2f(a.suh_d[(size_t)uv.e * a.I + n + j]);
+            v[j] = gs[j] / (1.f + expf_path(-gs[j])) * us[j] * ss[j];
         }
     }
     fwht128_w64(v[0], v[1], lane);
@@ -530,14 +544,16 @@ __global__ void __launch_bounds__(DL_THREADS) epilogue_kernel(DLArgs a) {
     UnitView uv;
     if (!unit_from_layout(a, unit, uv, s_mem)) return;
     __syncthreads();
+    const uint32_t svg = svh_pair(a, uv, nh, 0, lane), svu = svh_pair(a, uv, nh, 1, lane);
+    const uint32_t sd = suhd_pair(a, uv, nh, lane);
     for (int m = wave; m < uv.nm; m += DL_WAVES) {
         const int q = member_q(a, uv, m);
         float2 zg[DL_MAXKC], zu[DL_MAXKC];
         zp_load(a, q, nh, 0, lane, zg);
         zp_load(a, q, nh, 1, lane, zu);
-        const float2 g = gu_out(a, uv, nh, 0, zp_sum(a, zg), lane);
-        const float2 u = gu_out(a, uv, nh, 1, zp_sum(a, zu), lane);
-        *reinterpret_cast<uint32_t*>(a.lay.xd + (size_t)q * a.I + nh * 128 + 2 * lane) = act_pair(a, uv, nh, g, u, lane);
+        const float2 g = gu_out(uv, zp_sum(a, zg), svg, lane);
+        const float2 u = gu_out(uv, zp_sum(a, zu), svu, lane);
+        *reinterpret_cast<uint32_t*>(a.lay.xd + (size_t)q * a.I + nh * 128 + 2 * lane) = act_pair(uv, g, u, sd, lane);
     }
 }
 
@@ -640,57 +656,76 @@ gateup_kernel(DLArgs a) {
 
 // ---- down ---------------------------------------------------------------------------------------------------------
 
-// The unit's down inputs into xs, then the product. FOLD (one row: a unit has at most 8 members): the block computes
-// the inputs itself from the gate|up partials, a wave a (member, column block, matrix) task, instead of the epilogue
-// launch; the first task's partials load ahead of the trellis. Otherwise they are the epilogue's, loaded ahead of the
-// trellis. Loads complete in order, so the inputs never wait for the trellis.
-template <int CB, int SCB, int NKT, bool FOLD>
+// The unit's down inputs into xs, then the product, for a block of NW waves. FOLD (one row: a unit has at most 8
+// members): the block computes the inputs itself from the gate|up partials, a wave a (member, column block, matrix)
+// task, instead of the epilogue launch; a wave's first task's partials load ahead of its trellis, and a wave without a
+// task loads only its trellis. Otherwise they are the epilogue's, loaded ahead of the trellis. Loads complete in
+// order, so the inputs never wait for the trellis.
+template <int CB, int SCB, int NKT, bool FOLD, int NW>
 __device__ __forceinline__ bool down_product(const DLArgs& a, const UnitView& uv, const TileSpan& sp, int k2,
                                              uint16_t* xs, float* gus, uint32_t* st, f4v (&acc)[2]) {
+    constexpr int NT = 64 * NW;
     const int lane = opaque_lane(threadIdx.x & 63), wave = uniform((int)threadIdx.x >> 6);
     const LaneQuad lq = lane_quad(k2, lane);
     u4v v[stage_loads<NKT>()];
     if constexpr (FOLD) {
         const int NH = a.I / 128, tasks = uv.nm * NH * 2;
-        float2 zv[DL_MAXKC];
-        const int t0 = min(wave, tasks - 1);  // unconditional (see stage_issue); a wave without a task repeats one
-        zp_load(a, member_q(a, uv, t0 / (2 * NH)), (t0 >> 1) % NH, t0 & 1, lane, zv);
-        stage_issue<NKT>(sp, k2, lane, v);
-        issued();
-        zero_rows(xs, uv.nm, DL_MAXR);  // the MFMAs read all 16 rows
+        // the scales of the wave's first epilogue task ((member, column block, matrix), then (member, column block)
+        // of the activation), loaded with its partial sums and ahead of the trellis; a wave past the last task
+        // reads the last one's
+        const int t0 = min(wave, tasks - 1), a0 = min(wave, uv.nm * NH - 1);
+        uint32_t sv0 = svh_pair(a, uv, (t0 >> 1) % NH, t0 & 1, lane), sd0 = suhd_pair(a, uv, a0 % NH, lane);
+        if (wave < tasks) {
+            float2 zv[DL_MAXKC];
+            zp_load(a, member_q(a, uv, wave / (2 * NH)), (wave >> 1) % NH, wave & 1, lane, zv);
+            stage_issue<NKT>(sp, k2, lane, v);
+            issued();
+            hold(sv0);
+            hold(sd0);
 #pragma unroll
-        for (int cc = 0; cc < DL_MAXKC; ++cc) hold(zv[cc]);
-        for (int task = wave; task < tasks; task += DL_WAVES) {
-            const int m = task / (2 * NH), nh = (task >> 1) % NH, mat = task & 1;
-            if (task != wave) zp_load(a, member_q(a, uv, m), nh, mat, lane, zv);
-            const float2 o = gu_out(a, uv, nh, mat, zp_sum(a, zv), lane);
-            *reinterpret_cast<float2*>(gus + (m * 2 + mat) * DL_MAXI + nh * 128 + 2 * lane) = o;
+            for (int cc = 0; cc < DL_MAXKC; ++cc) hold(zv[cc]);
+            for (int task = wave; task < tasks; task += NW) {
+                const int m = task / (2 * NH), nh = (task >> 1) % NH, mat = task & 1;
+                uint32_t sv = sv0;
+                if (task != wave) {
+                    zp_load(a, member_q(a, uv, m), nh, mat, lane, zv);
+                    sv = svh_pair(a, uv, nh, mat, lane);
+                }
+                const float2 o = gu_out(uv, zp_sum(a, zv), sv, lane);
+                *reinterpret_cast<float2*>(gus + (m * 2 + mat) * DL_MAXI + nh * 128 + 2 * lane) = o;
+            }
+        } else {
+            stage_issue<NKT>(sp, k2, lane, v);
+            issued();
+            hold(sd0);
         }
+        zero_rows<NT>(xs, uv.nm, DL_MAXR);  // the MFMAs read all 16 rows
         __syncthreads();
-        for (int task = wave; task < uv.nm * NH; task += DL_WAVES) {
+        for (int task = wave; task < uv.nm * NH; task += NW) {
             const int m = task / NH, nh = task % NH;
             const float2 g = *reinterpret_cast<const float2*>(gus + (m * 2) * DL_MAXI + nh * 128 + 2 * lane);
             const float2 u = *reinterpret_cast<const float2*>(gus + (m * 2 + 1) * DL_MAXI + nh * 128 + 2 * lane);
-            *reinterpret_cast<uint32_t*>(xs + m * DL_RS + nh * 128 + 2 * lane) = act_pair(a, uv, nh, g, u, lane);
+            const uint32_t sd = task == wave ? sd0 : suhd_pair(a, uv, nh, lane);
+            *reinterpret_cast<uint32_t*>(xs + m * DL_RS + nh * 128 + 2 * lane) = act_pair(uv, g, u, sd, lane);
         }
     } else {
         constexpr int WPR = NKT * 16 / 2;  // words a row
-        constexpr int MW = DL_MAXR * WPR / DL_THREADS;
+        constexpr int MW = DL_MAXR * WPR / NT;
         uint32_t xv[MW];
 #pragma unroll
         for (int i = 0; i < MW; ++i) {
-            const int idx = threadIdx.x + DL_THREADS * i;
+            const int idx = threadIdx.x + NT * i;
             const int m = min(idx / WPR, uv.nm - 1), k = 2 * (idx % WPR);  // unconditional (see stage_issue)
             xv[i] = *reinterpret_cast<const uint32_t*>(a.lay.xd + (size_t)member_q(a, uv, m) * a.I + k);
         }
         stage_issue<NKT>(sp, k2, lane, v);
         issued();
-        zero_rows(xs, uv.nm, DL_MAXR);  // the MFMAs read all 16 rows
+        zero_rows<NT>(xs, uv.nm, DL_MAXR);  // the MFMAs read all 16 rows
 #pragma unroll
         for (int i = 0; i < MW; ++i) hold(xv[i]);
 #pragma unroll
         for (int i = 0; i < MW; ++i) {
-            const int idx = threadIdx.x + DL_THREADS * i;
+            const int idx = threadIdx.x + NT * i;
             const int m = idx / WPR, k = 2 * (idx % WPR);
             if (m < uv.nm) *reinterpret_cast<uint32_t*>(xs + m * DL_RS + k) = xv[i];
         }
@@ -701,26 +736,34 @@ __device__ __forceinline__ bool down_product(const DLArgs& a, const UnitView& uv
                      : mfma_tiles_k2<CB, NKT>(k2, st, lq, xs, uv.nm, lane, acc);
 }
 
-// The down launches' LDS besides the staged activations: the folded epilogue's gate and up values, the trellis staging
-// and the product's column sums are live one after another, so they share one region.
+// The down launches' LDS besides the staged activations, for a block of NW waves (NW / 4 column blocks of 128): the
+// folded epilogue's gate and up values, the trellis staging and the product's column sums are live one after
+// another, so they share one region.
+template <int NW>
 union DownSh {
     float gus[DL_SLOTS * 2 * DL_MAXI];
-    __attribute__((aligned(16))) uint32_t stage[DL_WAVES][DL_STAGE_WORDS];
-    float ys[DL_MAXR * 128];
+    __attribute__((aligned(16))) uint32_t stage[NW][DL_STAGE_WORDS];
+    float ys[DL_MAXR * 128 * (NW / 4)];
 };
 
-// Block (unit, column block of 128 outputs): the members' down products, FWHT, svh -> the pair's y (or the shared
-// expert's sy).
-template <int CB, int SCB, bool FOLD>
-__device__ __forceinline__ void down_block(const DLArgs& a, uint16_t* xs, DownSh& ds, int16_t* s_mem) {
-    const int DB = a.D / 128;
-    const int u = blockIdx.x / DB, cb = blockIdx.x % DB;
+// Block (unit, NW / 4 adjacent column blocks of 128 outputs), four waves a column block: the members' down products,
+// FWHT, svh -> the pair's y (or the shared expert's sy). The unit's down inputs are formed once for all of the
+// block's column blocks.
+template <int CB, int SCB, bool FOLD, int NW>
+__device__ __forceinline__ void down_block(const DLArgs& a, uint16_t* xs, DownSh<NW>& ds, int16_t* s_mem) {
+    constexpr int CBB = NW / 4;
+    const int GB = a.D / 128 / CBB;
+    const int u = blockIdx.x / GB, cg = blockIdx.x % GB;
     const int lane = threadIdx.x & 63, wave = uniform((int)threadIdx.x >> 6);
     UnitView uv;
     UnitDown dn;
     if (!unit_from_layout(a, u, uv, s_mem, &dn)) return;
     __syncthreads();
-    const int nt0 = cb * 8 + 2 * wave, KT = a.I / 16;
+    const int cbl = wave >> 2, nt0 = (cg * CBB + cbl) * 8 + 2 * (wave & 3), KT = a.I / 16;
+    // the output scales of the wave's column block in the FWHT tasks below (every task of a wave has the same one),
+    // loaded ahead of the trellis
+    const uint16_t* svh = uv.shared ? a.sh_svh[2] : a.svh_d + (size_t)uv.e * a.D;
+    uint32_t sd = *reinterpret_cast<const uint32_t*>(svh + (cg * CBB + wave % CBB) * 128 + 2 * lane);
     f4v acc[2] = {f4v{0.f, 0.f, 0.f, 0.f}, f4v{0.f, 0.f, 0.f, 0.f}};
     // matrix I x D: routed in the expert layout, the shared expert in strips ([D / 128][I / 16][8][TW])
     const int ns = a.D / 16;
@@ -735,46 +778,52 @@ __device__ __forceinline__ void down_block(const DLArgs& a, uint16_t* xs, DownSh
         sp.off = nt0 * TWB;
         sp.kstride = ns * TWB;
     }
-    const bool ok = a.I == 256 ? down_product<CB, SCB, 16, FOLD>(a, uv, sp, k2, xs, ds.gus, ds.stage[wave], acc)
-                               : down_product<CB, SCB, 8, FOLD>(a, uv, sp, k2, xs, ds.gus, ds.stage[wave], acc);
+    const bool ok = a.I == 256
+                        ? down_product<CB, SCB, 16, FOLD, NW>(a, uv, sp, k2, xs, ds.gus, ds.stage[wave], acc)
+                        : down_product<CB, SCB, 8, FOLD, NW>(a, uv, sp, k2, xs, ds.gus, ds.stage[wave], acc);
     if (!ok && lane == 0) record_error(a.status, DEV_UNSUPPORTED_WIDTH);
     __syncthreads();  // the column sums overwrite the other waves' staging
+    constexpr int YS = 128 * CBB;  // ys row stride
     float* ys = ds.ys;
 #pragma unroll
     for (int j = 0; j < 2; ++j)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) ys[(4 * (lane >> 4) + i) * 128 + (2 * wave + j) * 16 + (lane & 15)] = acc[j][i];
+        for (int i = 0; i < 4; ++i)
+            ys[(4 * (lane >> 4) + i) * YS + cbl * 128 + (2 * (wave & 3) + j) * 16 + (lane & 15)] = acc[j][i];
     __syncthreads();
-    // FWHT of each member's 128 columns, * HAD_SCALE * svh_d
-    const int n = cb * 128 + 2 * lane;
-    for (int m = wave; m < uv.nm; m += DL_WAVES) {
-        float v0 = ys[m * 128 + 2 * lane], v1 = ys[m * 128 + 2 * lane + 1];
+    // FWHT of each member's 128 columns of each column block, * HAD_SCALE * svh_d
+    hold(sd);
+    const float s0 = h2f((uint16_t)(sd & 0xffffu)), s1 = h2f((uint16_t)(sd >> 16));
+    for (int task = wave; task < uv.nm * CBB; task += NW) {
+        const int m = task / CBB, c = task % CBB;
+        const int n = (cg * CBB + c) * 128 + 2 * lane;
+        float v0 = ys[m * YS + c * 128 + 2 * lane], v1 = ys[m * YS + c * 128 + 2 * lane + 1];
         fwht128_w64(v0, v1, lane);
-        const uint16_t* svh = uv.shared ? a.sh_svh[2] : a.svh_d + (size_t)uv.e * a.D;
         float* dst = uv.shared ? a.lay.sy + (size_t)m * a.D : a.yroute + (size_t)member_q(a, uv, m) * a.D;
-        *reinterpret_cast<float2*>(dst + n) = float2{v0 * HAD_SCALE * h2f(svh[n]), v1 * HAD_SCALE * h2f(svh[n + 1])};
+        *reinterpret_cast<float2*>(dst + n) = float2{v0 * HAD_SCALE * s0, v1 * HAD_SCALE * s1};
     }
 }
 
 template <int CB, int SCB>
 __global__ void __launch_bounds__(DL_THREADS) __attribute__((amdgpu_waves_per_eu(4))) down_kernel(DLArgs a) {
     __shared__ __attribute__((aligned(16))) uint16_t xs[DL_MAXR * DL_RS];
-    __shared__ DownSh ds;
+    __shared__ DownSh<DL_WAVES> ds;
     __shared__ int16_t s_mem[DL_MAXR];
-    down_block<CB, SCB, false>(a, xs, ds, s_mem);
+    down_block<CB, SCB, false, DL_WAVES>(a, xs, ds, s_mem);
 }
 
 // One row: the epilogue folded in (a unit has at most DL_SLOTS members; the grid covers few blocks, so two waves a
-// SIMD are enough and the partials and the trellis stay in registers together).
+// SIMD are enough and the partials and the trellis stay in registers together). Every block of a unit reads the
+// unit's gate|up partial sums: a block of eight waves over two column blocks halves those reads with the same waves a
+// SIMD. (Sixteen waves over four column blocks measured slower: four waves a SIMD decode one after another.)
+constexpr int DL_FOLD_WAVES = 8;
 template <int CB, int SCB>
-__global__ void __launch_bounds__(DL_THREADS) __attribute__((amdgpu_waves_per_eu(2))) down_fold_kernel(DLArgs a) {
+__global__ void __launch_bounds__(64 * DL_FOLD_WAVES) __attribute__((amdgpu_waves_per_eu(2))) down_fold_kernel(DLArgs a) {
     __shared__ __attribute__((aligned(16))) uint16_t xs[DL_MAXR * DL_RS];
-    __shared__ DownSh ds;
+    __shared__ DownSh<DL_FOLD_WAVES> ds;
     __shared__ int16_t s_mem[DL_MAXR];
-    down_block<CB, SCB, true>(a, xs, ds, s_mem);
+    down_block<CB, SCB, true, DL_FOLD_WAVES>(a, xs, ds, s_mem);
 }
-
-// ---- combine -------------------------------------------------------------------------------------------------------
 
 // A wave a (row, column block of 128): out = fma chain over the slots in order from 0 of wts * y (a slot whose pick
 // is not an expert reads y as it is; exl3_experts.cu:256-267), then + the shared expert (forward.zig:2403).
@@ -896,10 +945,11 @@ static int dl_launch(hipStream_t s, const DLArgs& a, int cus, int device) {
     int r = launched();
     if (r) return r;
     mark_stage(s, device, 1);
-    if (a.R == 1) {
+    constexpr int FCB = DL_FOLD_WAVES / 4;  // column blocks a fold block
+    if (a.R == 1 && DB % FCB == 0) {
         // one row: the down launch computes its own inputs (the epilogue stage is empty)
         mark_stage(s, device, 2);
-        down_fold_kernel<CB, SCB><<<a.U * DB, DL_THREADS, 0, s>>>(a);
+        down_fold_kernel<CB, SCB><<<a.U * (DB / FCB), 64 * DL_FOLD_WAVES, 0, s>>>(a);
         if ((r = launched())) return r;
     } else {
         epilogue_kernel<<<a.U * NH, DL_THREADS, 0, s>>>(a);
