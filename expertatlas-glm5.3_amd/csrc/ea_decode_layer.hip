@@ -1,12 +1,13 @@
-// One decode window's MoE FFN (R <= 16 rows, top-8) in four launches, each boundary carrying one dependency and no
+// One decode window's MoE FFN (R <= 16 rows, top-8) in a few launches, each boundary carrying one dependency and no
 // block ever waiting on, or counting with, another:
-//   gate|up: every block computes the router top-8 and the grouping of the window itself (in LDS), then works through
-//     its share of the (unit, column block, matrix, k chunk) items, a unit being a distinct routed expert or the
-//     shared expert. An item issues all of its trellis loads before it rotates its activations, multiplies on MFMA
-//     and stores its partial sums.
-//   epilogue: a block per (unit, column block) sums the chunks in order and runs FWHT, SwiGLU and FWHT into the
-//     unit's down inputs.
-//   down: a block per (unit, column block of 128 outputs): the pair's (or the shared expert's) output rows.
+//   route (more than one row): one block computes the router top-8 of every row and the grouping, and publishes
+//     them; with one row every gate|up block routes the row itself (in LDS) instead, which costs less than a launch.
+//   gate|up: every block works through its share of the (unit, column block, matrix, k chunk) items, a unit being a
+//     distinct routed expert or the shared expert. An item issues all of its trellis loads before it rotates its
+//     activations, multiplies on MFMA and stores its partial sums.
+//   epilogue (more than one row): a block per (unit, column block, group of members) sums the chunks in order and
+//     runs FWHT, SwiGLU and FWHT into the members' down inputs; with one row the down launch does this itself.
+//   down: a block per (unit, column blocks of 128 outputs): the pair's (or the shared expert's) output rows.
 //   combine: out = the slots in order from 0 (+ the shared expert).
 // In-launch hand-offs between blocks were measured slower: a release fence writes back the XCD's whole L2, and
 // polling blocks saturate the memory channel of the flag they poll.
@@ -46,8 +47,8 @@ struct DLLayout {
     int* ucount;        // [1] routed units
     int* members;       // [DL_MAXP, DL_MAXR] pair ids of a routed unit, ascending
     int* mcount;        // [DL_MAXP]
-    uint64_t* dptr;     // [DL_MAXP] a routed unit's down trellis address
-    int* dk2;           // [DL_MAXP] and width
+    uint64_t* tptr;     // [DL_MAXP, 3] a routed unit's gate, up and down trellis addresses
+    int* tk2;           // [DL_MAXP, 3] and widths
 };
 
 struct DLArgs {
@@ -107,7 +108,8 @@ __device__ __forceinline__ uint32_t wave_reduce(uint32_t v) {
 struct RouteScratch {
     int pick[DL_MAXP];
     float wts[DL_MAXP];
-    int unit[DL_MAXE];  // count of an expert's picks
+    int unit[DL_MAXE];  // count of an expert's picks (mask of the rows that pick it, from logits)
+    int uidx[256];      // an expert's unit, from logits
     int wsum[DL_WAVES];
     uint64_t tptr[3][256];  // one row's path: every expert's addresses and widths, loaded with the logits
     int tk2[3][256];
@@ -125,6 +127,85 @@ struct RouteSh {
         __attribute__((aligned(16))) uint32_t stage[DL_WAVES][DL_STAGE_WORDS];
     };
 };
+
+// The top-8 of NR rows on one wave, interleaved, for windows of more than one row (one row: topk8_wave below). E =
+// 256: expert q * 64 + lane in choice[q]; choice = sigmoid + bias, the larger first, the lower id on a tie; wts =
+// sigmoid / (sum of the picks' sigmoids in pick order + 1e-20) * scale (native_ops.cu:1015-1068). Row j of the wave is logits row `row0 + j * rstep`; rows from `nrows` on are
+// computed on row0's logits and not written. A round: the wave maximum of the choices' keys (one broadcast), then the
+// lowest id holding it from four ballots, one a key register: the first non-empty ballot names q and its lowest set
+// bit the lane, in scalar registers. A round is a chain of dependent cross-lane steps, so the NR rows' chains run
+// side by side. (Finding the eighth largest key bit by bit and placing the picks by counting, with no rounds,
+// measured slower: 32 dependent ballot counts.) The routing is the serial head of every routed item and its wave
+// shares a SIMD with other blocks' decoding waves, so it runs at the highest wave priority. `rounds` < 8 stops
+// after the first picks (wts are then not written: they need all eight).
+template <int NR>
+__device__ __forceinline__ void topk8_rows(const float* logits, int row0, int rstep, int nrows, const float* bias,
+                                           float scale, int* pick, float* wts, int lane, int rounds = DL_SLOTS) {
+    __builtin_amdgcn_s_setprio(3);
+    // every load in flight before any is used
+    float lg[NR][4], bs[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) bs[q] = bias[q * 64 + lane];
+#pragma unroll
+    for (int j = 0; j < NR; ++j) {
+        const int row = j < nrows ? row0 + j * rstep : row0;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) lg[j][q] = logits[(size_t)row * 256 + q * 64 + lane];
+    }
+#pragma unroll
+    for (int j = 0; j < NR; ++j) asm volatile("" : "+v"(lg[j][0]), "+v"(lg[j][1]), "+v"(lg[j][2]), "+v"(lg[j][3]));
+    asm volatile("" : "+v"(bs[0]), "+v"(bs[1]), "+v"(bs[2]), "+v"(bs[3]));
+    float score[NR][4];
+    uint32_t key[NR][4];
+#pragma unroll
+    for (int j = 0; j < NR; ++j)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            score[j][q] = 1.0f / (expf_path(0.0f - lg[j][q]) + 1.0f);
+            key[j][q] = order_key(score[j][q] + bs[q]);
+        }
+    float total[NR], my_w[NR];
+    int my_p[NR];
+#pragma unroll
+    for (int j = 0; j < NR; ++j) {
+        total[j] = 0.0f;
+        my_w[j] = 0.0f;
+        my_p[j] = 0;
+    }
+    for (int k = 0; k < rounds; ++k) {
+#pragma unroll
+        for (int j = 0; j < NR; ++j) {
+            uint32_t(&kj)[4] = key[j];
+            const uint32_t km = kj[0] > kj[1] ? kj[0] : kj[1], kn = kj[2] > kj[3] ? kj[2] : kj[3];
+            const uint32_t m = wave_reduce<true>(km > kn ? km : kn);
+            // some key equals the maximum, so one ballot is non-empty
+            const uint64_t b0 = __builtin_amdgcn_ballot_w64(kj[0] == m), b1 = __builtin_amdgcn_ballot_w64(kj[1] == m);
+            const uint64_t b2 = __builtin_amdgcn_ballot_w64(kj[2] == m), b3 = __builtin_amdgcn_ballot_w64(kj[3] == m);
+            const int q = b0 ? 0 : (b1 ? 1 : (b2 ? 2 : 3));
+            const uint64_t bq = b0 ? b0 : (b1 ? b1 : (b2 ? b2 : b3));
+            const int src = (int)__builtin_ctzll(bq), e = q * 64 + src;
+            const float sq = q == 0 ? score[j][0] : (q == 1 ? score[j][1] : (q == 2 ? score[j][2] : score[j][3]));
+            const float sw = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sq), src));
+            total[j] = total[j] + sw;
+            my_w[j] = lane == k ? sw : my_w[j];
+            my_p[j] = lane == k ? e : my_p[j];
+            const bool mine = lane == src;
+            kj[0] = (mine && q == 0) ? 0u : kj[0];
+            kj[1] = (mine && q == 1) ? 0u : kj[1];
+            kj[2] = (mine && q == 2) ? 0u : kj[2];
+            kj[3] = (mine && q == 3) ? 0u : kj[3];
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < NR; ++j)
+        if (j < nrows) {
+            const int row = row0 + j * rstep;
+            if (lane < rounds) pick[row * DL_SLOTS + lane] = my_p[j];
+            if (rounds == DL_SLOTS && lane < DL_SLOTS)
+                wts[row * DL_SLOTS + lane] = my_w[j] / (total[j] + 1e-20f) * scale;
+        }
+    __builtin_amdgcn_s_setprio(0);
+}
 
 // One row's top-8 on one wave (E = 256: expert q * 64 + lane in choice[q]): choice = sigmoid + bias, the larger
 // first, the lower id on a tie; wts = sigmoid / (sum of the picks' sigmoids in pick order + 1e-20) * scale
@@ -180,14 +261,17 @@ __device__ __forceinline__ void topk8_wave(const float* logits, const float* bia
 }
 
 // The trellis addresses and widths of every routed unit, into LDS (one round trip for the block, instead of one an
-// item): gate and up, and down for the block that publishes them.
+// item): gate and up, and down for the block that publishes them. Routed from logits, every expert's tables are in
+// LDS already (loaded with the logits) and no round trip is left.
 __device__ __forceinline__ void route_tables(const DLArgs& a, RouteSh& sh, int mats) {
     for (int u = threadIdx.x; u < sh.ucount; u += DL_THREADS) {
         const int e = sh.uids[u];
-        for (int m = 0; m < mats; ++m) {
-            sh.uptr[u][m] = (uint64_t)a.ptr[m][e];
-            sh.uk2[u][m] = a.k2t[m][e];
-        }
+#pragma unroll
+        for (int m = 0; m < 3; ++m)
+            if (m < mats) {
+                sh.uptr[u][m] = a.logits ? sh.r.tptr[m][e] : (uint64_t)a.ptr[m][e];
+                sh.uk2[u][m] = a.logits ? sh.r.tk2[m][e] : a.k2t[m][e];
+            }
     }
     __syncthreads();
 }
@@ -195,7 +279,7 @@ __device__ __forceinline__ void route_tables(const DLArgs& a, RouteSh& sh, int m
 // The window's routing in LDS: picks (top-8 of the logits, or the given picks), the distinct picked experts in id
 // order and each one's first R pairs in ascending order (exl3_experts.cu:36-90), and the units' trellis tables
 // (`mats` matrices of each). One row from logits: the units are the picks in order, and a block that runs only units
-// below `need` stops the top-8 there (its loads then start sooner).
+// below `need` stops the top-8 there (its loads then start sooner; the tables of units from `need` on are not set).
 __device__ __forceinline__ void route_block(const DLArgs& a, RouteSh& sh, int mats, int need = DL_SLOTS) {
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const int n = a.R * DL_SLOTS;
@@ -232,20 +316,47 @@ __device__ __forceinline__ void route_block(const DLArgs& a, RouteSh& sh, int ma
         return;
     }
     if (a.logits) {
-        for (int r = wave; r < a.R; r += DL_WAVES)
-            topk8_wave(a.logits + (size_t)r * 256, a.bias, a.scale, sh.r.pick + r * DL_SLOTS, sh.r.wts + r * DL_SLOTS,
-                       lane);
+        // E = 256: every expert's tables are loaded with the logits (a thread an expert); wave w routes rows w, w + 4,
+        // ... side by side
+        uint64_t tp[3];
+        int tk[3];
+#pragma unroll
+        for (int m = 0; m < 3; ++m)
+            if (m < mats) {
+                tp[m] = (uint64_t)a.ptr[m][t];
+                tk[m] = a.k2t[m][t];
+            }
+        const int nr = wave < a.R ? (a.R - wave + DL_WAVES - 1) / DL_WAVES : 0;
+        if (a.R > 2 * DL_WAVES)
+            topk8_rows<4>(a.logits, wave, DL_WAVES, nr, a.bias, a.scale, sh.r.pick, sh.r.wts, lane);
+        else if (a.R > DL_WAVES)
+            topk8_rows<2>(a.logits, wave, DL_WAVES, nr, a.bias, a.scale, sh.r.pick, sh.r.wts, lane);
+        else if (nr > 0)
+            topk8_rows<1>(a.logits, wave, DL_WAVES, nr, a.bias, a.scale, sh.r.pick, sh.r.wts, lane);
+#pragma unroll
+        for (int m = 0; m < 3; ++m)
+            if (m < mats) {
+                sh.r.tptr[m][t] = tp[m];
+                sh.r.tk2[m][t] = tk[m];
+            }
     } else {
         for (int i = t; i < n; i += DL_THREADS) {
             sh.r.pick[i] = a.pick[i];
             sh.r.wts[i] = a.wts[i];
         }
     }
+    // unit[e]: the count of expert e's picks, or (routed from logits, where a row's picks are distinct) the mask of the
+    // rows that pick it
     for (int e = t; e < a.E; e += DL_THREADS) sh.r.unit[e] = 0;
     __syncthreads();
     for (int i = t; i < n; i += DL_THREADS) {
         const int e = sh.r.pick[i];
-        if (e >= 0 && e < a.E) atomicAdd(&sh.r.unit[e], 1);
+        if (e >= 0 && e < a.E) {
+            if (a.logits)
+                atomicOr(&sh.r.unit[e], 1 << (i / DL_SLOTS));
+            else
+                atomicAdd(&sh.r.unit[e], 1);
+        }
     }
     __syncthreads();
     // units in expert order: an exclusive scan of "picked" over experts 4t .. 4t + 3
@@ -268,18 +379,31 @@ __device__ __forceinline__ void route_block(const DLArgs& a, RouteSh& sh, int ma
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
         const int e = 4 * t + q;
-        if (e < a.E && sh.r.unit[e] > 0) sh.uids[place++] = e;
+        if (e < a.E && sh.r.unit[e] > 0) {
+            if (a.logits) sh.r.uidx[e] = place;
+            sh.uids[place++] = e;
+        }
     }
     if (t == DL_THREADS - 1) sh.ucount = place;
     __syncthreads();
     // a unit's members: its first R pairs in pair order (exl3_experts.cu:83-86 with maxm = R, moe.zig:288); a pair
-    // past them keeps its y as it is, as a slot without an expert does
-    for (int u = t; u < sh.ucount; u += DL_THREADS) {
-        const int e = sh.uids[u];
-        int c = 0;
-        for (int i = 0; i < n && c < a.R; ++i)
-            if (sh.r.pick[i] == e) sh.members[u][c++] = (int16_t)i;
-        sh.mcount[u] = c;
+    // past them keeps its y as it is, as a slot without an expert does. From logits a unit has one pair a row that
+    // picks it, so a pair's place is the count of the earlier rows in its expert's mask (a thread a pair).
+    if (a.logits) {
+        for (int i = t; i < n; i += DL_THREADS) {
+            const int e = sh.r.pick[i], r = i / DL_SLOTS, u = sh.r.uidx[e];
+            const uint32_t mask = (uint32_t)sh.r.unit[e];
+            sh.members[u][__builtin_popcount(mask & ((1u << r) - 1u))] = (int16_t)i;
+            if ((mask >> r) == 1u) sh.mcount[u] = __builtin_popcount(mask);  // the unit's last row
+        }
+    } else {
+        for (int u = t; u < sh.ucount; u += DL_THREADS) {
+            const int e = sh.uids[u];
+            int c = 0;
+            for (int i = 0; i < n && c < a.R; ++i)
+                if (sh.r.pick[i] == e) sh.members[u][c++] = (int16_t)i;
+            sh.mcount[u] = c;
+        }
     }
     __syncthreads();
     route_tables(a, sh, mats);
@@ -298,11 +422,52 @@ __device__ __forceinline__ void route_publish(const DLArgs& a, const RouteSh& sh
     for (int u = t; u < sh.ucount; u += DL_THREADS) {
         l.uids[u] = sh.uids[u];
         l.mcount[u] = sh.mcount[u];
-        l.dptr[u] = sh.uptr[u][2];
-        l.dk2[u] = sh.uk2[u][2];
+#pragma unroll
+        for (int m = 0; m < 3; ++m) {
+            l.tptr[u * 3 + m] = sh.uptr[u][m];
+            l.tk2[u * 3 + m] = sh.uk2[u][m];
+        }
         for (int i = 0; i < sh.mcount[u]; ++i) l.members[u * DL_MAXR + i] = sh.members[u][i];
     }
     if (t == 0) *l.ucount = sh.ucount;
+}
+
+// More than one row: one block routes the window (route_kernel) and publishes it, and every gate|up block reads the
+// grouping and the units' gate and up tables back into LDS in one round trip, instead of routing every row itself.
+// Every entry is read (entries past the counts are not used), so all the loads are in flight at once.
+constexpr int DL_MEMW = DL_MAXP * DL_MAXR / DL_THREADS;  // member entries a thread
+__device__ __forceinline__ void route_read(const DLArgs& a, RouteSh& sh) {
+    const int t = threadIdx.x;
+    const DLLayout& l = a.lay;
+    const int tu = t < DL_MAXP ? t : DL_MAXP - 1;
+    const int ucount = *l.ucount, uid = l.uids[tu], mc = l.mcount[tu];
+    const uint64_t p0 = l.tptr[tu * 3], p1 = l.tptr[tu * 3 + 1];
+    const int k0 = l.tk2[tu * 3], k1 = l.tk2[tu * 3 + 1];
+    int mem[DL_MEMW];
+#pragma unroll
+    for (int j = 0; j < DL_MEMW; ++j) mem[j] = l.members[t + j * DL_THREADS];
+    if (t < DL_MAXP) {
+        sh.uids[t] = uid;
+        sh.mcount[t] = mc;
+        sh.uptr[t][0] = p0;
+        sh.uptr[t][1] = p1;
+        sh.uk2[t][0] = k0;
+        sh.uk2[t][1] = k1;
+    }
+#pragma unroll
+    for (int j = 0; j < DL_MEMW; ++j) {
+        const int idx = t + j * DL_THREADS;
+        sh.members[idx / DL_MAXR][idx % DL_MAXR] = (int16_t)mem[j];
+    }
+    if (t == 0) sh.ucount = ucount;
+    __syncthreads();
+}
+
+// The window's routing and grouping, once, for the gate|up blocks and the later launches (more than one row).
+__global__ void __launch_bounds__(DL_THREADS) route_kernel(DLArgs a) {
+    __shared__ RouteSh sh;
+    route_block(a, sh, 3);
+    route_publish(a, sh);
 }
 
 // ---- the MFMA core of an item ------------------------------------------------------------------------------------
@@ -459,8 +624,8 @@ __device__ __forceinline__ bool unit_from_layout(const DLArgs& a, int u, UnitVie
     const DLLayout& l = a.lay;
     const int ur = u > a.hs ? u - a.hs : 0;
     const int ucount = *l.ucount;
-    const int nm = l.mcount[ur], e = l.uids[ur], dk2 = l.dk2[ur];
-    const uint64_t dptr = l.dptr[ur];
+    const int nm = l.mcount[ur], e = l.uids[ur], dk2 = l.tk2[ur * 3 + 2];
+    const uint64_t dptr = l.tptr[ur * 3 + 2];
     if (threadIdx.x < DL_MAXR) s_mem[threadIdx.x] = l.members[ur * DL_MAXR + threadIdx.x];
     if (u >= a.hs + ucount) return false;
     uv.shared = a.hs && u == 0;
@@ -547,18 +712,20 @@ __device__ __forceinline__ uint32_t act_pair(const UnitView& uv, float2 g, float
     return (uint32_t)f2h(v[0] * HAD_SCALE) | ((uint32_t)f2h(v[1] * HAD_SCALE) << 16);
 }
 
-// Block (unit, column block nh of 128): the unit's down inputs, a wave a member.
+// Block (unit, column block nh of 128, group g of DL_WAVES members): the down inputs of the group's members, a wave a
+// member, so that every member's partial sums are in flight at once.
 __global__ void __launch_bounds__(DL_THREADS) epilogue_kernel(DLArgs a) {
     __shared__ int16_t s_mem[DL_MAXR];
-    const int NH = a.I / 128;
-    const int unit = blockIdx.x / NH, nh = blockIdx.x % NH;
+    const int NH = a.I / 128, MG = (a.R + DL_WAVES - 1) / DL_WAVES;
+    const int unit = blockIdx.x / (NH * MG), nh = (blockIdx.x / MG) % NH, grp = blockIdx.x % MG;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     UnitView uv;
     if (!unit_from_layout(a, unit, uv, s_mem)) return;
     __syncthreads();
-    const uint32_t svg = svh_pair(a, uv, nh, 0, lane), svu = svh_pair(a, uv, nh, 1, lane);
-    const uint32_t sd = suhd_pair(a, uv, nh, lane);
-    for (int m = wave; m < uv.nm; m += DL_WAVES) {
+    const int m = grp * DL_WAVES + wave;
+    if (m < uv.nm) {
+        const uint32_t svg = svh_pair(a, uv, nh, 0, lane), svu = svh_pair(a, uv, nh, 1, lane);
+        const uint32_t sd = suhd_pair(a, uv, nh, lane);
         const int q = member_q(a, uv, m);
         float2 zg[DL_MAXKC], zu[DL_MAXKC];
         zp_load(a, q, nh, 0, lane, zg);
@@ -666,18 +833,24 @@ gateup_kernel(DLArgs a) {
         __syncthreads();
     }
     if (it >= items) return;
-    const bool publisher = it == first_routed;
-    int need = DL_SLOTS;  // one row: the picks up to the block's last unit (the publisher needs them all)
-    if (a.logits && a.R == 1 && !publisher) {
-        const int last = it + (items - 1 - it) / (int)gridDim.x * (int)gridDim.x;
-        need = min(DL_SLOTS, last / per_unit - a.hs + 1);
+    if (a.R > 1) {
+        route_read(a, sh);
+    } else {
+        const bool publisher = it == first_routed;
+        int need = DL_SLOTS;  // from logits: the picks up to the block's last unit (the publisher needs them all)
+        if (a.logits && !publisher) {
+            const int last = it + (items - 1 - it) / (int)gridDim.x * (int)gridDim.x;
+            need = min(DL_SLOTS, last / per_unit - a.hs + 1);
+        }
+        route_block(a, sh, publisher ? 3 : 2, need);
+        if (publisher) route_publish(a, sh);
     }
-    route_block(a, sh, publisher ? 3 : 2, need);
-    if (publisher) route_publish(a, sh);
+    // the routed items, in unit order (issuing the next item's loads before the current item's product measured no
+    // faster: with more than one row the items are decode-bound, and the larger kernel slowed the one-row layer)
     const int units = a.hs + sh.ucount;
     for (; it < items; it += gridDim.x) {
         const int u = it / per_unit, rem = it % per_unit;
-        if (u >= units) break;  // items run in unit order
+        if (u >= units) break;
         const int nm = sh.mcount[u - a.hs];
         if (nm < dirty) zero_rows(xs, nm, dirty);
         gateup_item<CB, false>(a, sh, u, rem / (2 * KC), (rem / KC) & 1, rem % KC, xs);
@@ -909,7 +1082,7 @@ static DLCarve dl_carve(uint32_t rows, uint32_t D, uint32_t I, uint32_t E) {
     c.zp = take(Q * c.NH * 2 * KC * 128 * 4);
     c.xd = take(Q * I * 2);
     c.sy = take((size_t)rows * D * 4);
-    c.ws = take((size_t)DL_MAXP * 8 + ((size_t)DL_MAXP + 1 + (size_t)DL_MAXP * DL_MAXR + 2 * DL_MAXP) * 4);
+    c.ws = take((size_t)DL_MAXP * 3 * 8 + ((size_t)DL_MAXP + 1 + (size_t)DL_MAXP * DL_MAXR + 4 * DL_MAXP) * 4);
     c.total = off;
     return c;
 }
@@ -930,13 +1103,13 @@ static DLLayout dl_layout(uint64_t base, uint32_t rows, uint32_t D, uint32_t I, 
     l.zp = dptr<float>(base + c.zp);
     l.xd = dptr<uint16_t>(base + c.xd);
     l.sy = dptr<float>(base + c.sy);
-    l.dptr = dptr<uint64_t>(base + c.ws);  // 256-byte aligned
-    int* ws = dptr<int>(base + c.ws + (size_t)DL_MAXP * 8);
+    l.tptr = dptr<uint64_t>(base + c.ws);  // 256-byte aligned
+    int* ws = dptr<int>(base + c.ws + (size_t)DL_MAXP * 3 * 8);
     l.uids = ws;
     l.ucount = ws + DL_MAXP;
     l.members = l.ucount + 1;
     l.mcount = l.members + DL_MAXP * DL_MAXR;
-    l.dk2 = l.mcount + DL_MAXP;
+    l.tk2 = l.mcount + DL_MAXP;
     return l;
 }
 
@@ -973,6 +1146,11 @@ static int dl_launch(hipStream_t s, const DLArgs& a, int cus, int device) {
     int grid = per_cu * cus;
     if (grid > items) grid = items;
     mark_stage(s, device, 0);
+    if (a.R > 1) {
+        route_kernel<<<1, DL_THREADS, 0, s>>>(a);
+        const int r = launched();
+        if (r) return r;
+    }
     gateup_kernel<CB, SCB><<<grid, DL_THREADS, 0, s>>>(a);
     int r = launched();
     if (r) return r;
@@ -984,7 +1162,7 @@ static int dl_launch(hipStream_t s, const DLArgs& a, int cus, int device) {
         down_fold_kernel<CB, SCB><<<a.U * (DB / FCB), 64 * DL_FOLD_WAVES, 0, s>>>(a);
         if ((r = launched())) return r;
     } else {
-        epilogue_kernel<<<a.U * NH, DL_THREADS, 0, s>>>(a);
+        epilogue_kernel<<<a.U * NH * ((a.R + DL_WAVES - 1) / DL_WAVES), DL_THREADS, 0, s>>>(a);
         if ((r = launched())) return r;
         mark_stage(s, device, 2);
         down_kernel<CB, SCB><<<a.U * DB, DL_THREADS, 0, s>>>(a);
