@@ -110,7 +110,7 @@ struct RouteScratch {
     float wts[DL_MAXP];
     int unit[DL_MAXE];  // count of an expert's picks (mask of the rows that pick it, from logits)
     int uidx[256];      // an expert's unit, from logits
-    int wsum[DL_WAVES];
+    int wsum[16];       // a wave's count of picked experts (up to 16 waves)
     uint64_t tptr[3][256];  // one row's path: every expert's addresses and widths, loaded with the logits
     int tk2[3][256];
 };
@@ -127,85 +127,6 @@ struct RouteSh {
         __attribute__((aligned(16))) uint32_t stage[DL_WAVES][DL_STAGE_WORDS];
     };
 };
-
-// The top-8 of NR rows on one wave, interleaved, for windows of more than one row (one row: topk8_wave below). E =
-// 256: expert q * 64 + lane in choice[q]; choice = sigmoid + bias, the larger first, the lower id on a tie; wts =
-// sigmoid / (sum of the picks' sigmoids in pick order + 1e-20) * scale (native_ops.cu:1015-1068). Row j of the wave is logits row `row0 + j * rstep`; rows from `nrows` on are
-// computed on row0's logits and not written. A round: the wave maximum of the choices' keys (one broadcast), then the
-// lowest id holding it from four ballots, one a key register: the first non-empty ballot names q and its lowest set
-// bit the lane, in scalar registers. A round is a chain of dependent cross-lane steps, so the NR rows' chains run
-// side by side. (Finding the eighth largest key bit by bit and placing the picks by counting, with no rounds,
-// measured slower: 32 dependent ballot counts.) The routing is the serial head of every routed item and its wave
-// shares a SIMD with other blocks' decoding waves, so it runs at the highest wave priority. `rounds` < 8 stops
-// after the first picks (wts are then not written: they need all eight).
-template <int NR>
-__device__ __forceinline__ void topk8_rows(const float* logits, int row0, int rstep, int nrows, const float* bias,
-                                           float scale, int* pick, float* wts, int lane, int rounds = DL_SLOTS) {
-    __builtin_amdgcn_s_setprio(3);
-    // every load in flight before any is used
-    float lg[NR][4], bs[4];
-#pragma unroll
-    for (int q = 0; q < 4; ++q) bs[q] = bias[q * 64 + lane];
-#pragma unroll
-    for (int j = 0; j < NR; ++j) {
-        const int row = j < nrows ? row0 + j * rstep : row0;
-#pragma unroll
-        for (int q = 0; q < 4; ++q) lg[j][q] = logits[(size_t)row * 256 + q * 64 + lane];
-    }
-#pragma unroll
-    for (int j = 0; j < NR; ++j) asm volatile("" : "+v"(lg[j][0]), "+v"(lg[j][1]), "+v"(lg[j][2]), "+v"(lg[j][3]));
-    asm volatile("" : "+v"(bs[0]), "+v"(bs[1]), "+v"(bs[2]), "+v"(bs[3]));
-    float score[NR][4];
-    uint32_t key[NR][4];
-#pragma unroll
-    for (int j = 0; j < NR; ++j)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            score[j][q] = 1.0f / (expf_path(0.0f - lg[j][q]) + 1.0f);
-            key[j][q] = order_key(score[j][q] + bs[q]);
-        }
-    float total[NR], my_w[NR];
-    int my_p[NR];
-#pragma unroll
-    for (int j = 0; j < NR; ++j) {
-        total[j] = 0.0f;
-        my_w[j] = 0.0f;
-        my_p[j] = 0;
-    }
-    for (int k = 0; k < rounds; ++k) {
-#pragma unroll
-        for (int j = 0; j < NR; ++j) {
-            uint32_t(&kj)[4] = key[j];
-            const uint32_t km = kj[0] > kj[1] ? kj[0] : kj[1], kn = kj[2] > kj[3] ? kj[2] : kj[3];
-            const uint32_t m = wave_reduce<true>(km > kn ? km : kn);
-            // some key equals the maximum, so one ballot is non-empty
-            const uint64_t b0 = __builtin_amdgcn_ballot_w64(kj[0] == m), b1 = __builtin_amdgcn_ballot_w64(kj[1] == m);
-            const uint64_t b2 = __builtin_amdgcn_ballot_w64(kj[2] == m), b3 = __builtin_amdgcn_ballot_w64(kj[3] == m);
-            const int q = b0 ? 0 : (b1 ? 1 : (b2 ? 2 : 3));
-            const uint64_t bq = b0 ? b0 : (b1 ? b1 : (b2 ? b2 : b3));
-            const int src = (int)__builtin_ctzll(bq), e = q * 64 + src;
-            const float sq = q == 0 ? score[j][0] : (q == 1 ? score[j][1] : (q == 2 ? score[j][2] : score[j][3]));
-            const float sw = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sq), src));
-            total[j] = total[j] + sw;
-            my_w[j] = lane == k ? sw : my_w[j];
-            my_p[j] = lane == k ? e : my_p[j];
-            const bool mine = lane == src;
-            kj[0] = (mine && q == 0) ? 0u : kj[0];
-            kj[1] = (mine && q == 1) ? 0u : kj[1];
-            kj[2] = (mine && q == 2) ? 0u : kj[2];
-            kj[3] = (mine && q == 3) ? 0u : kj[3];
-        }
-    }
-#pragma unroll
-    for (int j = 0; j < NR; ++j)
-        if (j < nrows) {
-            const int row = row0 + j * rstep;
-            if (lane < rounds) pick[row * DL_SLOTS + lane] = my_p[j];
-            if (rounds == DL_SLOTS && lane < DL_SLOTS)
-                wts[row * DL_SLOTS + lane] = my_w[j] / (total[j] + 1e-20f) * scale;
-        }
-    __builtin_amdgcn_s_setprio(0);
-}
 
 // One row's top-8 on one wave (E = 256: expert q * 64 + lane in choice[q]): choice = sigmoid + bias, the larger
 // first, the lower id on a tie; wts = sigmoid / (sum of the picks' sigmoids in pick order + 1e-20) * scale
@@ -276,75 +197,11 @@ __device__ __forceinline__ void route_tables(const DLArgs& a, RouteSh& sh, int m
     __syncthreads();
 }
 
-// The window's routing in LDS: picks (top-8 of the logits, or the given picks), the distinct picked experts in id
-// order and each one's first R pairs in ascending order (exl3_experts.cu:36-90), and the units' trellis tables
-// (`mats` matrices of each). One row from logits: the units are the picks in order, and a block that runs only units
-// below `need` stops the top-8 there (its loads then start sooner; the tables of units from `need` on are not set).
-__device__ __forceinline__ void route_block(const DLArgs& a, RouteSh& sh, int mats, int need = DL_SLOTS) {
+// The grouping of the picks in sh.r.pick (route_block, route_kernel), by a block of DL_THREADS or more threads: the
+// distinct picked experts in id order, each one's members, the units' tables.
+__device__ __forceinline__ void route_group(const DLArgs& a, RouteSh& sh, int mats) {
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const int n = a.R * DL_SLOTS;
-    if (a.logits && a.R == 1) {
-        // one row: the tables of all 256 experts are loaded with the logits (a thread an expert), so the picks' need
-        // no round trip after the top-8; each pick names a different expert and is a unit of its own
-        uint64_t tp[3];
-        int tk[3];
-#pragma unroll
-        for (int m = 0; m < 3; ++m) {
-            tp[m] = (uint64_t)a.ptr[m][t];
-            tk[m] = a.k2t[m][t];
-        }
-        if (wave == 0) topk8_wave(a.logits, a.bias, a.scale, sh.r.pick, sh.r.wts, lane, need);
-#pragma unroll
-        for (int m = 0; m < 3; ++m) {
-            sh.r.tptr[m][t] = tp[m];
-            sh.r.tk2[m][t] = tk[m];
-        }
-        __syncthreads();
-        if (t < need) {
-            const int e = sh.r.pick[t];
-            sh.uids[t] = e;
-            sh.mcount[t] = 1;
-            sh.members[t][0] = t;
-#pragma unroll
-            for (int m = 0; m < 3; ++m) {
-                sh.uptr[t][m] = sh.r.tptr[m][e];
-                sh.uk2[t][m] = sh.r.tk2[m][e];
-            }
-        }
-        if (t == 0) sh.ucount = DL_SLOTS;
-        __syncthreads();
-        return;
-    }
-    if (a.logits) {
-        // E = 256: every expert's tables are loaded with the logits (a thread an expert); wave w routes rows w, w + 4,
-        // ... side by side
-        uint64_t tp[3];
-        int tk[3];
-#pragma unroll
-        for (int m = 0; m < 3; ++m)
-            if (m < mats) {
-                tp[m] = (uint64_t)a.ptr[m][t];
-                tk[m] = a.k2t[m][t];
-            }
-        const int nr = wave < a.R ? (a.R - wave + DL_WAVES - 1) / DL_WAVES : 0;
-        if (a.R > 2 * DL_WAVES)
-            topk8_rows<4>(a.logits, wave, DL_WAVES, nr, a.bias, a.scale, sh.r.pick, sh.r.wts, lane);
-        else if (a.R > DL_WAVES)
-            topk8_rows<2>(a.logits, wave, DL_WAVES, nr, a.bias, a.scale, sh.r.pick, sh.r.wts, lane);
-        else if (nr > 0)
-            topk8_rows<1>(a.logits, wave, DL_WAVES, nr, a.bias, a.scale, sh.r.pick, sh.r.wts, lane);
-#pragma unroll
-        for (int m = 0; m < 3; ++m)
-            if (m < mats) {
-                sh.r.tptr[m][t] = tp[m];
-                sh.r.tk2[m][t] = tk[m];
-            }
-    } else {
-        for (int i = t; i < n; i += DL_THREADS) {
-            sh.r.pick[i] = a.pick[i];
-            sh.r.wts[i] = a.wts[i];
-        }
-    }
     // unit[e]: the count of expert e's picks, or (routed from logits, where a row's picks are distinct) the mask of the
     // rows that pick it
     for (int e = t; e < a.E; e += DL_THREADS) sh.r.unit[e] = 0;
@@ -409,6 +266,53 @@ __device__ __forceinline__ void route_block(const DLArgs& a, RouteSh& sh, int ma
     route_tables(a, sh, mats);
 }
 
+// The window's routing in LDS: picks (top-8 of the logits, or the given picks), the distinct picked experts in id
+// order and each one's first R pairs in ascending order (exl3_experts.cu:36-90), and the units' trellis tables
+// (`mats` matrices of each). One row from logits: the units are the picks in order, and a block that runs only units
+// below `need` stops the top-8 there (its loads then start sooner; the tables of units from `need` on are not set).
+__device__ __forceinline__ void route_block(const DLArgs& a, RouteSh& sh, int mats, int need = DL_SLOTS) {
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int n = a.R * DL_SLOTS;
+    if (a.logits && a.R == 1) {
+        // one row: the tables of all 256 experts are loaded with the logits (a thread an expert), so the picks' need
+        // no round trip after the top-8; each pick names a different expert and is a unit of its own
+        uint64_t tp[3];
+        int tk[3];
+#pragma unroll
+        for (int m = 0; m < 3; ++m) {
+            tp[m] = (uint64_t)a.ptr[m][t];
+            tk[m] = a.k2t[m][t];
+        }
+        if (wave == 0) topk8_wave(a.logits, a.bias, a.scale, sh.r.pick, sh.r.wts, lane, need);
+#pragma unroll
+        for (int m = 0; m < 3; ++m) {
+            sh.r.tptr[m][t] = tp[m];
+            sh.r.tk2[m][t] = tk[m];
+        }
+        __syncthreads();
+        if (t < need) {
+            const int e = sh.r.pick[t];
+            sh.uids[t] = e;
+            sh.mcount[t] = 1;
+            sh.members[t][0] = t;
+#pragma unroll
+            for (int m = 0; m < 3; ++m) {
+                sh.uptr[t][m] = sh.r.tptr[m][e];
+                sh.uk2[t][m] = sh.r.tk2[m][e];
+            }
+        }
+        if (t == 0) sh.ucount = DL_SLOTS;
+        __syncthreads();
+        return;
+    }
+    // given picks (with more than one row route_kernel routes the window)
+    for (int i = t; i < n; i += DL_THREADS) {
+        sh.r.pick[i] = a.pick[i];
+        sh.r.wts[i] = a.wts[i];
+    }
+    route_group(a, sh, mats);
+}
+
 // One block hands the routing to the caller (pick, wts) and the grouping to the later launches.
 __device__ __forceinline__ void route_publish(const DLArgs& a, const RouteSh& sh) {
     const int t = threadIdx.x;
@@ -463,10 +367,38 @@ __device__ __forceinline__ void route_read(const DLArgs& a, RouteSh& sh) {
     __syncthreads();
 }
 
-// The window's routing and grouping, once, for the gate|up blocks and the later launches (more than one row).
-__global__ void __launch_bounds__(DL_THREADS) route_kernel(DLArgs a) {
+// The window's routing and grouping, once, for the gate|up blocks and the later launches (more than one row): a wave
+// a row's top-8 (DL_MAXR waves), every expert's tables loaded with the logits by the first DL_THREADS threads.
+constexpr int DL_ROUTE_THREADS = 64 * DL_MAXR;
+__global__ void __launch_bounds__(DL_ROUTE_THREADS) route_kernel(DLArgs a) {
+    static_assert(DL_ROUTE_THREADS <= 1024 && DL_ROUTE_THREADS / 64 <= 16, "a wave a row; wsum holds 16 waves");
     __shared__ RouteSh sh;
-    route_block(a, sh, 3);
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    if (a.logits) {
+        const int te = t < 256 ? t : 255;  // E = 256
+        uint64_t tp[3];
+        int tk[3];
+#pragma unroll
+        for (int m = 0; m < 3; ++m) {
+            tp[m] = (uint64_t)a.ptr[m][te];
+            tk[m] = a.k2t[m][te];
+        }
+        if (wave < a.R)
+            topk8_wave(a.logits + (size_t)wave * 256, a.bias, a.scale, sh.r.pick + wave * DL_SLOTS,
+                       sh.r.wts + wave * DL_SLOTS, lane);
+        if (t < 256)
+#pragma unroll
+            for (int m = 0; m < 3; ++m) {
+                sh.r.tptr[m][t] = tp[m];
+                sh.r.tk2[m][t] = tk[m];
+            }
+    } else {
+        for (int i = t; i < a.R * DL_SLOTS; i += DL_ROUTE_THREADS) {
+            sh.r.pick[i] = a.pick[i];
+            sh.r.wts[i] = a.wts[i];
+        }
+    }
+    route_group(a, sh, 3);  // its first barrier orders the picks and tables before their readers
     route_publish(a, sh);
 }
 
@@ -1147,7 +1079,7 @@ static int dl_launch(hipStream_t s, const DLArgs& a, int cus, int device) {
     if (grid > items) grid = items;
     mark_stage(s, device, 0);
     if (a.R > 1) {
-        route_kernel<<<1, DL_THREADS, 0, s>>>(a);
+        route_kernel<<<1, DL_ROUTE_THREADS, 0, s>>>(a);
         const int r = launched();
         if (r) return r;
     }
