@@ -480,22 +480,12 @@ __device__ __forceinline__ int member_q(const DLArgs& a, const UnitView& uv, int
 }
 __device__ __forceinline__ int member_row(const UnitView& uv, int m) { return uv.shared ? m : uv.mem[m] / DL_SLOTS; }
 
-// A slice of a unit's down matrix that one of the unit's gate|up items reads ahead, one dword a lane a 64-byte line
-// apart, after its own trellis: the down launch then finds those lines in the memory-side cache instead of HBM. The
-// value read is not used.
-struct DownAhead {
-    __amdgpu_buffer_rsrc_t r;  // the down matrix (no records when nothing is read ahead)
-    int off;                   // the slice's first byte
-    int last;                  // its last line's offset in the slice
-    int end;                   // the matrix's last dword: every offset read is clamped to it
-};
-
-// The item's product for one width: prefetch every trellis word (and the down slice), rotate the activations of the
-// k chunk into xs (xs[m][k] = fp16(((x * suh) @ H) * HAD_SCALE), a wave a (row, 128-block)), then the MFMAs.
+// The item's product for one width: prefetch every trellis word, rotate the activations of the k chunk into xs
+// (xs[m][k] = fp16(((x * suh) @ H) * HAD_SCALE), a wave a (row, 128-block)), then the MFMAs.
 template <int CB>
 __device__ __forceinline__ bool gateup_product(const DLArgs& a, const UnitView& uv, const TileSpan& sp, int k2,
                                                const uint16_t* suh, int c, uint16_t* xs, uint32_t* st,
-                                               const DownAhead& da, uint32_t& ahead, f4v (&acc)[2]) {
+                                               f4v (&acc)[2]) {
     const int lane = opaque_lane(threadIdx.x & 63), wave = uniform((int)threadIdx.x >> 6);
     const LaneQuad lq = lane_quad(k2, lane);
     // activations and suh of this wave's (row, block) tasks, then the trellis: loads complete in order, so the
@@ -515,8 +505,6 @@ __device__ __forceinline__ bool gateup_product(const DLArgs& a, const UnitView& 
     }
     u4v v[stage_loads<DL_KT>()];
     stage_issue<DL_KT>(sp, k2, lane, v);
-    ahead = __builtin_amdgcn_raw_buffer_load_b32(da.r, min(da.off + min((wave * 64 + lane) * 64, da.last), da.end), 0,
-                                                 0);
     issued();
 #pragma unroll
     for (int i = 0; i < MT; ++i) {
@@ -706,26 +694,7 @@ __device__ __forceinline__ void gateup_item(const DLArgs& a, RouteSh& sh, int u,
         sp.kstride = ns * TWB;
         suh = (mat ? a.suh_u : a.suh_g) + (size_t)uv.e * a.D;
     }
-    // the unit's down matrix: slice (nh, mat, c) of the unit's items. One row routed from logits: the block's
-    // routing holds the down address of every unit up to its own (route_block); otherwise a block that does not
-    // publish the routing holds only the gate and up tables and reads nothing ahead.
-    DownAhead da;
-    {
-        const int per_unit = NH * 2 * KC, rem = (nh * 2 + mat) * KC + c;
-        const bool on = SHARED || (a.logits && a.R == 1);
-        const uint32_t* dT = SHARED ? a.sh_w[2] : (on ? uniform(reinterpret_cast<const uint32_t*>(sh.uptr[ur][2]))
-                                                      : nullptr);
-        const int dk2 = SHARED ? a.sh_k2 : (on ? uniform(sh.uk2[ur][2]) : 0);
-        const bool fits = on && dT && dk2 >= 2 && dk2 <= DL_MAXK2;
-        const uint32_t bytes = fits ? (uint32_t)((a.I / 16) * (a.D / 16) * 16 * dk2) : 0u;
-        const int slice = ((int)((bytes + per_unit - 1) / per_unit) + 63) & ~63;
-        da.r = buffer_rsrc(fits ? dT : static_cast<const uint32_t*>(a.x), bytes);
-        da.off = rem * slice;
-        da.last = slice > 64 ? slice - 64 : 0;
-        da.end = bytes >= 4 ? (int)bytes - 4 : 0;
-    }
-    uint32_t ahead;
-    const bool ok = gateup_product<CB>(a, uv, sp, k2, suh, c, xs, sh.stage[wave], da, ahead, acc);
+    const bool ok = gateup_product<CB>(a, uv, sp, k2, suh, c, xs, sh.stage[wave], acc);
     if (!ok && lane == 0) record_error(a.status, DEV_UNSUPPORTED_WIDTH);
     // partial sums of this chunk: zp[q][nh][mat][c][128]
 #pragma unroll
@@ -738,7 +707,6 @@ __device__ __forceinline__ void gateup_item(const DLArgs& a, RouteSh& sh, int u,
                 a.lay.zp[((((size_t)member_q(a, uv, m) * NH + nh) * 2 + mat) * KC + c) * 128 + col] = acc[j][i];
             }
         }
-    asm volatile("" ::"v"(ahead));  // the read-ahead is kept (its value is not needed)
 }
 
 template <int CB, int SCB>
