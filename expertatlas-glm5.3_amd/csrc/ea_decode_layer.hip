@@ -341,29 +341,31 @@ __device__ __forceinline__ void route_publish(const DLArgs& a, const RouteSh& sh
 // Every entry is read (entries past the counts are not used), so all the loads are in flight at once.
 constexpr int DL_MEMW = DL_MAXP * DL_MAXR / DL_THREADS;  // member entries a thread
 __device__ __forceinline__ void route_read(const DLArgs& a, RouteSh& sh) {
-    const int t = threadIdx.x;
-    const DLLayout& l = a.lay;
-    const int tu = t < DL_MAXP ? t : DL_MAXP - 1;
-    const int ucount = *l.ucount, uid = l.uids[tu], mc = l.mcount[tu];
-    const uint64_t p0 = l.tptr[tu * 3], p1 = l.tptr[tu * 3 + 1];
-    const int k0 = l.tk2[tu * 3], k1 = l.tk2[tu * 3 + 1];
-    int mem[DL_MEMW];
+    const int t = threadIdx.x;  // the first DL_THREADS threads of the block read
+    if (t < DL_THREADS) {
+        const DLLayout& l = a.lay;
+        const int tu = t < DL_MAXP ? t : DL_MAXP - 1;
+        const int ucount = *l.ucount, uid = l.uids[tu], mc = l.mcount[tu];
+        const uint64_t p0 = l.tptr[tu * 3], p1 = l.tptr[tu * 3 + 1];
+        const int k0 = l.tk2[tu * 3], k1 = l.tk2[tu * 3 + 1];
+        int mem[DL_MEMW];
 #pragma unroll
-    for (int j = 0; j < DL_MEMW; ++j) mem[j] = l.members[t + j * DL_THREADS];
-    if (t < DL_MAXP) {
-        sh.uids[t] = uid;
-        sh.mcount[t] = mc;
-        sh.uptr[t][0] = p0;
-        sh.uptr[t][1] = p1;
-        sh.uk2[t][0] = k0;
-        sh.uk2[t][1] = k1;
-    }
+        for (int j = 0; j < DL_MEMW; ++j) mem[j] = l.members[t + j * DL_THREADS];
+        if (t < DL_MAXP) {
+            sh.uids[t] = uid;
+            sh.mcount[t] = mc;
+            sh.uptr[t][0] = p0;
+            sh.uptr[t][1] = p1;
+            sh.uk2[t][0] = k0;
+            sh.uk2[t][1] = k1;
+        }
 #pragma unroll
-    for (int j = 0; j < DL_MEMW; ++j) {
-        const int idx = t + j * DL_THREADS;
-        sh.members[idx / DL_MAXR][idx % DL_MAXR] = (int16_t)mem[j];
+        for (int j = 0; j < DL_MEMW; ++j) {
+            const int idx = t + j * DL_THREADS;
+            sh.members[idx / DL_MAXR][idx % DL_MAXR] = (int16_t)mem[j];
+        }
+        if (t == 0) sh.ucount = ucount;
     }
-    if (t == 0) sh.ucount = ucount;
     __syncthreads();
 }
 
@@ -482,7 +484,7 @@ __device__ __forceinline__ int member_row(const UnitView& uv, int m) { return uv
 
 // The item's product for one width: prefetch every trellis word, rotate the activations of the k chunk into xs
 // (xs[m][k] = fp16(((x * suh) @ H) * HAD_SCALE), a wave a (row, 128-block)), then the MFMAs.
-template <int CB>
+template <int CB, int NW>
 __device__ __forceinline__ bool gateup_product(const DLArgs& a, const UnitView& uv, const TileSpan& sp, int k2,
                                                const uint16_t* suh, int c, uint16_t* xs, uint32_t* st,
                                                f4v (&acc)[2]) {
@@ -491,12 +493,12 @@ __device__ __forceinline__ bool gateup_product(const DLArgs& a, const UnitView& 
     // activations and suh of this wave's (row, block) tasks, then the trellis: loads complete in order, so the
     // rotation waits only for the first two while the trellis is in flight. The trellis goes to the wave's LDS region
     // after the block barrier, so the barrier never waits for it.
-    constexpr int MT = 2 * DL_MAXR / DL_WAVES;
+    constexpr int MT = 2 * DL_MAXR / NW;
     uint32_t xv[MT], sv[MT];
     const int ntask = 2 * uv.nm;
 #pragma unroll
     for (int i = 0; i < MT; ++i) {
-        const int task = min(wave + DL_WAVES * i, ntask - 1);  // unconditional (see stage_issue); extra lanes repeat
+        const int task = min(wave + NW * i, ntask - 1);  // unconditional (see stage_issue); extra lanes repeat
         const int m = task >> 1, blk = task & 1;
         const int k = c * 256 + blk * 128 + 2 * lane;
         const uint16_t* xr = static_cast<const uint16_t*>(a.x) + (size_t)member_row(uv, m) * a.x_stride;
@@ -514,7 +516,7 @@ __device__ __forceinline__ bool gateup_product(const DLArgs& a, const UnitView& 
     const bool bf = a.x_dtype == BF16;
 #pragma unroll
     for (int i = 0; i < MT; ++i) {
-        const int task = wave + DL_WAVES * i;
+        const int task = wave + NW * i;
         if (task < ntask) {
             const int m = task >> 1, blk = task & 1;
             const uint16_t xl = (uint16_t)(xv[i] & 0xffffu), xh = (uint16_t)(xv[i] >> 16);
@@ -658,11 +660,17 @@ __global__ void __launch_bounds__(DL_THREADS) epilogue_kernel(DLArgs a) {
 
 // Item (unit u, column block nh, matrix mat, k chunk c) of the shared expert (SHARED, codebook CB) or of a routed
 // unit.
-template <int CB, bool SHARED>
+// NW = 2 * DL_WAVES (more than one row, I = 256): the block covers both column blocks of the unit, waves from
+// DL_WAVES on the second (nh is then the wave's), and rotates the members' activations once for both; st is the
+// wave's trellis staging.
+template <int CB, bool SHARED, int NW = DL_WAVES>
 __device__ __forceinline__ void gateup_item(const DLArgs& a, RouteSh& sh, int u, int nh, int mat, int c,
-                                            uint16_t* xs) {
+                                            uint16_t* xs, uint32_t* st) {
+    static_assert(NW == DL_WAVES || NW == 2 * DL_WAVES, "one or both column blocks of 128");
     const int lane = threadIdx.x & 63, wave = uniform((int)threadIdx.x >> 6);
     const int KC = a.D / 256, NH = a.I / 128;
+    const int wl = wave & (DL_WAVES - 1);  // the wave within its column block
+    if (NW != DL_WAVES) nh = wave / DL_WAVES;
     UnitView uv;
     uv.shared = SHARED;
     const int ur = u - a.hs;
@@ -670,7 +678,7 @@ __device__ __forceinline__ void gateup_item(const DLArgs& a, RouteSh& sh, int u,
     uv.e = SHARED ? -1 : uniform(sh.uids[ur]);
     uv.mem = SHARED ? nullptr : sh.members[ur];
     // wave w: n tiles nh * 8 + 2w, + 1 over the 16 k tiles of chunk c
-    const int nt0 = nh * 8 + 2 * wave, kt0 = c * DL_KT;
+    const int nt0 = nh * 8 + 2 * wl, kt0 = c * DL_KT;
     f4v acc[2] = {f4v{0.f, 0.f, 0.f, 0.f}, f4v{0.f, 0.f, 0.f, 0.f}};
     // matrix D x I: routed in the expert layout (tile (kt, nt) at (kt * I / 16 + nt) * TW words), the shared expert
     // in strips ([I / 128][D / 16][8][TW])
@@ -694,7 +702,7 @@ __device__ __forceinline__ void gateup_item(const DLArgs& a, RouteSh& sh, int u,
         sp.kstride = ns * TWB;
         suh = (mat ? a.suh_u : a.suh_g) + (size_t)uv.e * a.D;
     }
-    const bool ok = gateup_product<CB>(a, uv, sp, k2, suh, c, xs, sh.stage[wave], acc);
+    const bool ok = gateup_product<CB, NW>(a, uv, sp, k2, suh, c, xs, st, acc);
     if (!ok && lane == 0) record_error(a.status, DEV_UNSUPPORTED_WIDTH);
     // partial sums of this chunk: zp[q][nh][mat][c][128]
 #pragma unroll
@@ -703,7 +711,7 @@ __device__ __forceinline__ void gateup_item(const DLArgs& a, RouteSh& sh, int u,
         for (int i = 0; i < 4; ++i) {
             const int m = 4 * (lane >> 4) + i;
             if (m < uv.nm) {
-                const int col = (2 * wave + j) * 16 + (lane & 15);
+                const int col = (2 * wl + j) * 16 + (lane & 15);
                 a.lay.zp[((((size_t)member_q(a, uv, m) * NH + nh) * 2 + mat) * KC + c) * 128 + col] = acc[j][i];
             }
         }
@@ -729,7 +737,7 @@ gateup_kernel(DLArgs a) {
     int dirty = a.R;  // rows that may hold an earlier item's activations
     int it = blockIdx.x;
     for (; it < items && it < first_routed; it += gridDim.x) {
-        gateup_item<SCB, true>(a, sh, 0, it / (2 * KC), (it / KC) & 1, it % KC, xs);
+        gateup_item<SCB, true>(a, sh, 0, it / (2 * KC), (it / KC) & 1, it % KC, xs, sh.stage[uniform((int)threadIdx.x >> 6)]);
         __syncthreads();
     }
     if (it >= items) return;
@@ -753,7 +761,45 @@ gateup_kernel(DLArgs a) {
         if (u >= units) break;
         const int nm = sh.mcount[u - a.hs];
         if (nm < dirty) zero_rows(xs, nm, dirty);
-        gateup_item<CB, false>(a, sh, u, rem / (2 * KC), (rem / KC) & 1, rem % KC, xs);
+        gateup_item<CB, false>(a, sh, u, rem / (2 * KC), (rem / KC) & 1, rem % KC, xs,
+                               sh.stage[uniform((int)threadIdx.x >> 6)]);
+        dirty = nm;
+        __syncthreads();
+    }
+}
+
+// More than one row with I = 256: items (unit, matrix, k chunk) over both column blocks, blocks of 2 * DL_WAVES
+// waves, the routing read from route_kernel's output. Each item rotates its members' activations once for both column
+// blocks (a block of DL_WAVES waves per column block rotates them twice).
+template <int CB, int SCB>
+__global__ void __launch_bounds__(2 * DL_THREADS) __attribute__((amdgpu_waves_per_eu(2)))
+gateup_wide_kernel(DLArgs a) {
+    constexpr int NW = 2 * DL_WAVES, NT = 64 * NW;
+    __shared__ RouteSh sh;
+    __shared__ __attribute__((aligned(16))) uint32_t stage_hi[DL_WAVES][DL_STAGE_WORDS];  // waves DL_WAVES.. 2 DL_WAVES
+    __shared__ __attribute__((aligned(16))) uint16_t xs[DL_MAXR * DL_RS];
+    const int KC = a.D / 256;
+    const int per_unit = 2 * KC;
+    const int items = a.U * per_unit;
+    const int first_routed = a.hs * per_unit;
+    const int wave = uniform((int)threadIdx.x >> 6);
+    uint32_t* st = wave < DL_WAVES ? sh.stage[wave] : stage_hi[wave - DL_WAVES];
+    zero_rows<NT>(xs, a.R, DL_MAXR);
+    int dirty = a.R;
+    int it = blockIdx.x;
+    for (; it < items && it < first_routed; it += gridDim.x) {
+        gateup_item<SCB, true, NW>(a, sh, 0, 0, it / KC, it % KC, xs, st);
+        __syncthreads();
+    }
+    if (it >= items) return;
+    route_read(a, sh);
+    const int units = a.hs + sh.ucount;
+    for (; it < items; it += gridDim.x) {
+        const int u = it / per_unit, rem = it % per_unit;
+        if (u >= units) break;
+        const int nm = sh.mcount[u - a.hs];
+        if (nm < dirty) zero_rows<NT>(xs, nm, dirty);
+        gateup_item<CB, false, NW>(a, sh, u, 0, rem / KC, rem % KC, xs, st);
         dirty = nm;
         __syncthreads();
     }
@@ -1033,17 +1079,24 @@ static void mark_stage(hipStream_t s, int device, int k) {
 
 template <int CB, int SCB>
 static int dl_launch(hipStream_t s, const DLArgs& a, int cus, int device) {
-    static int per_cu = 0;  // resident gate|up blocks a CU, once per instantiation
+    static int per_cu = 0, per_cu_wide = 0;  // resident gate|up blocks a CU, once per instantiation
     if (per_cu == 0) {
         int n = 0;
         if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, gateup_kernel<CB, SCB>, DL_THREADS, 0) != hipSuccess ||
             n < 1)
             n = 1;
         per_cu = n;
+        n = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, gateup_wide_kernel<CB, SCB>, 2 * DL_THREADS, 0) !=
+                hipSuccess ||
+            n < 1)
+            n = 1;
+        per_cu_wide = n;
     }
     const int NH = a.I / 128, KC = a.D / 256, DB = a.D / 128;
-    const int items = a.U * NH * 2 * KC;
-    int grid = per_cu * cus;
+    const bool wide = a.R > 1 && NH == 2;  // items over both column blocks
+    const int items = a.U * (wide ? 1 : NH) * 2 * KC;
+    int grid = (wide ? per_cu_wide : per_cu) * cus;
     if (grid > items) grid = items;
     mark_stage(s, device, 0);
     if (a.R > 1) {
@@ -1051,7 +1104,10 @@ static int dl_launch(hipStream_t s, const DLArgs& a, int cus, int device) {
         const int r = launched();
         if (r) return r;
     }
-    gateup_kernel<CB, SCB><<<grid, DL_THREADS, 0, s>>>(a);
+    if (wide)
+        gateup_wide_kernel<CB, SCB><<<grid, 2 * DL_THREADS, 0, s>>>(a);
+    else
+        gateup_kernel<CB, SCB><<<grid, DL_THREADS, 0, s>>>(a);
     int r = launched();
     if (r) return r;
     mark_stage(s, device, 1);
