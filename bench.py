@@ -6,7 +6,8 @@
 A step is one pass of the hot path over one batch of synthetic input, with every input already in HBM:
   decode (default): one GLM-5.3 MoE layer of a TP=8 rank at batch 1 -- router top-8 from logits,
       the routed experts (moe.routed), the shared expert (EXL3 linears + SwiGLU) and their sum: ea_ffn_moe_decode,
-      three launches at one row (gate|up, down with the SwiGLU epilogue, combine), four above;
+      three launches at one row (gate|up, down with the SwiGLU epilogue, combine), five above (route, gate|up,
+      epilogue, down, combine);
   multi (config 3): the same layer at 16 rows, uniform top-8, 70 % of the experts at 3 bits;
   stack (config 5): 75 resident layers (3-bit for 70 % of the experts), one token through all of them (us / token);
   linear (config 1): one 4-bit EXL3 linear 6144 x 2048 at one row (linear.call);
@@ -380,7 +381,10 @@ def run_decode(args, torch, np) -> dict:
         durs = [ms[0] for _, ms in ev]
         nbytes = [bench.gateup_bytes(j, picks) for j, _ in ev]
         kernel = ("gateup_kernel (ea_ffn_moe_decode's first launch: per-block top-8 and grouping, then the gate and "
-                  "up EXL3 GEMV of every touched routed expert and of the shared expert)")
+                  "up EXL3 GEMV of every touched routed expert and of the shared expert)" if R == 1 else
+                  "route_kernel + gateup_wide_kernel (ea_ffn_moe_decode's first two launches, timed together: the "
+                  "window's top-8 and grouping once, then the gate and up EXL3 GEMV of every touched routed expert and "
+                  "of the shared expert)")
         stages = {name: round(sum(ms[k] for _, ms in ev) / len(ev) * 1e3, 3)
                   for k, name in enumerate(("gateup_us", "epilogue_us", "down_us", "combine_us"))}
     else:

@@ -136,7 +136,7 @@ int ea_moe_scratch_init(ea_stream_t stream, ea_moe_scratch* s, void* base, size_
 
 /* out fp32 [R, D] = the R rows' routed experts weighted by wts. Replaces moe.routed (moe.zig:279-293).
  * x: [R, D] rows x_stride apart; pick int32 / wts fp32 [R, slots]. With a scratch of at most 16 rows, widths
- * 2..10, mcg or mul1 and I of 128 or 256, the decode layer's launches (three at one row, four above); otherwise the
+ * 2..10, mcg or mul1 and I of 128 or 256, the decode layer's launches (three at one row, five above); otherwise the
  * six-launch sequence of moe.zig:279-293. As the reference groups pairs (maxm = R), an expert computes its first R
  * pairs in pair order; a slot past them (picks naming one expert more than R times) reads y as it is, as a slot
  * without an expert does. */
@@ -225,7 +225,7 @@ int ea_add_f32(ea_stream_t stream, float* a, const float* b, size_t n);
 
 /* ---- the decode layer in one call --------------------------------------------------------------------------- */
 
-/* ffnMain's expert part for a decode window in one call (three launches at one row, four above): pick / wts
+/* ffnMain's expert part for a decode window in one call (three launches at one row, five above): pick / wts
  * [R, 8] = top-8 of logits [R, 256] (as
  * ea_topk8, written out), out [R, D] = moe.routed(x) + the shared expert's mlp(x) (gate and up EXL3 linears with
  * bf16 outputs, swiglu2, the down linear with fp32 output), or the routed part alone when shared is NULL.
