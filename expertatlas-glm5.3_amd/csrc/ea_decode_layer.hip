@@ -283,7 +283,8 @@ __device__ __forceinline__ void route_block(const DLArgs& a, RouteSh& sh, int ma
             tp[m] = (uint64_t)a.ptr[m][t];
             tk[m] = a.k2t[m][t];
         }
-        if (wave == 0) topk8_wave(a.logits, a.bias, a.scale, sh.r.pick, sh.r.wts, lane, need);
+        // the routing wave by block, so that the routing waves of a CU's blocks are not all on one SIMD
+        if (wave == (int)(blockIdx.x % DL_WAVES)) topk8_wave(a.logits, a.bias, a.scale, sh.r.pick, sh.r.wts, lane, need);
 #pragma unroll
         for (int m = 0; m < 3; ++m) {
             sh.r.tptr[m][t] = tp[m];
