@@ -15,8 +15,17 @@
 
 namespace ea {
 
-constexpr int IPM = 112;           // routed pairs an item (prompt_experts.cu:55-58, TF_PE_GPM)
+// Routed pairs an item at most. The reference's items hold up to 112 (prompt_experts.cu:55-58, TF_PE_GPM), as do
+// this library's for the register-streaming GEMM of widths above 10 (IPM_WIDE); the staged GEMMs (widths 2..10) take
+// items of up to 48 (three row tiles), which measured 6 % faster at 512 rows and the same at 2048: more blocks of
+// shorter MFMA chains and fewer accumulators, for more decoding of the experts split into several items. A pair's
+// sums do not depend on its item. (An item cap of 48 on the register-streaming path gave wrong results in
+// test_prompt_experts_run[120-32-256-128-12], whose most picked expert then has three items; the cause is not found,
+// so that path keeps the cap it was tested with.)
+constexpr int IPM = 48;
 constexpr int IPM_TILES = IPM / 16;
+constexpr int IPM_WIDE = 112;
+constexpr int IPM_WIDE_TILES = IPM_WIDE / 16;
 constexpr uint32_t CHUNK_ROWS = 4096;  // rows a pass at most (prompt_experts.zig:17)
 constexpr int ROUTE_THREADS = 1024;
 
@@ -35,14 +44,14 @@ __device__ __forceinline__ bool item_at(const int* __restrict__ items, const int
 }
 
 // One block: per-expert counts; exclusive scans over experts of the counts and of both lists' items; items
-// (e, first, cnt <= IPM) of an expert in pair order, each into its list; sorted[] = pair ids grouped by expert (order
+// (e, first, cnt <= ipm) of an expert in pair order, each into its list; sorted[] = pair ids grouped by expert (order
 // within an expert: arrival); pclass[pair] = 1 when the pair's item is in the list of larger items. (prompt_experts.cu:
 // 162-244 with by_count off; the two lists are this library's: they let a launch size its registers for its items'
 // rows, and the larger items split K.)
 __global__ void __launch_bounds__(ROUTE_THREADS) route_kernel(const int* __restrict__ pick, int n, int E,
                                                              int* __restrict__ sorted, int* __restrict__ items,
                                                              int* __restrict__ item_count, int* __restrict__ pclass,
-                                                             int max_items) {
+                                                             int max_items, int ipm) {
     extern __shared__ int sh[];
     int* cnt = sh;          // [E]
     int* cur = sh + E;      // [E]
@@ -61,7 +70,7 @@ __global__ void __launch_bounds__(ROUTE_THREADS) route_kernel(const int* __restr
     for (int q = 0; q < per; ++q) {
         const int e = e0 + q;
         if (e < E) {
-            const int c = cnt[e], full = c / IPM, rem = c - full * IPM;
+            const int c = cnt[e], full = c / ipm, rem = c - full * ipm;
             own[0] += c;
             own[1] += rem > 0 && rem <= SMALL_ROWS;
             own[2] += full + (rem > SMALL_ROWS);
@@ -104,8 +113,8 @@ __global__ void __launch_bounds__(ROUTE_THREADS) route_kernel(const int* __restr
         const int c = cnt[e];
         cur[e] = off;
         start[e] = off;
-        for (int f = 0; f < c; f += IPM) {
-            const int m = min(IPM, c - f);
+        for (int f = 0; f < c; f += ipm) {
+            const int m = min(ipm, c - f);
             const int at = m <= SMALL_ROWS ? si++ : max_items - 1 - bi++;
             if (at >= 0 && at < max_items) {
                 items[3 * at] = e;
@@ -122,15 +131,15 @@ __global__ void __launch_bounds__(ROUTE_THREADS) route_kernel(const int* __restr
         if (e >= 0 && e < E) {
             const int at = atomicAdd(&cur[e], 1);
             sorted[at] = i;
-            const int f = (at - start[e]) / IPM * IPM;  // the first pair of its item, within the expert
-            big = min(IPM, cnt[e] - f) > SMALL_ROWS;
+            const int f = (at - start[e]) / ipm * ipm;  // the first pair of its item, within the expert
+            big = min(ipm, cnt[e] - f) > SMALL_ROWS;
         }
         pclass[i] = big;
     }
 }
 
 // Block (item, n block of NW * NTW tiles, matrix): wave w covers NTW n tiles over the whole K range for all of the
-// item's rows (IPM_TILES groups of 16), so each trellis tile is decoded once per item. Z[mat][pair][n] fp32.
+// item's rows (IPM_WIDE_TILES groups of 16), so each trellis tile is decoded once per item. Z[mat][pair][n] fp32.
 template <int CB, int LO, int HI, int NTW, int NW>
 __global__ void __launch_bounds__(NW * 64) item_gemm_kernel(
     const uint16_t* __restrict__ X0, const uint16_t* __restrict__ X1, const int64_t* __restrict__ TP0,
@@ -144,26 +153,26 @@ __global__ void __launch_bounds__(NW * 64) item_gemm_kernel(
     const uint32_t* T = reinterpret_cast<const uint32_t*>(mat ? TP1[e] : TP0[e]);
     const int k2 = mat ? K2_1[e] : K2_0[e];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    __shared__ int pair_sh[IPM];
-    if (threadIdx.x < IPM) pair_sh[threadIdx.x] = (int)threadIdx.x < cnt ? sorted[first + threadIdx.x] : -1;
+    __shared__ int pair_sh[IPM_WIDE];
+    if (threadIdx.x < IPM_WIDE) pair_sh[threadIdx.x] = (int)threadIdx.x < cnt ? sorted[first + threadIdx.x] : -1;
     __syncthreads();
     const int nt0 = (blockIdx.y * NW + wave) * NTW;
     if (nt0 * 16 >= N) return;
-    const uint16_t* xrow[IPM_TILES];
+    const uint16_t* xrow[IPM_WIDE_TILES];
 #pragma unroll
-    for (int m = 0; m < IPM_TILES; ++m) {
+    for (int m = 0; m < IPM_WIDE_TILES; ++m) {
         const int p = pair_sh[m * 16 + (lane & 15)];
         xrow[m] = p >= 0 ? X + (size_t)p * K : nullptr;
     }
-    f4v acc[IPM_TILES][NTW];
+    f4v acc[IPM_WIDE_TILES][NTW];
 #pragma unroll
-    for (int m = 0; m < IPM_TILES; ++m)
+    for (int m = 0; m < IPM_WIDE_TILES; ++m)
 #pragma unroll
         for (int j = 0; j < NTW; ++j) acc[m][j] = f4v{0.f, 0.f, 0.f, 0.f};
     const int ns = N >> 4;
     const uint32_t* base = T + (size_t)nt0 * 4 * k2;
     const bool ok = EA_K2_SWITCH(k2, LO, HI,
-                                 (wave_tiles<CB, K2V, NTW, IPM_TILES>(base, (size_t)ns * 4 * K2V, K >> 4, 0, xrow,
+                                 (wave_tiles<CB, K2V, NTW, IPM_WIDE_TILES>(base, (size_t)ns * 4 * K2V, K >> 4, 0, xrow,
                                                                       lane, acc)));
     if (!ok) {
         if (lane == 0) record_error(status, DEV_UNSUPPORTED_WIDTH);
@@ -171,7 +180,7 @@ __global__ void __launch_bounds__(NW * 64) item_gemm_kernel(
     }
     float* Zm = Z + (size_t)mat * P * N;
 #pragma unroll
-    for (int m = 0; m < IPM_TILES; ++m)
+    for (int m = 0; m < IPM_WIDE_TILES; ++m)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int row = m * 16 + 4 * (lane >> 4) + i;
@@ -741,7 +750,7 @@ static PromptLayout prompt_layout(const ea_routed* ex, uint32_t rows, uint32_t s
     const uint32_t r = rows < CHUNK_ROWS ? rows : CHUNK_ROWS;
     const size_t n = (size_t)r * slots, D = ex->dims, I = ex->width;
     l.rows = r;
-    l.max_items = (uint32_t)(n / IPM + (n < ex->count ? n : ex->count));
+    l.max_items = (uint32_t)(n / IPM + (n < ex->count ? n : ex->count));  // IPM <= IPM_WIDE: room for either
     size_t off = 0;
     auto take = [&](size_t b) {
         const size_t at = off;
@@ -912,14 +921,15 @@ int ea_prompt_experts_run(ea_stream_t stream, const void* x, int x_dtype, uint32
     for (uint32_t r0 = 0; r0 < R; r0 += sc->rows) {
         const uint32_t n = R - r0 < sc->rows ? R - r0 : sc->rows;
         const uint32_t pairs = n * S;
-        const uint32_t items_n = (uint32_t)(pairs / IPM + (pairs < E ? pairs : E));
+        const int ipm = wide ? IPM_WIDE : IPM;
+        const uint32_t items_n = (uint32_t)(pairs / ipm + (pairs < E ? pairs : E));
         const uint32_t max_items = items_n < sc->max_items ? items_n : sc->max_items;
         const char* xs = static_cast<const char*>(x) + (size_t)r0 * xstride * xb;
         const int32_t* pk = pick + (size_t)r0 * S;
         const float* wt = wts + (size_t)r0 * S;
         route_kernel<<<1, ROUTE_THREADS, 3 * E * sizeof(int), s>>>(pk, (int)pairs, (int)E, dptr<int>(sc->sorted),
                                                                   dptr<int>(sc->items), dptr<int>(sc->count),
-                                                                  dptr<int>(sc->pclass), (int)max_items);
+                                                                  dptr<int>(sc->pclass), (int)max_items, ipm);
         int r = launched();
         if (r) return r;
         r = launch_rot_in(s, xs, x_dtype, xstride, pk, dptr<const uint16_t>(ex->suh_g), dptr<const uint16_t>(ex->suh_u),

@@ -132,7 +132,7 @@ def _prompt_case(ea, R, E, D, I, k2, seed, x_dtype=1, zipf=True, cb=1):
 
 
 @pytest.mark.parametrize("R,E,D,I,k2", [(130, 64, 512, 256, 8), (300, 256, 1024, 256, "mixed"), (40, 32, 256, 128, 6),
-                                        (120, 32, 256, 128, 12)])
+                                        (120, 32, 256, 128, 12), (300, 32, 256, 128, 12), (300, 32, 256, 128, 8)])
 def test_prompt_experts_run(ea, R, E, D, I, k2):
     device, _, _, pe, synth = ea
     k2v = synth.mixed_widths(5, E) if k2 == "mixed" else k2
