@@ -199,7 +199,7 @@ constexpr int PW = 4;                             // waves a block: 8 column til
 constexpr int PSTAGE = PK * 2 * 4 * STAGE_MAXK2;  // a wave's staged trellis words a chunk
 constexpr int DNG = 8;                            // down matrix: column blocks of 128 a block (small items)
 constexpr int DNG_BIG = 2;                        // the same for the larger items: more blocks for fewer items
-constexpr int GU_SPLIT = 4;                       // K splits of a larger item's gate|up
+constexpr int GU_SPLIT = 2;                       // K splits of a larger item's gate|up (4 and 8 measured slower)
 // The number of K splits of a larger item's gate|up over K (at most one a chunk).
 static int gu_splits(int K) { return K / (PK * 16) < GU_SPLIT ? K / (PK * 16) : GU_SPLIT; }
 constexpr int DXS = 2 * PK * 16 + 8;              // down matrix: LDS row stride of the activations (K up to 256)
