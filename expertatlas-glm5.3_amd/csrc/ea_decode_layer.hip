@@ -38,7 +38,7 @@ constexpr int DL_MAXKC = 24;                 // k chunks of 256 (D up to 6144)
 constexpr int DL_MAXK2 = STAGE_MAXK2;        // widest trellis (K2) the decode layer runs
 constexpr int DL_STAGE_WORDS = DL_KT * 2 * 4 * DL_MAXK2;  // a wave's staged trellis words: 16 rows of 2 tiles
 
-// Scratch of the four launches, carved on the host for the scratch's row capacity (any R up to it runs).
+// Scratch of the layer's launches, carved on the host for the scratch's row capacity (any R up to it runs).
 struct DLLayout {
     float* zp;          // [Q, NH, 2, KC, 128] gate|up partial sums, Q = pairs + rows (the shared expert's rows last)
     uint16_t* xd;       // [Q, I] down inputs
@@ -1060,7 +1060,8 @@ static DLLayout dl_layout(uint64_t base, uint32_t rows, uint32_t D, uint32_t I, 
     return l;
 }
 
-// Stage events for benchmarks (ea_profile_enable): recorded on the call's stream around the four launches.
+// Stage events for benchmarks (ea_profile_enable): recorded on the call's stream around the layer's stages (route
+// and gate|up, epilogue, down, combine).
 constexpr int DL_STAGES = 4;
 struct DLProfile {
     bool on = false, recorded = false;
@@ -1132,7 +1133,7 @@ static int dl_launch(hipStream_t s, const DLArgs& a, int cus, int device) {
     return EA_OK;
 }
 
-// The decode layer in four launches: routing from logits (when given), the routed experts of `ex`, the shared expert
+// The decode layer in three to five launches: routing from logits (when given), the routed experts of `ex`, the shared expert
 // (when given) and their sum into out [R, D]. EA_UNPORTED_GROUPED_VARIANT when the shape, widths or codebooks are
 // not instantiated here; the caller then runs the launch sequence.
 int decode_layer(hipStream_t s, const void* x, int x_dtype, uint32_t x_stride, const float* logits,
