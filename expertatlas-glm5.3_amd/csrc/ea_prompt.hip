@@ -198,7 +198,7 @@ constexpr int PXS = PK * 16 + 8;                  // LDS row stride of a staged 
 constexpr int PW = 4;                             // waves a block: 8 column tiles, 128 columns
 constexpr int PSTAGE = PK * 2 * 4 * STAGE_MAXK2;  // a wave's staged trellis words a chunk
 constexpr int DNG = 16;  // down matrix: column blocks of 128 a block, small items (8, 24 and 48 measured slower at 512 rows)
-constexpr int DNG_BIG = 2;                        // the same for the larger items: more blocks for fewer items
+constexpr int DNG_BIG = 2;  // the same for the larger items: more blocks for fewer items (4: 1 % slower at 512 rows)
 constexpr int GU_SPLIT = 2;                       // K splits of a larger item's gate|up (4 and 8 measured slower)
 // The number of K splits of a larger item's gate|up over K (at most one a chunk).
 static int gu_splits(int K) { return K / (PK * 16) < GU_SPLIT ? K / (PK * 16) : GU_SPLIT; }
