@@ -51,24 +51,25 @@ __global__ void __launch_bounds__(256) unpack_kernel(const uint32_t* __restrict_
 }
 
 // ---- router top-8 ----------------------------------------------------------------------------------------------
-// One block a row, a thread an expert (E = 256). Eight rounds of a block arg-max over choice = sigmoid + bias, the
-// lower id winning ties; the winner's choice becomes -inf (native_ops.cu:1015-1068).
+// One block a row, a thread an expert (E = 256). Eight rounds of a block arg-max over the ranking key of choice =
+// sigmoid + bias (order_key: NaN below every number), the lower id winning ties; the winner's key becomes 0, below
+// every choice (native_ops.cu:1015-1068).
 __global__ void __launch_bounds__(256) topk8_kernel(const float* __restrict__ logits, const float* __restrict__ bias,
                                                     int32_t* __restrict__ pick, float* __restrict__ wts, float scale,
                                                     uint8_t* __restrict__ log) {
-    __shared__ float s_val[4];
+    __shared__ uint32_t s_key[4];
     __shared__ int s_idx[4];
     __shared__ float s_wts[8];
     __shared__ int s_pick[8];
     const int r = blockIdx.x, t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const float score = 1.0f / (expf_path(0.0f - logits[(size_t)r * 256 + t]) + 1.0f);
-    float choice = score + bias[t];
+    uint32_t key = order_key(score + bias[t]);
     for (int k = 0; k < 8; ++k) {
-        float v = choice;
+        uint32_t v = key;
         int i = t;
 #pragma unroll
         for (int o = 32; o > 0; o >>= 1) {
-            const float ov = __shfl_xor(v, o, 64);
+            const uint32_t ov = (uint32_t)__shfl_xor((int)v, o, 64);
             const int oi = __shfl_xor(i, o, 64);
             if (ov > v || (ov == v && oi < i)) {
                 v = ov;
@@ -76,23 +77,23 @@ __global__ void __launch_bounds__(256) topk8_kernel(const float* __restrict__ lo
             }
         }
         if (lane == 0) {
-            s_val[wave] = v;
+            s_key[wave] = v;
             s_idx[wave] = i;
         }
         __syncthreads();
-        float bv = s_val[0];
+        uint32_t bv = s_key[0];
         int bi = s_idx[0];
 #pragma unroll
         for (int w = 1; w < 4; ++w)
-            if (s_val[w] > bv || (s_val[w] == bv && s_idx[w] < bi)) {
-                bv = s_val[w];
+            if (s_key[w] > bv || (s_key[w] == bv && s_idx[w] < bi)) {
+                bv = s_key[w];
                 bi = s_idx[w];
             }
         __syncthreads();  // every thread has read the winners before the next round writes them
         if (t == bi) {
             s_pick[k] = bi;
             s_wts[k] = score;
-            choice = -__builtin_inff();
+            key = 0u;
         }
     }
     __syncthreads();
@@ -229,6 +230,13 @@ int ea_device_status(int* code) {
     int r = hip_status(hipMemcpy(code, c->status, sizeof(int), hipMemcpyDeviceToHost));
     if (r) return r;
     return hip_status(hipMemset(c->status, 0, sizeof(int)));
+}
+
+int ea_device_status_address(void** addr) {
+    EA_REQUIRE_CTX(c);
+    if (!addr) return EA_BAD_ARGUMENT;
+    *addr = c->status;
+    return EA_OK;
 }
 
 static int unpack_launch(ea_stream_t stream, const void* t, void* w, uint32_t kdim, uint32_t n, uint32_t k2,

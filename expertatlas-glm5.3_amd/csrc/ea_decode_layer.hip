@@ -76,14 +76,6 @@ struct DLArgs {
 
 // ---- the router and the grouping, per block ------------------------------------------------------------------------
 
-// An order-preserving integer key of a float: a larger float has a larger key, +0 and -0 share one, and NaN sits just
-// above 0, the key of a taken expert.
-__device__ __forceinline__ uint32_t order_key(float f) {
-    const uint32_t b = __builtin_bit_cast(uint32_t, f + 0.0f);
-    const uint32_t k = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
-    return f != f ? 1u : k;
-}
-
 // The largest (MAX) or smallest key over the wavefront, in every lane: DPP within rows of 16 (quad swaps, rotations
 // by 4 and 8), then row broadcasts 15 and 31 leave the result in lane 63. Integer compares fold into the DPP moves.
 template <int CTRL, int ROW_MASK, bool MAX>
@@ -704,7 +696,10 @@ __device__ __forceinline__ void gateup_item(const DLArgs& a, RouteSh& sh, int u,
         suh = (mat ? a.suh_u : a.suh_g) + (size_t)uv.e * a.D;
     }
     const bool ok = gateup_product<CB, NW>(a, uv, sp, k2, suh, c, xs, st, acc);
-    if (!ok && lane == 0) record_error(a.status, DEV_UNSUPPORTED_WIDTH);
+    if (!ok) {
+        if (lane == 0) record_error(a.status, DEV_UNSUPPORTED_WIDTH);
+        acc[0] = acc[1] = nan4();
+    }
     // partial sums of this chunk: zp[q][nh][mat][c][128]
 #pragma unroll
     for (int j = 0; j < 2; ++j)
@@ -933,7 +928,10 @@ __device__ __forceinline__ void down_block(const DLArgs& a, uint16_t* xs, DownSh
     const bool ok = a.I == 256
                         ? down_product<CB, SCB, 16, FOLD, NW>(a, uv, sp, k2, xs, ds.gus, ds.stage[wave], acc)
                         : down_product<CB, SCB, 8, FOLD, NW>(a, uv, sp, k2, xs, ds.gus, ds.stage[wave], acc);
-    if (!ok && lane == 0) record_error(a.status, DEV_UNSUPPORTED_WIDTH);
+    if (!ok) {
+        if (lane == 0) record_error(a.status, DEV_UNSUPPORTED_WIDTH);
+        acc[0] = acc[1] = nan4();
+    }
     __syncthreads();  // the column sums overwrite the other waves' staging
     constexpr int YS = 128 * CBB;  // ys row stride
     float* ys = ds.ys;

@@ -78,6 +78,15 @@ __device__ __forceinline__ float expf_path(float x) {
     return x != x ? x : v;
 }
 
+// The router top-8's ranking key of a choice: order-preserving over numbers (a larger float has a larger key, +0 and -0
+// share one), NaN just above 0, the key of a taken expert. A NaN choice so ranks below every number (-inf included),
+// NaNs among themselves by the lower id, and a taken expert is never picked again. Both top-8 paths rank by it.
+__device__ __forceinline__ uint32_t order_key(float f) {
+    const uint32_t b = __builtin_bit_cast(uint32_t, f + 0.0f);
+    const uint32_t k = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+    return f != f ? 1u : k;
+}
+
 // ---- EXL3 trellis -------------------------------------------------------------------------------------------
 // A 16x16 tile is a circular big-endian bit stream of 128 * K2 bits in 4 * K2 words; value p's 16-bit state is
 // stream bits [E(p) - 16, E(p)); value p = 8 L + j sits at row 2 (L & 3) + (j & 1) + 8 ((j >> 1) & 1), column

@@ -15,61 +15,81 @@ namespace ea {
 
 // ---- grouping ---------------------------------------------------------------------------------------------------
 constexpr int GROUP_THREADS = 1024;
-constexpr int GROUP_PER_THREAD = 4;
+constexpr int GROUP_MAXE = 4096;  // experts the presence bitmap holds (experts.zig:99)
 
-// Distinct experts (< E) in id order; members[u][m] = row * 32 + slot in row order, -1 after the last
-// (exl3_experts.cu:36-90).
+// The number of lanes below this one: the lane's place among the set bits of a ballot.
+__device__ __forceinline__ int lanes_below(uint64_t mask) {
+    return (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
+}
+
+// Exclusive prefix sum over the wave of a value below 2^bits, one ballot a bit: a lane's sum is, for every bit, the
+// count of lower lanes with that bit set, times the bit's weight. Every lane gets its own prefix; `total` the sum.
+template <int BITS>
+__device__ __forceinline__ int wave_prefix(int v, int& total) {
+    int below = 0, all = 0;
+#pragma unroll
+    for (int b = 0; b < BITS; ++b) {
+        const uint64_t m = __builtin_amdgcn_ballot_w64((v >> b) & 1);
+        below += lanes_below(m) << b;
+        all += __builtin_popcountll(m) << b;
+    }
+    total = all;
+    return below;
+}
+
+// The distinct picked experts (< E) in id order, and each one's first maxm picks in pick order as row * 32 + slot,
+// -1 after its last (the grouping of exl3_experts.cu:36-90, a different decomposition):
+//   1. every pick sets its expert's bit in an LDS presence bitmap (E <= 4096: 128 words);
+//   2. wave 0 numbers the units: lane l owns bitmap words 2l, 2l + 1; its first unit is the count of set bits in the
+//      lower lanes' words (a bit-sliced ballot prefix), and it lists its experts in bit order;
+//   3. a wave a unit streams the picks 64 at a time: a ballot of the picks naming the unit's expert gives each
+//      match its place (the matches before it in this batch plus all earlier batches), until maxm are placed.
 __global__ void __launch_bounds__(GROUP_THREADS) group_kernel(const int* __restrict__ pick, int* __restrict__ uids,
                                                               int* __restrict__ ucount, int* __restrict__ members,
                                                               int R, int slots, int E, int maxm) {
-    extern __shared__ int sh_pick[];
-    __shared__ int wave_tot[GROUP_THREADS / 64];
-    const int n = R * slots;
-    for (int i = threadIdx.x; i < n; i += GROUP_THREADS) sh_pick[i] = pick[i];
+    extern __shared__ int s_pick[];
+    __shared__ uint32_t s_present[GROUP_MAXE / 32];
+    __shared__ int16_t s_expert[GROUP_MAXE];  // unit -> expert
+    __shared__ int s_units;
+    const int n = R * slots, t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    for (int w = t; w < GROUP_MAXE / 32; w += GROUP_THREADS) s_present[w] = 0u;
     __syncthreads();
-    int cnt[GROUP_PER_THREAD];
-    int used = 0;
-#pragma unroll
-    for (int q = 0; q < GROUP_PER_THREAD; ++q) {
-        const int e = threadIdx.x * GROUP_PER_THREAD + q;
-        int c = 0;
-        if (e < E)
-            for (int i = 0; i < n; ++i) c += sh_pick[i] == e;
-        cnt[q] = c;
-        used += c > 0;
+    for (int i = t; i < n; i += GROUP_THREADS) {
+        const int e = pick[i];
+        s_pick[i] = e;
+        if (e >= 0 && e < E) atomicOr(&s_present[e >> 5], 1u << (e & 31));
     }
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    int inc = used;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        const int v = __shfl_up(inc, o, 64);
-        if (lane >= o) inc += v;
-    }
-    if (lane == 63) wave_tot[wave] = inc;
     __syncthreads();
     if (wave == 0) {
-        const int v = lane < GROUP_THREADS / 64 ? wave_tot[lane] : 0;
-        int s = v;
-#pragma unroll
-        for (int o = 1; o < 64; o <<= 1) {
-            const int x = __shfl_up(s, o, 64);
-            if (lane >= o) s += x;
+        const uint32_t w0 = s_present[2 * lane], w1 = s_present[2 * lane + 1];
+        int total = 0;
+        int u = wave_prefix<7>(__builtin_popcount(w0) + __builtin_popcount(w1), total);  // <= 64 a lane
+        const uint64_t bits = (uint64_t)w0 | ((uint64_t)w1 << 32);
+        for (uint64_t b = bits; b; b &= b - 1) {
+            const int e = 64 * lane + (int)__builtin_ctzll(b);
+            s_expert[u] = (int16_t)e;
+            uids[u++] = e;
         }
-        if (lane < GROUP_THREADS / 64) wave_tot[lane] = s - v;
-        if (lane == GROUP_THREADS / 64 - 1) ucount[0] = s;
+        if (lane == 0) {
+            s_units = total;
+            ucount[0] = total;
+        }
     }
     __syncthreads();
-    int place = wave_tot[wave] + inc - used;
-#pragma unroll
-    for (int q = 0; q < GROUP_PER_THREAD; ++q) {
-        if (cnt[q] == 0) continue;
-        const int e = threadIdx.x * GROUP_PER_THREAD + q;
-        uids[place] = e;
-        int j = 0;
-        for (int i = 0; i < n && j < maxm; ++i)
-            if (sh_pick[i] == e) members[place * maxm + j++] = (i / slots) * 32 + (i % slots);
-        for (; j < maxm; ++j) members[place * maxm + j] = -1;
-        ++place;
+    const int units = s_units;
+    for (int u = wave; u < units; u += GROUP_THREADS / 64) {
+        const int e = s_expert[u];
+        int* mem = members + (size_t)u * maxm;
+        int placed = 0;
+        for (int c = 0; c < n && placed < maxm; c += 64) {
+            const int i = c + lane;
+            const bool hit = i < n && s_pick[i] == e;
+            const uint64_t m = __builtin_amdgcn_ballot_w64(hit);
+            const int at = placed + lanes_below(m);
+            if (hit && at < maxm) mem[at] = (i / slots) * 32 + (i % slots);
+            placed += __builtin_popcountll(m);
+        }
+        for (int j = (placed < maxm ? placed : maxm) + lane; j < maxm; j += 64) mem[j] = -1;
     }
 }
 
@@ -193,7 +213,8 @@ __global__ void __launch_bounds__(NW * 64) grouped_kernel(
                                                               lane, acc)));
     if (!ok) {
         if (threadIdx.x == 0) record_error(status, DEV_UNSUPPORTED_WIDTH);
-        return;
+#pragma unroll
+        for (int j = 0; j < NTW; ++j) acc[0][j] = nan4();
     }
 
     // wave partials through LDS, added in wave order; lane l holds D[4 (l >> 4) + i][l & 15] of each tile
@@ -323,10 +344,11 @@ __global__ void __launch_bounds__(DC_WAVES * 64) down_combine_kernel(
 int launch_group(hipStream_t s, const int* pick, int* uids, int* ucount, int* members, uint32_t rows, uint32_t slots,
                  uint32_t experts, uint32_t maxm) {
     EA_REQUIRE_CTX(c);
-    if (experts > GROUP_THREADS * GROUP_PER_THREAD) return EA_TOO_MANY_EXPERTS;
+    if (experts > GROUP_MAXE) return EA_TOO_MANY_EXPERTS;
     if (slots > 32) return EA_TOO_MANY_SLOTS;
     const size_t smem = (size_t)rows * slots * 4;
-    if (smem + GROUP_THREADS / 64 * 4 > c->lds_optin) return EA_GROUP_SHARED_MEMORY;
+    // the picks, the presence bitmap, the unit -> expert table and the unit count in LDS
+    if (smem + GROUP_MAXE / 8 + GROUP_MAXE * 2 + 4 > c->lds_optin) return EA_GROUP_SHARED_MEMORY;
     if (!pick || !uids || !ucount || !members) return EA_BAD_ARGUMENT;
     group_kernel<<<1, GROUP_THREADS, smem, s>>>(pick, uids, ucount, members, (int)rows, (int)slots, (int)experts,
                                                 (int)maxm);

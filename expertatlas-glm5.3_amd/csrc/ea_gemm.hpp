@@ -146,6 +146,13 @@ __device__ __forceinline__ void wave_tiles(const uint32_t* __restrict__ base, si
 
 __device__ __forceinline__ void record_error(int* status, int code) { atomicCAS(status, 0, code); }
 
+// A product that could not run (a width without a decoder, a bounded wait that gave up) stores NaN in place of its
+// sums, so the call's output shows the failure as well as the status word.
+__device__ __forceinline__ f4v nan4() {
+    const float n = __builtin_nanf("");
+    return f4v{n, n, n, n};
+}
+
 // A raw buffer resource over `bytes` bytes at `base` (gfx9 word 3: 32-bit data, no format conversion). `base` must
 // be wave-uniform.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, uint32_t bytes) {

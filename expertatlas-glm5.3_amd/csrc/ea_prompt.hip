@@ -176,7 +176,10 @@ __global__ void __launch_bounds__(NW * 64) item_gemm_kernel(
                                                                       lane, acc)));
     if (!ok) {
         if (lane == 0) record_error(status, DEV_UNSUPPORTED_WIDTH);
-        return;
+#pragma unroll
+        for (int m = 0; m < IPM_WIDE_TILES; ++m)
+#pragma unroll
+            for (int j = 0; j < NTW; ++j) acc[m][j] = nan4();
     }
     float* Zm = Z + (size_t)mat * P * N;
 #pragma unroll
@@ -384,7 +387,8 @@ item_gu_kernel(const uint16_t* __restrict__ X0, const uint16_t* __restrict__ X1,
         k2, 2, 10, (gu_loop<CB, K2V, MT>(xrs, aoff, lofs, sp, xa, st[wave], lane, tid & 15, mts, c0, nc, acc)));
     if (!ok) {
         if (lane == 0) record_error(status, DEV_UNSUPPORTED_WIDTH);
-        return;
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) acc[mt][0] = acc[mt][1] = nan4();
     }
     float* Zm = (split ? Zp + (size_t)(split - 1) * 2 * P * N : Z) + (size_t)mat * P * N;
 #pragma unroll
@@ -554,7 +558,7 @@ item_ring_kernel(const uint16_t* __restrict__ X0, const uint16_t* __restrict__ X
                                                          nsum, acc, tot, synced)));
     if (!ok || !synced) {
         if (lane == 0) record_error(status, ok ? DEV_SYNC_TIMEOUT : DEV_UNSUPPORTED_WIDTH);
-        return;
+        tot[0][0] = tot[0][1] = nan4();
     }
     float* Zm = Z + (size_t)mat * P * N;
 #pragma unroll
@@ -663,7 +667,14 @@ item_dn_kernel(const uint16_t* __restrict__ X, const int64_t* __restrict__ TP, c
     __syncthreads();  // the activations are in LDS
     const bool ok =
         EA_K2_SWITCH(k2, 2, 10, (dn_loop<CB, K2V, MT, NG>(sp, xa, st[wave], lane, wave, mts, nch, nb0, pair_sh, Z, N)));
-    if (!ok && lane == 0) record_error(status, DEV_UNSUPPORTED_WIDTH);
+    if (!ok) {  // no product ran: the item's outputs of the block's column blocks are NaN
+        if (lane == 0) record_error(status, DEV_UNSUPPORTED_WIDTH);
+        for (int g = 0; g < NG; ++g)
+            for (int i = 0; i < MT * 16; ++i) {
+                const int p = pair_sh[i];
+                if (p >= 0) Z[(size_t)p * N + (nb0 + g) * 128 + wave * 32 + (lane & 31)] = __builtin_nanf("");
+            }
+    }
 }
 
 // The down epilogue and slot combine of a prompt pass. Block (row r, 2048 columns): a thread holds 8 consecutive

@@ -74,6 +74,7 @@ SIGNATURES = {
     "ea_init": (I32, [I32]),
     "ea_fini": (I32, []),
     "ea_device_status": (I32, [C.POINTER(I32)]),
+    "ea_device_status_address": (I32, [C.POINTER(C.c_void_p)]),
     "ea_dequant": (I32, [P, P, P, U32, U32, U32, U32]),
     "ea_exl3_unpack": (I32, [P, P, P, U32, U32, U32, U32, I64, I64]),
     "ea_experts_group": (I32, [P, P, P, P, P, U32, U32, U32, U32]),

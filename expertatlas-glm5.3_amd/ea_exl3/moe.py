@@ -98,3 +98,4 @@ def ffn_decode(stream: int, x: int, x_stride: int, logits: int, bias: int, scale
     check(lib().ea_ffn_moe_decode(stream, x, x_dtype, x_stride, logits, bias, scale, pick, wts, C.byref(ex.c),
                                   C.addressof(arr) if arr is not None else None,
                                   C.byref(s.c), out, R), "ffn_decode")
+

@@ -56,9 +56,15 @@ const char* ea_strerror(int status);
  * prompt_experts.zig:72). Idempotent per device. */
 int ea_init(int device);
 int ea_fini(void);
-/* Device-side status word: kernels record an expert width they have no decoder for here instead of trapping
- * (experts_grouped.cuh:265-287 traps). Reads and clears it; synchronous (tests and health checks only). */
+/* Device-side status word: kernels record an expert width they have no decoder for, or a bounded in-kernel wait that
+ * gave up, here instead of trapping (experts_grouped.cuh:265-287 traps); the affected sums are stored as NaN, so the
+ * call's output carries the failure too. Reads and clears it; synchronous (tests and health checks only). */
 int ea_device_status(int* code);
+/* The device address of the current device's status word (one int32, 0 = no error; the first error's ea_status code
+ * otherwise), for a host that checks it without a synchronizing call: copy it asynchronously on its own stream (or
+ * inside its own graph) after a window's launches and read the copy later. Clearing it is the caller's (a 4-byte
+ * write of 0). No counterpart in the reference, whose kernels trap. */
+int ea_device_status_address(void** addr);
 
 /* ---- trellis decode --------------------------------------------------------------------------------------- */
 
@@ -160,7 +166,10 @@ int ea_prompt_scratch_init(ea_stream_t stream, ea_prompt_scratch* s, void* base,
                            uint32_t rows, uint32_t slots, int planes);
 
 /* out [R, D] fp32 (fp16 with half_sums) = sum over slots of wts * expert(x), rounded through bf16 when do_round.
- * Replaces prompt_experts.run (prompt_experts.zig:146-248). */
+ * Replaces prompt_experts.run (prompt_experts.zig:146-248). The two item lists run side by side: the call forks one
+ * per-device side stream off `stream` with events and joins it back before returning, so the call stays capturable;
+ * calls on one device therefore must not run or be captured concurrently from several host threads (the side stream
+ * and its events are shared; a mutex orders the forks, not the streams' work). */
 int ea_prompt_experts_run(ea_stream_t stream, const void* x, int x_dtype, uint32_t xstride, const int32_t* pick,
                           const float* wts, const ea_routed* ex, const ea_prompt_scratch* s, void* out, uint32_t R,
                           int do_round, int half_sums);

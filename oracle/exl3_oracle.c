@@ -604,25 +604,37 @@ void or_exl3_linear(const uint16_t* xh, const uint32_t* T, int64_t stride_k, int
 /* router top-8: native_ops.cu:998-1068                                                             */
 /* ------------------------------------------------------------------------------------------------ */
 
-/* score = sigmoid(logit) = 1 / (1 + exp(-logit)); choice = score + bias; eight rounds of arg-max (the larger
- * first, the lower id on a tie); wts = score / (sum of the picks' scores in pick order + 1e-20) * scale. */
+/* The top-8's ranking key of a choice: order-preserving over numbers (+0 and -0 share one), NaN just above 0, the key
+ * of a taken expert. So a NaN choice ranks below every number, -inf included, and NaNs among themselves by id; a
+ * taken expert is never picked again. (The reference compares floats in a lane-order butterfly, where a NaN's fate
+ * depends on its lane: native_ops.cu:1021-1027; this build fixes one rule for its two top-8 paths.) */
+static uint32_t or_order_key(float f) {
+    if (f != f) return 1u;
+    const float g = f + 0.0f;
+    uint32_t b;
+    memcpy(&b, &g, 4);
+    return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+
+/* native_ops.cu:1015-1068: choice = sigmoid(l) + bias; 8 rounds of the largest key, the lower id on a tie;
+ * wts = sigmoid / (sum of the picks' sigmoids in pick order + 1e-20) * scale. */
 void or_topk8(const float* logits, const float* bias, int rows, int E, float scale, int* pick, float* wts) {
     float* score = (float*)malloc(sizeof(float) * (size_t)E);
-    float* choice = (float*)malloc(sizeof(float) * (size_t)E);
+    uint32_t* key = (uint32_t*)malloc(sizeof(uint32_t) * (size_t)E);
     for (int r = 0; r < rows; ++r) {
         for (int e = 0; e < E; ++e) {
             score[e] = 1.0f / (or_expf(0.0f - logits[(size_t)r * E + e]) + 1.0f);
-            choice[e] = score[e] + bias[e];
+            key[e] = or_order_key(score[e] + bias[e]);
         }
         float sw[8];
         int sp[8];
         for (int k = 0; k < 8; ++k) {
             int bi = 0;
             for (int e = 1; e < E; ++e)
-                if (choice[e] > choice[bi]) bi = e;
+                if (key[e] > key[bi]) bi = e;
             sp[k] = bi;
             sw[k] = score[bi];
-            choice[bi] = -INFINITY;
+            key[bi] = 0u;
         }
         float total = 0.f;
         for (int k = 0; k < 8; ++k) total = total + sw[k];
@@ -632,7 +644,7 @@ void or_topk8(const float* logits, const float* bias, int rows, int E, float sca
         }
     }
     free(score);
-    free(choice);
+    free(key);
 }
 
 /* native_ops.cu:429-441: out = bf16(bf16(silu(g)) * u), silu(g) = g / (exp(-g) + 1). */

@@ -183,3 +183,72 @@ def test_moe_routed_one_row_given_picks(ea, repeat, mixed):
     got = device.download(out)
     assert device.device_status() == 0
     assert_close_rms(got, want, 2e-3, f"moe.routed R=1 repeat={repeat} mixed={mixed}")
+
+
+def test_topk8_nan_policy_both_paths(ea):
+    """One NaN rule for both top-8 paths (ea_topk8 and the decode layer's per-block top-8), the oracle's: a NaN choice
+    ranks below every number (-inf included), NaNs among themselves by the lower id. Rows where fewer than eight
+    choices are numbers pick NaN experts (their wts are then NaN, as the sum is)."""
+    device, linear, moe, synth = ea
+    from ea_exl3 import ops
+
+    R, E, D, I = 5, 256, 2048, 128
+    logits, bias = synth.logits(900, R)
+    bias[17] = -np.inf
+    logits[1, [7, 100, 200]] = np.nan
+    logits[2, :] = np.nan
+    logits[2, [9, 40, 41, 250, 3, 17]] = [0.5, -1.0, 2.0, 0.0, -np.inf, 1.0]
+    logits[3, :] = np.nan
+    pick_w, wts_w = orc.topk8(logits, bias)
+    dl, db = device.upload(logits), device.upload(bias)
+    dp, dw = device.zeros((R, 8), torch.int32), device.zeros((R, 8), torch.float32)
+    ops.topk(device.stream(), dl.data_ptr(), db.data_ptr(), dp.data_ptr(), dw.data_ptr(), R, 2.5)
+    np.testing.assert_array_equal(device.download(dp), pick_w)
+    np.testing.assert_array_equal(device.download(dw), wts_w)
+    host = synth.HostLayer(901, experts=E, dims=D, width=I, k2=8, only=np.unique(pick_w))
+    ex = moe.Routed(host)
+    for rows in (R, 1):  # the multi-row route launch, and the one-row per-block routing (row 2 alone)
+        lg = logits if rows == R else logits[2:3]
+        sc = moe.Scratch(ex, rows, 8)
+        x = synth.activations(902, rows, D, "f16")
+        _, pick, wts = _run(ea, host, None, sc, ex, x, lg, bias, rows, 0)
+        np.testing.assert_array_equal(pick, pick_w if rows == R else pick_w[2:3])
+        np.testing.assert_array_equal(wts, wts_w if rows == R else wts_w[2:3])
+
+
+def test_unsupported_width_poisons_output(ea):
+    """A width table entry the decode layer has no decoder for (an expert at K2 12 in a layer whose host tables claim
+    widths 8..8): the kernels record EA_UNSUPPORTED_WIDTH (19) in the status word, which ea_device_status_address
+    exposes for asynchronous checks, and store NaN in place of that expert's sums, so the row's output is NaN. The
+    condition is set from the host; every load stays inside the expert's real trellis and every kernel exits."""
+    import ctypes as C
+
+    device, linear, moe, synth = ea
+    from ea_exl3._lib import lib
+
+    R, E, D, I = 1, 64, 1024, 256
+    pick = synth.picks_uniform(950, R, E, 8)
+    wts = synth.routing_weights(951, R, 8)
+    k2 = np.full(E, 8, np.int32)
+    k2[pick[0, 2]] = 12
+    host = synth.HostLayer(952, experts=E, dims=D, width=I, k2=k2, only=np.unique(pick))
+    ex = moe.Routed(host)
+    ex.k2_gu, ex.k2_d = (8, 8), (8, 8)  # what the host claims: the decode layer's path
+    ex.c = ex.struct()
+    sc = moe.Scratch(ex, 1, 8)
+    assert sc.c.fused != 0
+    x = synth.activations(953, R, D, "f16")
+    dx, dp, dw = device.upload(x), device.upload(pick), device.upload(wts)
+    out = device.zeros((R, D), torch.float32)
+    assert device.device_status() == 0
+    moe.routed(device.stream(), dx.data_ptr(), D, dp.data_ptr(), dw.data_ptr(), ex, sc, out.data_ptr(), R, x_dtype=0)
+    torch.cuda.synchronize()
+    addr = C.c_void_p(0)
+    assert lib().ea_device_status_address(C.byref(addr)) == 0 and addr.value
+    word = C.c_int32(0)
+    hip = C.CDLL("libamdhip64.so")
+    assert hip.hipMemcpy(C.byref(word), addr, C.c_size_t(4), 2) == 0  # hipMemcpyDeviceToHost
+    assert word.value == 19
+    assert np.isnan(device.download(out)).all()
+    assert device.device_status() == 19  # read and cleared
+    assert device.device_status() == 0

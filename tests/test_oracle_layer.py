@@ -96,16 +96,23 @@ def test_route_items_cover_every_pair(R):
 
 
 def test_topk_brute_force_and_ties():
+    """The top-8 against a sort: the larger choice first, the lower id on a tie, a NaN choice below every number
+    (-inf included) and NaNs among themselves by id."""
     logits, bias = synth.logits(3, 40)
     logits[0, :] = 0.0
     bias[:] = np.round(bias, 1)  # many exact ties in choice
     logits[1, 5] = logits[1, 9] = 3.0
+    logits[2, [7, 100, 200]] = np.nan  # NaN choices that are never reached
+    bias[17] = -np.inf  # a choice of -inf wherever expert 17's logit is a number
+    logits[3, :] = np.nan  # six numbers (one choice -inf), so two NaN picks follow them
+    logits[3, [9, 40, 41, 250, 3, 17]] = [0.5, -1.0, 2.0, 0.0, -np.inf, 1.0]
+    logits[4, :] = np.nan  # NaN everywhere: ids 0..7
     pick, wts = orc.topk8(logits, bias)
     for r in range(logits.shape[0]):
         score = np.array([np.float32(1) / (np.float32(orc.expf(-float(l))) + np.float32(1)) for l in logits[r]],
                          np.float32)
         choice = (score + bias).astype(np.float32)
-        order = sorted(range(256), key=lambda e: (-float(choice[e]), e))[:8]
+        order = sorted(range(256), key=lambda e: (1, 0.0, e) if np.isnan(choice[e]) else (0, -float(choice[e]), e))[:8]
         assert list(pick[r]) == order
         total = np.float32(0)
         for e in order:
