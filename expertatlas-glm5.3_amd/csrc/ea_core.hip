@@ -178,6 +178,8 @@ int ea_init(int device) {
     if (r) return r;
     r = hip_status(hipEventCreateWithFlags(&c.join, hipEventDisableTiming));
     if (r) return r;
+    r = dl_static_setup(c);
+    if (r) return r;
     r = hip_status(hipDeviceSynchronize());
     if (r) return r;
     c.ready = true;
@@ -196,6 +198,7 @@ int ea_fini(void) {
             if (c.join) (void)hipEventDestroy(c.join);
             c.side = nullptr;
             c.fork = c.join = nullptr;
+            c.static_scratch = nullptr;  // the array itself lives until the process ends
             c.ready = false;
         }
     return EA_OK;

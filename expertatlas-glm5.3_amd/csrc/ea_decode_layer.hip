@@ -1198,11 +1198,60 @@ int decode_layer(hipStream_t s, const void* x, int x_dtype, uint32_t x_stride, c
     return EA_UNPORTED_GROUPED_VARIANT;
 }
 
+// ---- the allocation-free variant's scratch --------------------------------------------------------------------------
+
+// The scratch of ea_ffn_moe_decode_static: the per-pair down outputs and the decode layer's region, carved for
+// DL_MAXR rows of the call's layer shape. The largest shape the decode layer takes (D 6144, I 256) needs 10.7 MB.
+// Every call on a device shares that device's copy, which holds the last call's contents: the layer writes every
+// value it reads back within a call, so nothing in it needs to start at zero.
+constexpr size_t DL_STATIC_BYTES = (size_t)12 << 20;
+static __device__ __align__(256) uint8_t scratch[DL_STATIC_BYTES];
+
+// The byte offsets of the per-pair outputs and the region in the static scratch for a layer shape; false when the
+// layout does not fit.
+static bool dl_static_carve(uint32_t D, uint32_t I, uint32_t E, size_t& y_off, size_t& region_off) {
+    if (!dl_shape_ok(DL_MAXR, DL_SLOTS, D, I, E)) return false;
+    y_off = 0;
+    region_off = align256((size_t)DL_MAXP * D * 4);
+    return region_off + dl_carve(DL_MAXR, D, I, E).total <= DL_STATIC_BYTES;
+}
+
+int dl_static_setup(DevCtx& c) {
+    void* p = nullptr;
+    int r = hip_status(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    if (r) return r;
+    if (!p) return EA_HIP_FAILED;
+    r = hip_status(hipMemset(p, 0, DL_STATIC_BYTES));
+    if (r) return r;
+    c.static_scratch = p;
+    return EA_OK;
+}
+
 }  // namespace ea
 
 using namespace ea;
 
 extern "C" {
+
+int ea_ffn_moe_decode_static(ea_stream_t stream, const void* x, int x_dtype, uint32_t x_stride, const float* logits,
+                             const float* bias, float scale, int32_t* pick, float* wts, const ea_routed* ex,
+                             const ea_linear* const* shared, float* out, uint32_t R) {
+    EA_REQUIRE_CTX(c);
+    if (!x || !logits || !bias || !pick || !wts || !ex || !out) return EA_BAD_ARGUMENT;
+    if (!c->static_scratch) return EA_NOT_INITIALIZED;
+    if (R > (uint32_t)DL_MAXR) return EA_SCRATCH_TOO_SMALL;
+    size_t y_off = 0, region_off = 0;
+    if (!dl_static_carve(ex->dims, ex->width, ex->count, y_off, region_off)) return EA_SCRATCH_TOO_SMALL;
+    if (R == 0) return EA_OK;
+    const uint64_t base = reinterpret_cast<uintptr_t>(c->static_scratch);
+    ea_moe_scratch sc{};
+    sc.y = base + y_off;
+    sc.fused = base + region_off;
+    sc.rows = DL_MAXR;
+    sc.slots = DL_SLOTS;
+    return decode_layer(as_stream(stream), x, x_dtype, x_stride, logits, bias, scale, pick, wts, ex, shared, &sc, out,
+                        R);
+}
 
 int ea_profile_enable(int on) {
     EA_REQUIRE_CTX(c);

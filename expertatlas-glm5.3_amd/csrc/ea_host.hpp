@@ -20,7 +20,14 @@ struct DevCtx {
     // one call: fork (side waits for the caller's work so far), join (the caller waits for the side's launches).
     hipStream_t side = nullptr;
     hipEvent_t fork = nullptr, join = nullptr;
+    // This device's copy of the decode layer's file-scope scratch array (ea_ffn_moe_decode_static), from
+    // hipGetSymbolAddress at ea_init; the array's name is not a device address in host code.
+    void* static_scratch = nullptr;
 };
+
+// ea_init's set-up of the decode layer's file-scope scratch on the current device (ea_decode_layer.hip): resolves and
+// clears this device's copy of the array into c.static_scratch.
+int dl_static_setup(DevCtx& c);
 
 // Run `side_work(side stream)` beside `main_work(s)`: both start after everything already on s, and s waits for
 // both before anything later. Serialised per device (the side stream and events are shared).

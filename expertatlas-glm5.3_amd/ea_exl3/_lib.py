@@ -103,6 +103,7 @@ SIGNATURES = {
     "ea_profile_enable": (I32, [I32]),
     "ea_profile_stages": (I32, [P, U32]),
     "ea_ffn_moe_decode": (I32, [P, P, I32, U32, P, P, F32, P, P, C.POINTER(Routed), P, C.POINTER(MoeScratch), P, U32]),
+    "ea_ffn_moe_decode_static": (I32, [P, P, I32, U32, P, P, F32, P, P, C.POINTER(Routed), P, P, U32]),
 }
 
 _lib = None

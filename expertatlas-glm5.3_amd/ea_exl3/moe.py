@@ -99,3 +99,15 @@ def ffn_decode(stream: int, x: int, x_stride: int, logits: int, bias: int, scale
                                   C.addressof(arr) if arr is not None else None,
                                   C.byref(s.c), out, R), "ffn_decode")
 
+
+def ffn_decode_static(stream: int, x: int, x_stride: int, logits: int, bias: int, scale: float, pick: int, wts: int,
+                      ex: Routed, shared, out: int, R: int, x_dtype: int = 1) -> None:
+    """ffn_decode with no scratch argument (ea_ffn_moe_decode_static): the library's per-device scratch array, for
+    callers that cannot allocate; R <= 16; calls overlapping on one device race."""
+    arr = None
+    if shared is not None:
+        from ._lib import Linear as _Linear
+
+        arr = (C.POINTER(_Linear) * 3)(*[C.pointer(l) for l in shared])
+    check(lib().ea_ffn_moe_decode_static(stream, x, x_dtype, x_stride, logits, bias, scale, pick, wts, C.byref(ex.c),
+                                         C.addressof(arr) if arr is not None else None, out, R), "ffn_decode_static")

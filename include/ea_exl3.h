@@ -247,6 +247,18 @@ int ea_ffn_moe_decode(ea_stream_t stream, const void* x, int x_dtype, uint32_t x
                       const float* bias, float scale, int32_t* pick, float* wts, const ea_routed* ex,
                       const ea_linear* const* shared, const ea_moe_scratch* s, float* out, uint32_t R);
 
+/* ea_ffn_moe_decode without a scratch argument: it allocates nothing and takes no workspace. No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc). The scratch is a file-scope device array of 12 MiB that the library holds on each
+ * device it runs on until the process ends (resolved and cleared by ea_init), carved for 16 rows of the call's layer
+ * shape. R above 16, or a layer shape whose carve exceeds the array, returns EA_SCRATCH_TOO_SMALL before any launch;
+ * shapes the decode layer does not take return EA_UNPORTED_GROUPED_VARIANT (there is no sequence fallback). Every call
+ * on a device shares that device's array: calls that overlap in time on one device (several streams, or concurrent
+ * host threads) race and must not be issued. */
+int ea_ffn_moe_decode_static(ea_stream_t stream, const void* x, int x_dtype, uint32_t x_stride, const float* logits,
+                             const float* bias, float scale, int32_t* pick, float* wts, const ea_routed* ex,
+                             const ea_linear* const* shared, float* out, uint32_t R);
+
 /* ---- benchmark instrumentation (no counterpart in the reference) ------------------------------------------- */
 
 /* With on != 0, every call that runs the decode layer (ea_ffn_moe_decode, and ea_moe_routed when it takes that
