@@ -37,9 +37,12 @@ constexpr int DL_RS = 264;                   // LDS row stride of the staged act
 constexpr int DL_MAXKC = 24;                 // k chunks of 256 (D up to 6144)
 constexpr int DL_MAXK2 = STAGE_MAXK2;        // widest trellis (K2) the decode layer runs
 constexpr int DL_STAGE_WORDS = DL_KT * 2 * 4 * DL_MAXK2;  // a wave's staged trellis words: 16 rows of 2 tiles
+constexpr int L1_LINE = 32;                  // ints between two of the one-row launch's counters (a 128-byte line)
+constexpr size_t L1_SYNC_BYTES = 16384;      // the one-row launch's counters
 
 // Scratch of the layer's launches, carved on the host for the scratch's row capacity (any R up to it runs).
 struct DLLayout {
+    int* sync;          // the one-row launch's counters (first in the region; zero between launches)
     float* zp;          // [Q, NH, 2, KC, 128] gate|up partial sums, Q = pairs + rows (the shared expert's rows last)
     uint16_t* xd;       // [Q, I] down inputs
     float* sy;          // [rows, D] the shared expert's output
@@ -1001,13 +1004,376 @@ __global__ void __launch_bounds__(DL_THREADS) combine_kernel(DLArgs a) {
     *reinterpret_cast<float2*>(a.out + (size_t)r * a.D + n) = float2{a0, a1};
 }
 
+// ---- the one-row layer in one launch ---------------------------------------------------------------------------------
+// One row routed from logits runs as a single launch of DL_THREADS-thread blocks, one item a block, in two index
+// ranges:
+//   [0, U GU): gate|up items (unit, column block nh, matrix, k chunk of 256), the shared expert's (unit 0) first;
+//   [U GU, U GU + U DB): down items (unit, output column block of 128).
+// A gate|up block routes the row up to its unit's pick (the shared expert's items need no routing), stages its 16 k
+// tiles x 2 column tiles a wave of trellis in LDS, rotates the row's activations of its chunk, multiplies on MFMA and
+// stores its partial sums. The block that completes a (unit, nh) -- the last of its 2 KC items to count in -- sums the
+// chunks in order and runs the SwiGLU epilogue of that column block into the unit's down inputs, then counts the
+// column block ready. A down block routes the row, stages its unit's down trellis of its column block and waits until
+// both column blocks of its unit are ready; it multiplies, rotates and stores the unit's output of the column block.
+// The last of the U down blocks of a column block to count in combines it: the slots in order from 0, then the shared
+// expert.
+// Hand-offs need no fence: data handed on is written with agent-scope stores (coherent across the XCDs' L2s), each wave
+// waits for its stores (vmcnt 0), the block meets at a barrier, and only then one thread counts in; readers load with
+// agent-scope loads issued after they have seen the count. A down block waits only for items of lower block index,
+// which the hardware dispatched before it and which never wait, so every wait ends; it is bounded anyway (a give-up is
+// recorded as EA_SYNC_TIMEOUT and the block's output is NaN). Every counter is back at zero when the launch ends: a
+// counter's last arrival resets it, and the last down block of a unit resets the unit's ready count.
+
+constexpr int L1_UNITS = 1 + DL_SLOTS;  // the shared expert and the eight picks
+constexpr int L1_MAXDB = 256 * DL_MAXKC / 128;  // output column blocks at the largest D
+
+// The counters, one 128-byte line each: gate|up items done per (unit, nh); column blocks ready per unit; down items
+// done per unit; units done per output column block.
+__device__ __forceinline__ int* l1_gcnt(int* s, int u, int nh) { return s + (u * 2 + nh) * L1_LINE; }
+__device__ __forceinline__ int* l1_urdy(int* s, int u) { return s + (2 * L1_UNITS + u) * L1_LINE; }
+__device__ __forceinline__ int* l1_dcnt(int* s, int u) { return s + (3 * L1_UNITS + u) * L1_LINE; }
+__device__ __forceinline__ int* l1_ccnt(int* s, int cb) { return s + (4 * L1_UNITS + cb) * L1_LINE; }
+static_assert((4 * L1_UNITS + L1_MAXDB) * L1_LINE * 4 <= (int)L1_SYNC_BYTES, "the counters fit their region");
+
+// Agent-scope (coherent across the XCDs) stores and loads of handed-on data, and counting in.
+__device__ __forceinline__ void st_coh(float* p, float v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+__device__ __forceinline__ void st_coh(uint32_t* p, uint32_t v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_coh2(float* p, float2 v) {
+    __hip_atomic_store(reinterpret_cast<uint64_t*>(p), __builtin_bit_cast(uint64_t, v), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint32_t ld_coh(const uint32_t* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float2 ld_coh2(const float* p) {
+    return __builtin_bit_cast(float2, __hip_atomic_load(reinterpret_cast<const uint64_t*>(p), __ATOMIC_RELAXED,
+                                                        __HIP_MEMORY_SCOPE_AGENT));
+}
+__device__ __forceinline__ int ld_coh(const int* p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+__device__ __forceinline__ int count_in(int* c) { return __hip_atomic_fetch_add(c, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+__device__ __forceinline__ void reset_count(int* c) { __hip_atomic_store(c, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+// Every store this wave issued has completed (and, being agent-scope, is visible to every block).
+__device__ __forceinline__ void stores_done() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+struct L1Sh {
+    int pick[DL_SLOTS];
+    float wts[DL_SLOTS];
+    uint64_t tp;  // the block's unit: the trellis address and width of the block's matrix, its expert
+    int tk, e;
+    int flag;
+    __attribute__((aligned(16))) uint16_t xs[DL_RS];  // the row: its rotated activations, or the unit's down inputs
+    union {
+        struct {
+            uint64_t tptr[256];
+            int tk2[256];
+        } r;  // every expert's table of the block's matrix, loaded with the logits
+        __attribute__((aligned(16))) uint32_t stage[DL_WAVES][DL_STAGE_WORDS];
+        float gus[2][128];
+        float ys[128];
+    };
+};
+
+// The row's picks up to `need` (need = 8: all of them and their weights) and the tables of matrix `mat` of every
+// expert, a thread an expert (E = 256); then the block's unit u's entry (u >= 1: routed unit u - 1, pick u - 1).
+__device__ __forceinline__ void l1_route(const DLArgs& a, L1Sh& sh, int mat, int u, int need) {
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const uint64_t tp = (uint64_t)a.ptr[mat][t];
+    const int tk = a.k2t[mat][t];
+    if (wave == (int)(blockIdx.x % DL_WAVES)) topk8_wave(a.logits, a.bias, a.scale, sh.pick, sh.wts, lane, need);
+    sh.r.tptr[t] = tp;
+    sh.r.tk2[t] = tk;
+    __syncthreads();
+    if (t == 0) {
+        const int e = sh.pick[u - 1];
+        sh.e = e;
+        sh.tp = sh.r.tptr[e];
+        sh.tk = sh.r.tk2[e];
+    }
+    __syncthreads();
+}
+
+// The row's product over NKT k tiles with the wave's two column tiles staged in st: acc[j] (row 0 in lanes 0..15,
+// element 0) += xs (A rows 1..15 zero) x the tiles.
+template <int CB, int K2, int NKT>
+__device__ __forceinline__ void l1_mfma(const uint32_t* st, const LaneQuad& lq, const uint16_t* xs, int lane,
+                                        f4v (&acc)[2]) {
+    constexpr int TW = 4 * K2;
+    const uint32_t* wa = st + lq.w0;
+    const uint32_t* wb = st + lq.w1;
+    const bool row0 = (lane & 15) == 0;
+    const uint16_t* xr = xs + 2 * ((lane >> 4) & 3);
+#pragma unroll
+    for (int t = 0; t < NKT; t += 2) {
+        const uint16_t* xk = xr + t * 16;
+        u4v au = {*reinterpret_cast<const uint32_t*>(xk), *reinterpret_cast<const uint32_t*>(xk + 8),
+                  *reinterpret_cast<const uint32_t*>(xk + 16), *reinterpret_cast<const uint32_t*>(xk + 24)};
+        if (!row0) au = u4v{0u, 0u, 0u, 0u};
+        const h8v a = __builtin_bit_cast(h8v, au);
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int t0 = (2 * t + j) * TW, t1 = (2 * (t + 1) + j) * TW;
+            const u2v b0 = decode_quad<K2, CB>(wa[t0], wb[t0], lq.sh);
+            const u2v b1 = decode_quad<K2, CB>(wa[t1], wb[t1], lq.sh);
+            const h8v bb = __builtin_bit_cast(h8v, (u4v{b0.x, b0.y, b1.x, b1.y}));
+            acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bb, acc[j], 0, 0, 0);
+        }
+    }
+}
+template <int CB, int NKT>
+__device__ __forceinline__ bool l1_mfma_k2(int k2, const uint32_t* st, const LaneQuad& lq, const uint16_t* xs,
+                                           int lane, f4v (&acc)[2]) {
+    return EA_K2_SWITCH(k2, 2, 10, (l1_mfma<CB, K2V, NKT>(st, lq, xs, lane, acc)));
+}
+
+// Gate|up item (unit u, column block nh, matrix mat, chunk c) of the row. q: the unit's member (the pick's slot, or P
+// for the shared expert).
+template <int CB, bool SHARED>
+__device__ __forceinline__ void l1_gateup(const DLArgs& a, L1Sh& sh, int u, int nh, int mat, int c, int q) {
+    const int lane = opaque_lane(threadIdx.x & 63), wave = uniform((int)threadIdx.x >> 6);
+    const int KC = a.D / 256, NH = a.I / 128, ns = a.I / 16;
+    const int nt0 = nh * 8 + 2 * wave, kt0 = c * DL_KT;
+    TileSpan sp;
+    int k2;
+    const uint16_t* suh;
+    if constexpr (SHARED) {
+        k2 = a.sh_k2;
+        const int TWB = 16 * k2;
+        sp.r = buffer_rsrc(mat ? a.sh_w[1] : a.sh_w[0], (uint32_t)((a.D / 16) * ns * TWB));
+        sp.off = ((nt0 >> 3) * (a.D / 16) * 8 + kt0 * 8 + (nt0 & 7)) * TWB;
+        sp.kstride = 8 * TWB;
+        suh = mat ? a.sh_suh[1] : a.sh_suh[0];
+    } else {
+        k2 = uniform(sh.tk);
+        const int TWB = 16 * k2;
+        sp.r = buffer_rsrc(uniform(reinterpret_cast<const uint32_t*>(sh.tp)), (uint32_t)((a.D / 16) * ns * TWB));
+        sp.off = (kt0 * ns + nt0) * TWB;
+        sp.kstride = ns * TWB;
+        suh = (mat ? a.suh_u : a.suh_g) + (size_t)uniform(sh.e) * a.D;
+    }
+    const LaneQuad lq = lane_quad(k2, lane);
+    // the row's activations and suh of chunk c (waves 0 and 1 rotate a 128-block each; the others load the same
+    // addresses), then the trellis
+    const int blk = wave & 1;
+    const int k = c * 256 + blk * 128 + 2 * lane;
+    const uint32_t xv = *reinterpret_cast<const uint32_t*>(static_cast<const uint16_t*>(a.x) + k);
+    const uint32_t sv = *reinterpret_cast<const uint32_t*>(suh + k);
+    u4v v[stage_loads<DL_KT>()];
+    stage_issue<DL_KT>(sp, k2, lane, v);
+    issued();
+    uint32_t xh = xv, sh2 = sv;
+    hold(xh);
+    hold(sh2);
+    if (wave < 2) {
+        const bool bf = a.x_dtype == BF16;
+        const uint16_t xl = (uint16_t)(xh & 0xffffu), xu = (uint16_t)(xh >> 16);
+        float v0 = (bf ? bf2f(xl) : h2f(xl)) * h2f((uint16_t)(sh2 & 0xffffu));
+        float v1 = (bf ? bf2f(xu) : h2f(xu)) * h2f((uint16_t)(sh2 >> 16));
+        fwht128_w64(v0, v1, lane);
+        *reinterpret_cast<uint32_t*>(sh.xs + blk * 128 + 2 * lane) =
+            (uint32_t)f2h(v0 * HAD_SCALE) | ((uint32_t)f2h(v1 * HAD_SCALE) << 16);
+    }
+    __syncthreads();
+    uint32_t* st = sh.stage[wave];
+    stage_store<DL_KT>(st, k2, lane, v);
+    f4v acc[2] = {f4v{0.f, 0.f, 0.f, 0.f}, f4v{0.f, 0.f, 0.f, 0.f}};
+    const bool ok = l1_mfma_k2<CB, DL_KT>(k2, st, lq, sh.xs, lane, acc);
+    if (!ok) {
+        if (lane == 0) record_error(a.status, DEV_UNSUPPORTED_WIDTH);
+        acc[0] = acc[1] = nan4();
+    }
+    // row 0's partial sums of this chunk: zp[q][nh][mat][c][128]
+    if (lane < 16) {
+        float* z = a.lay.zp + ((((size_t)q * NH + nh) * 2 + mat) * KC + c) * 128;
+#pragma unroll
+        for (int j = 0; j < 2; ++j) st_coh(z + (2 * wave + j) * 16 + lane, acc[j][0]);
+    }
+}
+
+// The SwiGLU epilogue of (unit, column block nh) of the row's member q, after every chunk's partial sums are in:
+// waves 0 and 1 sum the gate's and the up's chunks in order and rotate them (gu_out), wave 0 forms the down inputs.
+__device__ __forceinline__ void l1_epilogue(const DLArgs& a, L1Sh& sh, const UnitView& uv, int nh, int q) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int KC = a.D / 256, NH = a.I / 128;
+    uint32_t sd = 0;
+    if (wave < 2) {
+        const uint32_t sv = svh_pair(a, uv, nh, wave, lane);
+        sd = suhd_pair(a, uv, nh, lane);
+        const float* z = a.lay.zp + (((size_t)q * NH + nh) * 2 + wave) * KC * 128 + 2 * lane;
+        float2 zv[DL_MAXKC];
+#pragma unroll
+        for (int cc = 0; cc < DL_MAXKC; ++cc) zv[cc] = ld_coh2(z + (cc < KC ? cc : KC - 1) * 128);
+        const float2 o = gu_out(uv, zp_sum(a, zv), sv, lane);
+        *reinterpret_cast<float2*>(&sh.gus[wave][2 * lane]) = o;
+    }
+    __syncthreads();
+    if (wave == 0) {
+        const float2 g = *reinterpret_cast<const float2*>(&sh.gus[0][2 * lane]);
+        const float2 u = *reinterpret_cast<const float2*>(&sh.gus[1][2 * lane]);
+        st_coh(reinterpret_cast<uint32_t*>(a.lay.xd + (size_t)q * a.I + nh * 128 + 2 * lane),
+               act_pair(uv, g, u, sd, lane));
+    }
+}
+
+// Down item (unit u, output column block cb) of the row's member q: its output columns of the unit (y or sy), then
+// whether this block combines the column block.
+template <int CB, int SCB, int NKT>
+__device__ __forceinline__ void l1_down(const DLArgs& a, L1Sh& sh, const UnitView& uv, int u, int cb, int q) {
+    const int lane = opaque_lane(threadIdx.x & 63), wave = uniform((int)threadIdx.x >> 6);
+    const int NH = a.I / 128, DB = a.D / 128, KT = a.I / 16, ns = a.D / 16;
+    const int nt0 = cb * 8 + 2 * wave;
+    const int k2 = uv.shared ? a.sh_k2 : uniform(sh.tk), TWB = 16 * k2;
+    TileSpan sp;
+    if (uv.shared) {
+        sp.r = buffer_rsrc(a.sh_w[2], (uint32_t)(KT * ns * TWB));
+        sp.off = ((nt0 >> 3) * KT * 8 + (nt0 & 7)) * TWB;
+        sp.kstride = 8 * TWB;
+    } else {
+        sp.r = buffer_rsrc(uniform(reinterpret_cast<const uint32_t*>(sh.tp)), (uint32_t)(KT * ns * TWB));
+        sp.off = nt0 * TWB;
+        sp.kstride = ns * TWB;
+    }
+    const LaneQuad lq = lane_quad(k2, lane);
+    const uint16_t* svh = uv.shared ? a.sh_svh[2] : a.svh_d + (size_t)uv.e * a.D;
+    uint32_t sd = *reinterpret_cast<const uint32_t*>(svh + cb * 128 + 2 * lane);
+    u4v v[stage_loads<NKT>()];
+    stage_issue<NKT>(sp, k2, lane, v);
+    issued();
+    hold(sd);
+    // both column blocks of the unit's down inputs ready
+    if (threadIdx.x == 0) {
+        int n = 0;
+        while (ld_coh(l1_urdy(a.lay.sync, u)) < NH) {
+            if (++n > (1 << 18)) {
+                record_error(a.status, DEV_SYNC_TIMEOUT);
+                break;
+            }
+            __builtin_amdgcn_s_sleep(2);
+        }
+        sh.flag = n > (1 << 18);
+    }
+    __syncthreads();
+    const bool timed_out = sh.flag;
+    if (threadIdx.x < a.I / 2)
+        reinterpret_cast<uint32_t*>(sh.xs)[threadIdx.x] =
+            ld_coh(reinterpret_cast<const uint32_t*>(a.lay.xd + (size_t)q * a.I) + threadIdx.x);
+    __syncthreads();
+    uint32_t* st = sh.stage[wave];
+    stage_store<NKT>(st, k2, lane, v);
+    f4v acc[2] = {f4v{0.f, 0.f, 0.f, 0.f}, f4v{0.f, 0.f, 0.f, 0.f}};
+    const bool ok = uv.shared ? l1_mfma_k2<SCB, NKT>(k2, st, lq, sh.xs, lane, acc)
+                              : l1_mfma_k2<CB, NKT>(k2, st, lq, sh.xs, lane, acc);
+    if (!ok || timed_out) {
+        if (lane == 0 && !ok) record_error(a.status, DEV_UNSUPPORTED_WIDTH);
+        acc[0] = acc[1] = nan4();
+    }
+    __syncthreads();  // every wave is done with its staging: the column sums take its place
+    if (lane < 16) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) sh.ys[(2 * wave + j) * 16 + lane] = acc[j][0];
+    }
+    __syncthreads();
+    if (wave == 0) {
+        float v0 = sh.ys[2 * lane], v1 = sh.ys[2 * lane + 1];
+        fwht128_w64(v0, v1, lane);
+        const float s0 = h2f((uint16_t)(sd & 0xffffu)), s1 = h2f((uint16_t)(sd >> 16));
+        float* dst = uv.shared ? a.lay.sy : a.yroute + (size_t)q * a.D;
+        st_coh2(dst + cb * 128 + 2 * lane, float2{v0 * HAD_SCALE * s0, v1 * HAD_SCALE * s1});
+    }
+    stores_done();
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const bool last = count_in(l1_ccnt(a.lay.sync, cb)) == a.U - 1;
+        if (last) reset_count(l1_ccnt(a.lay.sync, cb));
+        if (count_in(l1_dcnt(a.lay.sync, u)) == DB - 1) {  // every down block of the unit is past its wait
+            reset_count(l1_urdy(a.lay.sync, u));
+            reset_count(l1_dcnt(a.lay.sync, u));
+        }
+        sh.flag = last;
+    }
+    __syncthreads();
+    if (sh.flag && wave == 0) {
+        // the combine of the column block: the slots in order from 0 (exl3_experts.cu:256-267), then the shared expert
+        const int n = cb * 128 + 2 * lane;
+        float2 y[DL_SLOTS];
+#pragma unroll
+        for (int k = 0; k < DL_SLOTS; ++k) y[k] = ld_coh2(a.yroute + (size_t)k * a.D + n);
+        float2 sv = a.hs ? ld_coh2(a.lay.sy + n) : float2{0.f, 0.f};
+        float a0 = 0.f, a1 = 0.f;
+#pragma unroll
+        for (int k = 0; k < DL_SLOTS; ++k) {
+            a0 = __builtin_fmaf(sh.wts[k], y[k].x, a0);
+            a1 = __builtin_fmaf(sh.wts[k], y[k].y, a1);
+        }
+        if (a.hs) {
+            a0 = a0 + sv.x;
+            a1 = a1 + sv.y;
+        }
+        *reinterpret_cast<float2*>(a.out + n) = float2{a0, a1};
+    }
+}
+
+template <int CB, int SCB>
+__global__ void __launch_bounds__(DL_THREADS) __attribute__((amdgpu_waves_per_eu(6))) layer1_kernel(DLArgs a) {
+    __shared__ L1Sh sh;
+    const int NH = a.I / 128, KC = a.D / 256, DB = a.D / 128;
+    const int GU = NH * 2 * KC;  // gate|up items a unit
+    const int b = blockIdx.x;
+    UnitView uv;
+    uv.nm = 1;
+    uv.mem = nullptr;
+    if (b < a.U * GU) {
+        const int u = b / GU, rem = b % GU, nh = rem / (2 * KC), mat = (rem / KC) & 1, c = rem % KC;
+        uv.shared = a.hs && u == 0;
+        const int q = uv.shared ? DL_SLOTS : u - a.hs;
+        if (uv.shared) {
+            uv.e = -1;
+            l1_gateup<SCB, true>(a, sh, u, nh, mat, c, q);
+        } else {
+            const bool publisher = b == a.hs * GU;  // hands pick / wts to the caller
+            l1_route(a, sh, mat, u - a.hs + 1, publisher ? DL_SLOTS : u - a.hs + 1);
+            if (publisher && threadIdx.x < DL_SLOTS) {
+                a.pick[threadIdx.x] = sh.pick[threadIdx.x];
+                a.wts[threadIdx.x] = sh.wts[threadIdx.x];
+            }
+            uv.e = uniform(sh.e);
+            l1_gateup<CB, false>(a, sh, u, nh, mat, c, q);
+        }
+        stores_done();
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            const bool last = count_in(l1_gcnt(a.lay.sync, u, nh)) == 2 * KC - 1;
+            if (last) reset_count(l1_gcnt(a.lay.sync, u, nh));
+            sh.flag = last;
+        }
+        __syncthreads();
+        if (!sh.flag) return;
+        l1_epilogue(a, sh, uv, nh, q);
+        stores_done();
+        __syncthreads();
+        if (threadIdx.x == 0) count_in(l1_urdy(a.lay.sync, u));
+        return;
+    }
+    const int d = b - a.U * GU, u = d / DB, cb = d % DB;
+    uv.shared = a.hs && u == 0;
+    const int q = uv.shared ? DL_SLOTS : u - a.hs;
+    // every down block routes the whole row: the last of a column block combines all eight slots with their weights
+    l1_route(a, sh, 2, uv.shared ? 1 : u - a.hs + 1, DL_SLOTS);
+    uv.e = uv.shared ? -1 : uniform(sh.e);
+    if (a.I == 256)
+        l1_down<CB, SCB, 16>(a, sh, uv, u, cb, q);
+    else
+        l1_down<CB, SCB, 8>(a, sh, uv, u, cb, q);
+}
+
 // ---- host side ----------------------------------------------------------------------------------------------------
 
 static size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
 
 // Region offsets for a scratch of `rows` rows (capacity), in bytes from the region's base.
 struct DLCarve {
-    size_t zp, xd, sy, ws, total;
+    size_t sync, zp, xd, sy, ws, total;
     size_t U, NH, DB;
 };
 
@@ -1024,6 +1390,7 @@ static DLCarve dl_carve(uint32_t rows, uint32_t D, uint32_t I, uint32_t E) {
         off += align256(bytes);
         return at;
     };
+    c.sync = take(L1_SYNC_BYTES);
     c.zp = take(Q * c.NH * 2 * KC * 128 * 4);
     c.xd = take(Q * I * 2);
     c.sy = take((size_t)rows * D * 4);
@@ -1045,6 +1412,7 @@ size_t dl_region_bytes(uint32_t rows, uint32_t slots, uint32_t D, uint32_t I, ui
 static DLLayout dl_layout(uint64_t base, uint32_t rows, uint32_t D, uint32_t I, uint32_t E) {
     const DLCarve c = dl_carve(rows, D, I, E);
     DLLayout l;
+    l.sync = dptr<int>(base + c.sync);
     l.zp = dptr<float>(base + c.zp);
     l.xd = dptr<uint16_t>(base + c.xd);
     l.sy = dptr<float>(base + c.sy);
@@ -1094,6 +1462,15 @@ static int dl_launch(hipStream_t s, const DLArgs& a, int cus, int device) {
         per_cu_wide = n;
     }
     const int NH = a.I / 128, KC = a.D / 256, DB = a.D / 128;
+    if (a.R == 1 && a.logits) {
+        // one row routed from logits: the whole layer in one launch (the stage events then all follow it)
+        mark_stage(s, device, 0);
+        layer1_kernel<CB, SCB><<<a.U * NH * 2 * KC + a.U * DB, DL_THREADS, 0, s>>>(a);
+        const int r = launched();
+        if (r) return r;
+        for (int k = 1; k <= DL_STAGES; ++k) mark_stage(s, device, k);
+        return EA_OK;
+    }
     const bool wide = a.R > 1 && NH == 2;  // items over both column blocks
     const int items = a.U * (wide ? 1 : NH) * 2 * KC;
     int grid = (wide ? per_cu_wide : per_cu) * cus;
@@ -1203,7 +1580,8 @@ int decode_layer(hipStream_t s, const void* x, int x_dtype, uint32_t x_stride, c
 // The scratch of ea_ffn_moe_decode_static: the per-pair down outputs and the decode layer's region, carved for
 // DL_MAXR rows of the call's layer shape. The largest shape the decode layer takes (D 6144, I 256) needs 10.7 MB.
 // Every call on a device shares that device's copy, which holds the last call's contents: the layer writes every
-// value it reads back within a call, so nothing in it needs to start at zero.
+// value it reads back within a call, and the one-row launch's counters, which must start at zero, are cleared by
+// ea_init and left at zero by every launch.
 constexpr size_t DL_STATIC_BYTES = (size_t)12 << 20;
 static __device__ __align__(256) uint8_t scratch[DL_STATIC_BYTES];
 
@@ -1211,9 +1589,9 @@ static __device__ __align__(256) uint8_t scratch[DL_STATIC_BYTES];
 // layout does not fit.
 static bool dl_static_carve(uint32_t D, uint32_t I, uint32_t E, size_t& y_off, size_t& region_off) {
     if (!dl_shape_ok(DL_MAXR, DL_SLOTS, D, I, E)) return false;
-    y_off = 0;
-    region_off = align256((size_t)DL_MAXP * D * 4);
-    return region_off + dl_carve(DL_MAXR, D, I, E).total <= DL_STATIC_BYTES;
+    region_off = 0;  // the region first: its counters then sit at the array's start for every layer shape
+    y_off = dl_carve(DL_MAXR, D, I, E).total;
+    return y_off + align256((size_t)DL_MAXP * D * 4) <= DL_STATIC_BYTES;
 }
 
 int dl_static_setup(DevCtx& c) {
