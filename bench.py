@@ -6,19 +6,21 @@
 A step is one pass of the hot path over one batch of synthetic input, with every input already in HBM:
   decode (default): one GLM-5.3 MoE layer of a TP=8 rank at batch 1 -- router top-8 from logits,
       the routed experts (moe.routed), the shared expert (EXL3 linears + SwiGLU) and their sum: ea_ffn_moe_decode,
-      three launches at one row (gate|up, down with the SwiGLU epilogue, combine), five above (route, gate|up,
-      epilogue, down, combine);
-  multi (config 3): the same layer at 16 rows, uniform top-8, 70 % of the experts at 3 bits;
+      one launch at one row, five above (route, gate|up, epilogue, down, combine); the default line also carries
+      the metric's second half, the 512-token prefill chunk (config 4), as the object "prefill512";
+  multi (config 3): the same layer at 16 rows, uniform top-8 (no router bias), 70 % of the experts at 3 bits;
   stack (config 5): 75 resident layers (3-bit for 70 % of the experts), one token through all of them (us / token);
   linear (config 1): one 4-bit EXL3 linear 6144 x 2048 at one row (linear.call);
   prefill512 / prefill2048 (config 4): prompt_experts.run over 512 / 2048 rows with Zipf(1.1) routing.
 The decode configs cycle through several distinct resident layers and draw fresh router logits every layer, so the
-touched experts are not sitting in the 256 MB Infinity Cache. Prints one JSON line.
+touched experts are not sitting in the 256 MB Infinity Cache. Their timed region replays the K steps from a HIP
+graph (as the reference runs decode); the same steps launched one by one are reported beside it. Prints one JSON
+line, with the library's path and hash and the device it ran on.
 
 The dominant kernel's roofline is measured live: HIP events around each of its launches (on the stream the launches
-go to) over a second pass identical to the timed one; its algorithmic bytes per launch are the trellis + scales of
-every distinct expert the launch touches, the shared expert, the activations, logits and outputs. Its HBM traffic
-a launch comes from the committed rocprofv3 counter summary (profiles/gateup_kernel_config2_traffic.md).
+go to) over a further pass identical to the timed one; its algorithmic bytes per launch are the trellis + scales of
+every distinct expert the launch touches, the shared expert, the activations, logits and outputs. Its rocprof kernel
+duration and HBM traffic a launch come from the committed counter summary (profiles/layer1_kernel_config2.md).
 """
 from __future__ import annotations
 
@@ -55,6 +57,7 @@ def parse():
                     help="decode configs: ea_ffn_moe_decode, or the reference's launch sequence (topk, "
                          "moe.routed's six launches, the shared expert's linears, swiglu2, add)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-prefill", action="store_true", help="decode: leave out the 512-token prefill object")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a plain device copy of known size (for HBM counter calibration)")
     ap.add_argument("--seed", type=int, default=1234)
@@ -67,7 +70,8 @@ class DecodeBench:
     """`per_step` layers a step (1, or 75 for the stack), each router top-8 + routed experts + shared expert + sum on
     R rows; layer launch j uses resident layer j mod n_layers."""
 
-    def __init__(self, R: int, n_layers: int, per_step: int, mixed: bool, seed: int, steps_total: int, path: str):
+    def __init__(self, R: int, n_layers: int, per_step: int, mixed: bool, seed: int, steps_total: int, path: str,
+                 uniform: bool = False):
         import numpy as np
         import torch
         from ea_exl3 import device, experts, linear, moe, ops, synth
@@ -85,7 +89,8 @@ class DecodeBench:
         self.x = torch.randn((R, D), device="cuda", generator=gen).to(torch.float16)
         launches = steps_total * per_step
         self.logits = torch.randn((launches, R, E), device="cuda", generator=gen)
-        self.bias = 0.1 * torch.randn(E, device="cuda", generator=gen)
+        # uniform routing (config 3): no bias, so a row's top-8 of i.i.d. logits is a uniformly random 8-subset
+        self.bias = (0.0 if uniform else 0.1) * torch.randn(E, device="cuda", generator=gen)
         self.pick = torch.zeros((launches, R, SLOTS), dtype=torch.int32, device="cuda")
         self.wts = torch.zeros((launches, R, SLOTS), dtype=torch.float32, device="cuda")
         self.out = torch.zeros((R, D), dtype=torch.float32, device="cuda")
@@ -117,13 +122,13 @@ class DecodeBench:
     def layer_of(self, j: int) -> int:
         return j % len(self.layers)
 
-    def launch(self, j: int) -> None:
-        """Layer launch j."""
+    def launch(self, j: int, stream: int | None = None) -> None:
+        """Layer launch j, on the bench's stream or on `stream` (a graph capture's)."""
         if self.path != "fused":
             self.sequence(j)
             return
         l, R = self.layer_of(j), self.R
-        r = self.fn(self.s, self._x, 0, D, self._logits0 + j * R * E * 4, self._bias, ROUTED_SCALE,
+        r = self.fn(stream or self.s, self._x, 0, D, self._logits0 + j * R * E * 4, self._bias, ROUTED_SCALE,
                     self._pick0 + j * R * SLOTS * 4, self._wts0 + j * R * SLOTS * 4, self._ex_ref[l],
                     self._sh_ptr[l], self._sc_ref, self._out, R)
         if r:
@@ -131,9 +136,9 @@ class DecodeBench:
 
             check(r, "ffn_decode")
 
-    def step(self, i: int) -> None:
+    def step(self, i: int, stream: int | None = None) -> None:
         for q in range(self.per_step):
-            self.launch(i * self.per_step + q)
+            self.launch(i * self.per_step + q, stream)
 
     def step_events(self, i: int, ev: list) -> None:
         """Step i again, timing its launches: the fused path's launches from the library's stage events
@@ -233,6 +238,52 @@ def time_steps(fn, steps: int, warmup: int, torch, first: int = 0) -> float:
     e1.record()
     torch.cuda.synchronize()
     return e0.elapsed_time(e1) / steps
+
+
+def time_graph(step, steps: int, warmup: int, torch, first: int = 0) -> float:
+    """Milliseconds a step, the steps replayed from a HIP graph: `warmup` steps captured into one graph and `steps`
+    into another (step(i, stream) issues step i on the capture stream); the warm-up graph is replayed untimed, then
+    the timed graph once between two synchronised events."""
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):  # one eager step off the default stream before the captures, as torch advises
+        step(first, torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    graphs = []
+    for lo, n in ((first, warmup), (first + warmup, steps)):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=side):
+            cs = torch.cuda.current_stream().cuda_stream
+            for i in range(n):
+                step(lo + i, cs)
+        graphs.append(g)
+    torch.cuda.synchronize()
+    graphs[0].replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    graphs[1].replay()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps
+
+
+def library_identity() -> dict:
+    """The HIP library the run loaded: its path relative to the repository (or as given) and a hash of its bytes."""
+    import hashlib
+
+    from ea_exl3._lib import LIB_PATH
+
+    with open(LIB_PATH, "rb") as f:
+        digest = hashlib.sha256(f.read()).hexdigest()[:16]
+    rel = os.path.relpath(LIB_PATH, ROOT)
+    return {"path": rel if not rel.startswith("..") else LIB_PATH, "sha256_16": digest,
+            "override": bool(os.environ.get("EA_EXL3_LIB"))}
+
+
+def device_identity(torch) -> dict:
+    p = torch.cuda.get_device_properties(0)
+    return {"name": p.name, "arch": getattr(p, "gcnArchName", ""), "cus": p.multi_processor_count}
 
 
 def copy_calibration(torch) -> None:
@@ -341,15 +392,14 @@ def _line(args, value, unit, ms, config, roofline, cpu) -> dict:
             "cpu_baseline": cpu}
 
 
-def recorded_traffic() -> int | None:
-    """HBM bytes a launch of the gate|up kernel at config 2 from the committed rocprofv3 --pmc summary
-    (FETCH_SIZE + WRITE_SIZE, each scaled by the counter's reading for a plain copy of known size), or None."""
+def recorded_figure(profile: str, key: str) -> float | None:
+    """A figure from a committed rocprofv3 summary under profiles/: the line `key = value`, or None."""
     try:
-        with open(os.path.join(ROOT, "profiles", "gateup_kernel_config2_traffic.md")) as f:
+        with open(os.path.join(ROOT, "profiles", profile)) as f:
             for line in f:
-                if line.startswith("traffic_bytes_per_launch ="):
-                    return int(line.split("=")[1])
-    except OSError:
+                if line.startswith(key + " ="):
+                    return float(line.split("=")[1])
+    except (OSError, ValueError):
         pass
     return None
 
@@ -358,34 +408,43 @@ def run_decode(args, torch, np) -> dict:
     workload, R, mixed, per_step, unit = WORKLOADS[args.config]
     n_layers = 75 if args.config == "stack" else args.layers
     total = args.warmup + args.steps
-    bench = DecodeBench(R, n_layers, per_step, mixed, args.seed, 2 * total + 2, args.path)
-    # the timed region: K whole steps
-    ms = time_steps(bench.step, args.steps, args.warmup, torch)
+    bench = DecodeBench(R, n_layers, per_step, mixed, args.seed, 3 * total + 2, args.path,
+                        uniform=args.config == "multi")
+    # the timed region: K whole steps replayed from a HIP graph (how the reference runs decode); the same steps
+    # launched one by one from the host are timed beside it
+    graph_ms = time_graph(bench.step, args.steps, args.warmup, torch) if args.path == "fused" else None
+    eager_ms = time_steps(bench.step, args.steps, args.warmup, torch, first=total)
+    ms = graph_ms if graph_ms is not None else eager_ms
     # the same number of steps again, timing each launch of the dominant kernel on the stream it runs on
     ev = []
     for i in range(args.warmup):
-        bench.step(total + i)
+        bench.step(2 * total + i)
     torch.cuda.synchronize()
     from ea_exl3._lib import check, lib
 
     if args.path == "fused":
         check(lib().ea_profile_enable(1), "profile_enable")
     for i in range(args.steps):
-        bench.step_events(total + args.warmup + i, ev)
+        bench.step_events(2 * total + args.warmup + i, ev)
     torch.cuda.synchronize()
     if args.path == "fused":
         check(lib().ea_profile_enable(0), "profile_enable")
     picks = bench.pick.cpu().numpy()
     stages = None
-    if args.path == "fused":
-        durs = [ms[0] for _, ms in ev]
+    one_launch = args.path == "fused" and R == 1
+    if one_launch:
+        # one row routed from logits: the layer is one launch, so the dominant kernel is the whole layer
+        durs = [ms_[0] for _, ms_ in ev]
+        nbytes = [bench.launch_bytes(j, picks)[0] for j, _ in ev]
+        kernel = ("layer1_kernel (ea_ffn_moe_decode at one row routed from logits, the whole layer in one launch: "
+                  "top-8, gate|up of the 8 picks and the shared expert, SwiGLU, down, slot-ordered combine)")
+    elif args.path == "fused":
+        durs = [ms_[0] for _, ms_ in ev]
         nbytes = [bench.gateup_bytes(j, picks) for j, _ in ev]
-        kernel = ("gateup_kernel (ea_ffn_moe_decode's first launch: per-block top-8 and grouping, then the gate and "
-                  "up EXL3 GEMV of every touched routed expert and of the shared expert)" if R == 1 else
-                  "route_kernel + gateup_wide_kernel (ea_ffn_moe_decode's first two launches, timed together: the "
+        kernel = ("route_kernel + gateup_wide_kernel (ea_ffn_moe_decode's first two launches, timed together: the "
                   "window's top-8 and grouping once, then the gate and up EXL3 GEMV of every touched routed expert and "
                   "of the shared expert)")
-        stages = {name: round(sum(ms[k] for _, ms in ev) / len(ev) * 1e3, 3)
+        stages = {name: round(sum(ms_[k] for _, ms_ in ev) / len(ev) * 1e3, 3)
                   for k, name in enumerate(("gateup_us", "epilogue_us", "down_us", "combine_us"))}
     else:
         durs = [a.elapsed_time(b) for _, a, b, _ in ev]
@@ -395,24 +454,36 @@ def run_decode(args, torch, np) -> dict:
     avg_b = sum(nbytes) / len(nbytes)
     achieved = avg_b / (avg_ms * 1e-3) / 1e9
     # the step's own roofline, from the timed steps' launches
-    first = args.warmup * per_step
+    first = (args.warmup if graph_ms is not None else total + args.warmup) * per_step
     lb = [bench.launch_bytes(first + j, picks) for j in range(args.steps * per_step)]
     step_b = sum(b for b, _ in lb) / args.steps
     step_f = sum(f for _, f in lb) / args.steps
     us = ms * 1e3
     t_roof_us = max(step_b / (HBM_PEAK_GBS * 1e9), step_f / (FP16_PEAK_TFLOPS * 1e12)) * 1e6
-    config = {"workload": workload, "path": args.path, "layers_resident": n_layers, "step_bytes": int(step_b),
-              "step_flops": int(step_f), "step_roofline_us": round(t_roof_us, 3),
-              "step_hbm_frac": round(t_roof_us / us, 4), "step_gbs": round(step_b / (us * 1e-6) / 1e9, 1)}
+    distinct = float(np.mean([len(set(int(e) for e in picks[first + j].reshape(-1)))
+                              for j in range(args.steps * per_step)]))
+    config = {"workload": workload, "path": args.path, "timing": "hip graph" if graph_ms is not None else "eager",
+              "eager_us": round(eager_ms * 1e3, 3), "layers_resident": n_layers, "distinct_experts_per_layer":
+              round(distinct, 2), "step_bytes": int(step_b), "step_flops": int(step_f),
+              "step_roofline_us": round(t_roof_us, 3), "step_hbm_frac": round(t_roof_us / us, 4),
+              "step_gbs": round(step_b / (us * 1e-6) / 1e9, 1)}
     roofline = {"kernel": kernel, "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None, "avg_launch_us": round(avg_ms * 1e3, 3),
-                "bytes_per_launch": int(avg_b), "launches_timed": len(durs)}
+                "bytes_per_launch": int(avg_b), "launches_timed": len(durs),
+                "timing": "HIP events recorded on the launch stream around each launch (dispatch included)"}
     if stages:
         roofline["layer_stages"] = stages
-    if args.config == "decode" and args.path == "fused":
-        roofline["traffic"] = recorded_traffic()
-        if roofline["traffic"]:
-            roofline["traffic_source"] = "profiles/gateup_kernel_config2_traffic.md (rocprofv3 --pmc, copy-calibrated)"
+    if args.config == "decode" and one_launch:
+        prof = "layer1_kernel_config2.md"
+        rp = recorded_figure(prof, "layer1_kernel_avg_us")
+        if rp:
+            roofline["rocprof_avg_us"] = rp
+            roofline["rocprof_frac"] = round(avg_b / (rp * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)
+            roofline["rocprof_source"] = f"profiles/{prof} (rocprofv3 --kernel-trace --stats)"
+        tr = recorded_figure(prof, "traffic_bytes_per_launch")
+        if tr:
+            roofline["traffic"] = int(tr)
+            roofline["traffic_source"] = f"profiles/{prof} (rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE; copy-calibrated)"
     cpu = None if args.no_cpu_baseline else cpu_baseline_decode(args.seed, R, mixed, layers_per_unit=per_step,
                                                                 unit=unit)
     return _line(args, us, unit, ms, config, roofline, cpu)
@@ -458,11 +529,14 @@ def run_linear(args, torch, np) -> dict:
     return _line(args, us, "us/linear", ms, config, roofline, None)
 
 
-def run_prefill(args, torch, np, R: int) -> dict:
-    """Config 4: prompt_experts.run over R rows, Zipf(1.1) routing, 4-bit experts."""
+def run_prefill(args, torch, np, R: int, steps: int | None = None, warmup: int | None = None) -> dict:
+    """Config 4: prompt_experts.run over R rows, Zipf(1.1) routing, 4-bit experts. Its binding roof is HBM (about 68
+    flops a byte at 512 rows, below the ~312 ridge); the MFMA fraction is reported beside it."""
     from ea_exl3 import device, prompt_experts, synth
     from ea_exl3.resident import DeviceRouted
 
+    steps = args.steps if steps is None else steps
+    warmup = args.warmup if warmup is None else warmup
     lay = DeviceRouted(args.seed, E, D, I, k2=8, cb=1)
 
     class _Ex:
@@ -484,20 +558,27 @@ def run_prefill(args, torch, np, R: int) -> dict:
         prompt_experts.run(s, x.data_ptr(), D, dp.data_ptr(), dw.data_ptr(), ex, sc, out.data_ptr(), R,
                            do_round=False, x_dtype=0)
 
-    ms = time_steps(step, args.steps, args.warmup, torch)
+    ms = time_steps(step, steps, warmup, torch)
     distinct = sorted(set(int(e) for e in pick.reshape(-1)))
     b = sum(lay.expert_bytes(e) for e in distinct) + R * D * 2 + R * D * 4 + R * SLOTS * 8
     f = 2 * R * SLOTS * 3 * D * I
     us = ms * 1e3
-    t_roof = max(b / (HBM_PEAK_GBS * 1e9), f / (FP16_PEAK_TFLOPS * 1e12)) * 1e6
-    tfs = f / (us * 1e-6) / 1e12
+    t_hbm, t_mfma = b / (HBM_PEAK_GBS * 1e9) * 1e6, f / (FP16_PEAK_TFLOPS * 1e12) * 1e6
+    gbs, tfs = b / (us * 1e-6) / 1e9, f / (us * 1e-6) / 1e12
     config = {"workload": f"config 4: prefill chunk of {R} tokens x 6144 through prompt_experts.run, Zipf(1.1) top-8 "
                           "routing over 256 4-bit experts", "distinct_experts": len(distinct), "step_bytes": b,
-              "step_flops": f, "step_roofline_us": round(t_roof, 3), "step_roof_frac": round(t_roof / us, 4),
-              "step_gbs": round(b / (us * 1e-6) / 1e9, 1)}
-    roofline = {"kernel": "prompt_experts.run (whole call)", "bound": "mfma", "achieved": round(tfs, 2),
-                "peak": FP16_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(tfs / FP16_PEAK_TFLOPS, 4), "traffic": None}
-    return _line(args, us, "us/layer", ms, config, roofline, None)
+              "step_flops": f, "step_roofline_us": round(max(t_hbm, t_mfma), 3),
+              "step_roof_frac": round(max(t_hbm, t_mfma) / us, 4), "step_gbs": round(gbs, 1),
+              "step_tflops": round(tfs, 2), "mfma_frac": round(tfs / FP16_PEAK_TFLOPS, 4)}
+    roofline = {"kernel": "prompt_experts.run (whole call: route, rot_in, gate|up item GEMMs, epilogue, down item "
+                          "GEMMs, combine)", "bound": "hbm" if t_hbm >= t_mfma else "mfma",
+                "achieved": round(gbs, 1) if t_hbm >= t_mfma else round(tfs, 2),
+                "peak": HBM_PEAK_GBS if t_hbm >= t_mfma else FP16_PEAK_TFLOPS,
+                "unit": "GB/s" if t_hbm >= t_mfma else "TFLOP/s",
+                "frac": round(max(t_hbm, t_mfma) / us, 4), "traffic": None,
+                "mfma": {"achieved": round(tfs, 2), "peak": FP16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                         "frac": round(tfs / FP16_PEAK_TFLOPS, 4)}}
+    return _line(args, us, "us/layer", ms, config, roofline, None) | {"steps": steps, "warmup": warmup}
 
 
 def main() -> int:
@@ -520,6 +601,13 @@ def main() -> int:
         result = run_linear(args, torch, np)
     else:
         result = run_prefill(args, torch, np, 512 if args.config == "prefill512" else 2048)
+    if args.config == "decode" and not args.no_prefill:
+        # the metric's second half: the 512-token prefill chunk (config 4), a bounded run beside the decode layer
+        pf = run_prefill(args, torch, np, 512, steps=20, warmup=3)
+        result["prefill512"] = {k: pf[k] for k in ("value", "unit", "steps", "warmup", "ms_per_step", "config",
+                                                   "roofline")}
+    result["library"] = library_identity()
+    result["device"] = device_identity(torch)
     print(json.dumps(result))
     return 0
 
