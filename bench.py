@@ -58,6 +58,9 @@ def parse():
                          "moe.routed's six launches, the shared expert's linears, swiglu2, add)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-prefill", action="store_true", help="decode: leave out the 512-token prefill object")
+    ap.add_argument("--router", action="store_true",
+                    help="decode configs: compute each layer's logits from x by a bf16 router weight "
+                         "(ea_ffn_moe_decode_router) instead of reading given logits")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a plain device copy of known size (for HBM counter calibration)")
     ap.add_argument("--seed", type=int, default=1234)
@@ -71,7 +74,7 @@ class DecodeBench:
     R rows; layer launch j uses resident layer j mod n_layers."""
 
     def __init__(self, R: int, n_layers: int, per_step: int, mixed: bool, seed: int, steps_total: int, path: str,
-                 uniform: bool = False):
+                 uniform: bool = False, router: bool = False):
         import numpy as np
         import torch
         from ea_exl3 import device, experts, linear, moe, ops, synth
@@ -117,6 +120,13 @@ class DecodeBench:
         self._ex_ref = [C.byref(e.c) for e in self.ex]
         self._sc_ref = C.byref(self.scratch.c)
         self._logits0, self._pick0, self._wts0 = self.logits.data_ptr(), self.pick.data_ptr(), self.wts.data_ptr()
+        # with `router`, each layer computes its logits from x by its own bf16 router weight [256, D]
+        # (ea_ffn_moe_decode_router) instead of reading given ones
+        self.router = router
+        if router:
+            self.router_w = [(0.02 * torch.randn((E, D), device="cuda", generator=gen)).to(torch.bfloat16)
+                             for _ in range(n_layers)]
+            self.fn_router = lib().ea_ffn_moe_decode_router
         self._x, self._bias, self._out = self.x.data_ptr(), self.bias.data_ptr(), self.out.data_ptr()
 
     def layer_of(self, j: int) -> int:
@@ -128,6 +138,16 @@ class DecodeBench:
             self.sequence(j)
             return
         l, R = self.layer_of(j), self.R
+        if self.router:
+            r = self.fn_router(stream or self.s, self._x, 0, D, self.router_w[l].data_ptr(),
+                               self._logits0 + j * R * E * 4, self._bias, ROUTED_SCALE, self._pick0 + j * R * SLOTS * 4,
+                               self._wts0 + j * R * SLOTS * 4, self._ex_ref[l], self._sh_ptr[l], self._sc_ref,
+                               self._out, R)
+            if r:
+                from ea_exl3._lib import check
+
+                check(r, "ffn_decode_router")
+            return
         r = self.fn(stream or self.s, self._x, 0, D, self._logits0 + j * R * E * 4, self._bias, ROUTED_SCALE,
                     self._pick0 + j * R * SLOTS * 4, self._wts0 + j * R * SLOTS * 4, self._ex_ref[l],
                     self._sh_ptr[l], self._sc_ref, self._out, R)
@@ -204,6 +224,9 @@ class DecodeBench:
         b = sum(self.layers[l].expert_bytes(e) for e in distinct) + self.shared[l].bytes()
         b += self.R * D * 2 + self.R * E * 4 + E * 4 + self.R * D * 4 + 2 * self.R * SLOTS * 4
         f = 2 * (self.R * SLOTS + self.R) * 3 * D * I
+        if self.router:  # the router weight read once, its product
+            b += E * D * 2
+            f += 2 * self.R * E * D
         return b, f
 
     def gateup_bytes(self, j: int, picks) -> int:
@@ -409,7 +432,7 @@ def run_decode(args, torch, np) -> dict:
     n_layers = 75 if args.config == "stack" else args.layers
     total = args.warmup + args.steps
     bench = DecodeBench(R, n_layers, per_step, mixed, args.seed, 3 * total + 2, args.path,
-                        uniform=args.config == "multi")
+                        uniform=args.config == "multi", router=args.router)
     # the timed region: K whole steps replayed from a HIP graph (how the reference runs decode); the same steps
     # launched one by one from the host are timed beside it
     graph_ms = time_graph(bench.step, args.steps, args.warmup, torch) if args.path == "fused" else None
@@ -462,6 +485,8 @@ def run_decode(args, torch, np) -> dict:
     t_roof_us = max(step_b / (HBM_PEAK_GBS * 1e9), step_f / (FP16_PEAK_TFLOPS * 1e12)) * 1e6
     distinct = float(np.mean([len(set(int(e) for e in picks[first + j].reshape(-1)))
                               for j in range(args.steps * per_step)]))
+    if args.router:
+        workload += "; logits computed from x by a bf16 router weight [256, 6144] (ea_ffn_moe_decode_router)"
     config = {"workload": workload, "path": args.path, "timing": "hip graph" if graph_ms is not None else "eager",
               "eager_us": round(eager_ms * 1e3, 3), "layers_resident": n_layers, "distinct_experts_per_layer":
               round(distinct, 2), "step_bytes": int(step_b), "step_flops": int(step_f),
@@ -603,7 +628,7 @@ def main() -> int:
         result = run_prefill(args, torch, np, 512 if args.config == "prefill512" else 2048)
     if args.config == "decode" and not args.no_prefill:
         # the metric's second half: the 512-token prefill chunk (config 4), a bounded run beside the decode layer
-        pf = run_prefill(args, torch, np, 512, steps=20, warmup=3)
+        pf = run_prefill(args, torch, np, 512, steps=50, warmup=10)
         result["prefill512"] = {k: pf[k] for k in ("value", "unit", "steps", "warmup", "ms_per_step", "config",
                                                    "roofline")}
     result["library"] = library_identity()

@@ -56,6 +56,7 @@ struct DLLayout {
 
 struct DLArgs {
     const float* logits;  // [R, 256] or null: pick / wts are then inputs
+    const void* router_w; // bf16 [256, D] or null: when given, a router launch first writes the logits (host side only)
     const float* bias;
     float scale;
     int32_t* pick;
@@ -1462,9 +1463,15 @@ static int dl_launch(hipStream_t s, const DLArgs& a, int cus, int device) {
         per_cu_wide = n;
     }
     const int NH = a.I / 128, KC = a.D / 256, DB = a.D / 128;
+    mark_stage(s, device, 0);
+    if (a.router_w) {
+        // the router's logits first (ops.router: ea_router's launch), into the caller's logits buffer
+        const int r = launch_router(s, a.x, a.x_dtype, (uint32_t)a.x_stride, a.router_w, nullptr,
+                                    const_cast<float*>(a.logits), (uint32_t)a.R, (uint32_t)a.D, 256u);
+        if (r) return r;
+    }
     if (a.R == 1 && a.logits) {
         // one row routed from logits: the whole layer in one launch (the stage events then all follow it)
-        mark_stage(s, device, 0);
         layer1_kernel<CB, SCB><<<a.U * NH * 2 * KC + a.U * DB, DL_THREADS, 0, s>>>(a);
         const int r = launched();
         if (r) return r;
@@ -1475,7 +1482,6 @@ static int dl_launch(hipStream_t s, const DLArgs& a, int cus, int device) {
     const int items = a.U * (wide ? 1 : NH) * 2 * KC;
     int grid = (wide ? per_cu_wide : per_cu) * cus;
     if (grid > items) grid = items;
-    mark_stage(s, device, 0);
     if (a.R > 1) {
         route_kernel<<<1, DL_ROUTE_THREADS, 0, s>>>(a);
         const int r = launched();
@@ -1513,7 +1519,8 @@ static int dl_launch(hipStream_t s, const DLArgs& a, int cus, int device) {
 // not instantiated here; the caller then runs the launch sequence.
 int decode_layer(hipStream_t s, const void* x, int x_dtype, uint32_t x_stride, const float* logits,
                  const float* bias, float scale, int32_t* pick, float* wts, const ea_routed* ex,
-                 const ea_linear* const* shared, const ea_moe_scratch* sc, float* out, uint32_t R) {
+                 const ea_linear* const* shared, const ea_moe_scratch* sc, float* out, uint32_t R,
+                 const void* router_w) {
     EA_REQUIRE_CTX(c);
     const uint32_t D = ex->dims, I = ex->width, E = ex->count, slots = sc->slots;
     if (!sc->fused || R > sc->rows || !dl_shape_ok(sc->rows, slots, D, I, E)) return EA_UNPORTED_GROUPED_VARIANT;
@@ -1522,6 +1529,13 @@ int decode_layer(hipStream_t s, const void* x, int x_dtype, uint32_t x_stride, c
     if (x_dtype != EA_F16 && x_dtype != EA_BF16) return EA_UNPORTED_GROUPED_VARIANT;
     // activation rows are read a word (two values) at a time
     if ((reinterpret_cast<uintptr_t>(x) & 3) || (x_stride & 1)) return EA_UNPORTED_GROUPED_VARIANT;
+    if (router_w) {
+        // the router launch's own conditions, checked before anything is launched
+        if (!logits || E != 256) return EA_BAD_ARGUMENT;
+        if (D % 512 != 0) return EA_UNEVEN_SPLIT;
+        if (x_stride < D || x_stride % 4 != 0) return EA_BAD_ROW_STRIDE;
+        if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(router_w)) & 7) return EA_BAD_ARGUMENT;
+    }
     int scb = (int)ex->cb;
     DLArgs a{};
     if (shared) {
@@ -1540,6 +1554,7 @@ int decode_layer(hipStream_t s, const void* x, int x_dtype, uint32_t x_stride, c
         }
     }
     a.logits = logits;
+    a.router_w = router_w;
     a.bias = bias;
     a.scale = scale;
     a.pick = pick;
@@ -1628,7 +1643,7 @@ int ea_ffn_moe_decode_static(ea_stream_t stream, const void* x, int x_dtype, uin
     sc.rows = DL_MAXR;
     sc.slots = DL_SLOTS;
     return decode_layer(as_stream(stream), x, x_dtype, x_stride, logits, bias, scale, pick, wts, ex, shared, &sc, out,
-                        R);
+                        R, nullptr);
 }
 
 int ea_profile_enable(int on) {
@@ -1667,7 +1682,19 @@ int ea_ffn_moe_decode(ea_stream_t stream, const void* x, int x_dtype, uint32_t x
     if (R > sc->rows) return EA_SCRATCH_TOO_SMALL;
     if (R == 0) return EA_OK;
     return decode_layer(as_stream(stream), x, x_dtype, x_stride, logits, bias, scale, pick, wts, ex, shared, sc, out,
-                        R);
+                        R, nullptr);
+}
+
+int ea_ffn_moe_decode_router(ea_stream_t stream, const void* x, int x_dtype, uint32_t x_stride, const void* router_w,
+                             float* logits, const float* bias, float scale, int32_t* pick, float* wts,
+                             const ea_routed* ex, const ea_linear* const* shared, const ea_moe_scratch* sc, float* out,
+                             uint32_t R) {
+    EA_REQUIRE_CTX(c);
+    if (!x || !router_w || !logits || !bias || !pick || !wts || !ex || !sc || !out) return EA_BAD_ARGUMENT;
+    if (R > sc->rows) return EA_SCRATCH_TOO_SMALL;
+    if (R == 0) return EA_OK;
+    return decode_layer(as_stream(stream), x, x_dtype, x_stride, logits, bias, scale, pick, wts, ex, shared, sc, out,
+                        R, router_w);
 }
 
 }  // extern "C"

@@ -24,11 +24,17 @@ int launch_down_combine(hipStream_t s, const float* z, const int* pick, const ui
                         const float* wts, float* out, uint32_t rows, uint32_t p, uint32_t d, uint32_t sk,
                         uint32_t slots, uint32_t experts, bool skip_invalid = false);
 
-// The one-launch decode layer (ea_decode_layer.hip): the region a moe scratch of `rows` rows holds for it (zero when
-// the shape has none), and the launch itself (EA_UNPORTED_GROUPED_VARIANT when not instantiated for the layer).
+// The decode layer (ea_decode_layer.hip): the region a moe scratch of `rows` rows holds for it (zero when the shape
+// has none), and its launches (EA_UNPORTED_GROUPED_VARIANT when not instantiated for the layer). router_w (bf16
+// [256, D]) or null: when given, a router launch first writes the logits into `logits`.
 size_t dl_region_bytes(uint32_t rows, uint32_t slots, uint32_t D, uint32_t I, uint32_t E);
 int decode_layer(hipStream_t s, const void* x, int x_dtype, uint32_t x_stride, const float* logits,
                  const float* bias, float scale, int32_t* pick, float* wts, const ea_routed* ex,
-                 const ea_linear* const* shared, const ea_moe_scratch* sc, float* out, uint32_t R);
+                 const ea_linear* const* shared, const ea_moe_scratch* sc, float* out, uint32_t R,
+                 const void* router_w = nullptr);
+
+// The router's logits (ea_router.hip): out fp32 [m, ne] = x [m, d] @ w^T, eight slices added in order.
+int launch_router(hipStream_t s, const void* x, int x_dtype, uint32_t x_stride, const void* w, float* part, float* out,
+                  uint32_t m, uint32_t d, uint32_t ne);
 
 }  // namespace ea

@@ -98,11 +98,14 @@ SIGNATURES = {
     "ea_linear_call_rotated": (I32, [P, C.POINTER(LinearScratch), C.POINTER(C.POINTER(Linear)), U32, U32,
                                      C.POINTER(U64), C.POINTER(C.c_int)]),
     "ea_topk8": (I32, [P, P, P, P, P, U32, F32, P]),
+    "ea_router": (I32, [P, P, I32, U32, P, P, P, U32, U32, U32]),
     "ea_swiglu2": (I32, [P, P, P, P, U32, U32]),
     "ea_add_f32": (I32, [P, P, P, C.c_size_t]),
     "ea_profile_enable": (I32, [I32]),
     "ea_profile_stages": (I32, [P, U32]),
     "ea_ffn_moe_decode": (I32, [P, P, I32, U32, P, P, F32, P, P, C.POINTER(Routed), P, C.POINTER(MoeScratch), P, U32]),
+    "ea_ffn_moe_decode_router": (I32, [P, P, I32, U32, P, P, P, F32, P, P, C.POINTER(Routed), P,
+                                       C.POINTER(MoeScratch), P, U32]),
     "ea_ffn_moe_decode_static": (I32, [P, P, I32, U32, P, P, F32, P, P, C.POINTER(Routed), P, P, U32]),
 }
 

@@ -100,6 +100,20 @@ def ffn_decode(stream: int, x: int, x_stride: int, logits: int, bias: int, scale
                                   C.byref(s.c), out, R), "ffn_decode")
 
 
+def ffn_decode_router(stream: int, x: int, x_stride: int, router_w: int, logits: int, bias: int, scale: float,
+                      pick: int, wts: int, ex: Routed, shared, s: Scratch, out: int, R: int, x_dtype: int = 1) -> None:
+    """ffn_decode from the normed activations (forward.zig:2350-2403): logits fp32 [R, 256] = x @ router_w^T (bf16
+    router weight [256, D], ops.router's eight ordered slices) into `logits`, then ffn_decode on them."""
+    arr = None
+    if shared is not None:
+        from ._lib import Linear as _Linear
+
+        arr = (C.POINTER(_Linear) * 3)(*[C.pointer(l) for l in shared])
+    check(lib().ea_ffn_moe_decode_router(stream, x, x_dtype, x_stride, router_w, logits, bias, scale, pick, wts,
+                                         C.byref(ex.c), C.addressof(arr) if arr is not None else None, C.byref(s.c),
+                                         out, R), "ffn_decode_router")
+
+
 def ffn_decode_static(stream: int, x: int, x_stride: int, logits: int, bias: int, scale: float, pick: int, wts: int,
                       ex: Routed, shared, out: int, R: int, x_dtype: int = 1) -> None:
     """ffn_decode with no scratch argument (ea_ffn_moe_decode_static): the library's per-device scratch array, for

@@ -1,7 +1,15 @@
-"""The routing input and the shared expert's activation: ops.topk (ops.zig:187-191) and swiglu2 (native_ops.cu)."""
+"""The routing input and the shared expert's activation: ops.router (ops.zig:131-136), ops.topk (ops.zig:187-191)
+and swiglu2 (native_ops.cu)."""
 from __future__ import annotations
 
 from ._lib import check, lib
+
+
+def router(stream: int, x: int, x_stride: int, w: int, part: int, out: int, m: int, d: int, ne: int,
+           x_dtype: int = 1) -> None:
+    """out fp32 [m, ne] = x [m, d] @ w^T (w bf16 [ne, d]), the reduction in eight slices of d / 8 added in order
+    (written to part fp32 [8, m, ne] too when part != 0). x bf16 as the reference's, or fp16 (x_dtype 0)."""
+    check(lib().ea_router(stream, x, x_dtype, x_stride, w, part, out, m, d, ne), "router")
 
 
 def topk(stream: int, logits: int, bias: int, pick: int, wts: int, rows: int, scale: float = 2.5, log: int = 0) -> None:

@@ -225,6 +225,17 @@ int ea_linear_call_rotated(ea_stream_t stream, const ea_linear_scratch* s, const
 int ea_topk8(ea_stream_t stream, const float* logits, const float* bias, int32_t* pick, float* wts, uint32_t rows,
              float scale, uint8_t* log);
 
+/* The router's logits: out fp32 [m, ne] = x [m, d] @ w^T, w bf16 [ne, d] (rows of d), x fp16 or bf16 (x_dtype 0 / 1;
+ * the reference takes bf16) with rows x_stride elements apart. The reduction over d is cut into eight slices of d / 8
+ * that are added in slice order; when part is not NULL the slice sums are also written to part fp32 [8, m, ne]. One
+ * launch. Replaces ops.router (ops.zig:131-136): router_part (native_ops.cu:1405-1460) + router_sum (:335-362).
+ * Within a slice the order is this build's (the reference's is inside tensor-core MMAs): lane l of a wave sums the
+ * 4-value chunks l, l + 64, .. of the slice in order by fp32 fma, then a butterfly adds the 64 lane sums over lane
+ * distances 32, 16, 8, 4, 2, 1. d % 512 != 0: EA_UNEVEN_SPLIT (ops.zig:134 unsupported); x_stride < d or not a
+ * multiple of 4: EA_BAD_ROW_STRIDE; x or w not 8-byte aligned: EA_BAD_ARGUMENT. */
+int ea_router(ea_stream_t stream, const void* x, int x_dtype, uint32_t x_stride, const void* w, float* part,
+              float* out, uint32_t m, uint32_t d, uint32_t ne);
+
 /* out = bf16(bf16(silu(g)) * u) over rows of `width` bf16. Replaces ops.swiglu2 (native_ops.cu:429-441). */
 int ea_swiglu2(ea_stream_t stream, const void* g, const void* u, void* out, uint32_t rows, uint32_t width);
 
@@ -246,6 +257,17 @@ int ea_add_f32(ea_stream_t stream, float* a, const float* b, size_t n);
 int ea_ffn_moe_decode(ea_stream_t stream, const void* x, int x_dtype, uint32_t x_stride, const float* logits,
                       const float* bias, float scale, int32_t* pick, float* wts, const ea_routed* ex,
                       const ea_linear* const* shared, const ea_moe_scratch* s, float* out, uint32_t R);
+
+/* ffnMain's routing and expert part from the normed activations: logits fp32 [R, 256] = x @ router_w^T (router_w bf16
+ * [256, D]; ea_router's launch and summation order), written to `logits` (caller-owned, as the reference's mlog), then
+ * ea_ffn_moe_decode on them. Replaces ops.router -> ops.topk -> moe.routed -> forward.mlp -> glue.addF32
+ * (forward.zig:2350-2403; ops.zig:131-136). Beyond ea_ffn_moe_decode's conditions: D % 512 == 0 (EA_UNEVEN_SPLIT),
+ * x_stride >= D and a multiple of 4 (EA_BAD_ROW_STRIDE), x and router_w 8-byte aligned (EA_BAD_ARGUMENT); all are
+ * checked before the first launch. */
+int ea_ffn_moe_decode_router(ea_stream_t stream, const void* x, int x_dtype, uint32_t x_stride, const void* router_w,
+                             float* logits, const float* bias, float scale, int32_t* pick, float* wts,
+                             const ea_routed* ex, const ea_linear* const* shared, const ea_moe_scratch* s, float* out,
+                             uint32_t R);
 
 /* ea_ffn_moe_decode without a scratch argument: it allocates nothing and takes no workspace. No counterpart in the
  * reference: it is for callers that cannot allocate device memory (code under HIP graph capture, tight serving loops,

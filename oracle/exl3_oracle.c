@@ -647,6 +647,41 @@ void or_topk8(const float* logits, const float* bias, int rows, int E, float sca
     free(key);
 }
 
+/* ops.zig:131-136 (router_part native_ops.cu:1405-1460, router_sum :335-362): out [m, ne] = x [m, d] @ w^T, the
+ * reduction in eight slices of kw = d / 8 added in slice order (part [8, m, ne] holds the slice sums when given).
+ * Inside a slice, the order of this build's kernel (the reference's is inside tensor-core MMAs): 64 lane sums, lane l
+ * taking the 4-value chunks c = l, l + 64, .. (c < kw / 4) in order by fp32 fma, then a butterfly: at distance
+ * 32, 16, 8, 4, 2, 1 each lane sum becomes itself + the sum of lane (l ^ distance). x_dtype 0 fp16, 1 bf16. */
+void or_router(const uint16_t* x, int x_dtype, int x_stride, const uint16_t* w, int m, int d, int ne, float* part,
+               float* out) {
+    const int kw = d / 8, nc = kw / 4;
+#pragma omp parallel for schedule(static)
+    for (int r = 0; r < m; ++r) {
+        for (int e = 0; e < ne; ++e) {
+            float tot = 0.f;
+            for (int s = 0; s < 8; ++s) {
+                float lane[64], nxt[64];
+                for (int l = 0; l < 64; ++l) lane[l] = 0.f;
+                for (int c = 0; c < nc; ++c) {
+                    const size_t k = (size_t)s * kw + 4 * (size_t)c;
+                    for (int i = 0; i < 4; ++i) {
+                        const uint16_t xv = x[(size_t)r * x_stride + k + i];
+                        const float xf = x_dtype == 1 ? or_bf2f(xv) : or_h2f(xv);
+                        lane[c % 64] = fmaf(xf, or_bf2f(w[(size_t)e * d + k + i]), lane[c % 64]);
+                    }
+                }
+                for (int dist = 32; dist >= 1; dist >>= 1) {
+                    for (int l = 0; l < 64; ++l) nxt[l] = lane[l] + lane[l ^ dist];
+                    memcpy(lane, nxt, sizeof(lane));
+                }
+                if (part) part[((size_t)s * m + r) * ne + e] = lane[0];
+                tot = s ? tot + lane[0] : lane[0];
+            }
+            out[(size_t)r * ne + e] = tot;
+        }
+    }
+}
+
 /* native_ops.cu:429-441: out = bf16(bf16(silu(g)) * u), silu(g) = g / (exp(-g) + 1). */
 void or_swiglu2(const uint16_t* g, const uint16_t* u, uint16_t* out, int n) {
     for (int i = 0; i < n; ++i) {

@@ -110,6 +110,10 @@ void or_exl3_linear(const uint16_t* xh, const uint32_t* T, int64_t stride_k, int
                     const uint16_t* svh, const uint16_t* bias, void* y, int y_dtype, int M, int K, int N,
                     int k2, int cb, int SK, int WK);
 
+/* ---- router logits (ops.zig:131-136; native_ops.cu:335-362, 1405-1460) ---- */
+void or_router(const uint16_t* x, int x_dtype, int x_stride, const uint16_t* w, int m, int d, int ne, float* part,
+               float* out);
+
 /* ---- router top-8 (native_ops.cu:998-1068) ---- */
 void or_topk8(const float* logits, const float* bias, int rows, int E, float scale, int* pick, float* wts);
 

@@ -65,6 +65,7 @@ def _declare(L):
         "or_linear_plan": (None, [I, I, P, P]),
         "or_exl3_rot_in": (None, [P, I, P, P, I, I]),
         "or_exl3_linear": (None, [P, P, I64, I64, P, P, P, I, I, I, I, I, I, I, I]),
+        "or_router": (None, [P, I, I, P, I, I, I, P, P]),
         "or_topk8": (None, [P, P, I, I, F, P, P]),
         "or_swiglu2": (None, [P, P, P, I]),
         "or_mix64": (C.c_uint64, [C.c_uint64]),
@@ -312,6 +313,19 @@ def exl3_linear(xh, T, stride_k, stride_nb, svh, M, K, N, k2, cb, SK, WK, bias=N
 
 
 # ---- router and shared expert ----------------------------------------------------------------------------------
+
+def router(x, w, x_dtype=1, with_part=False):
+    """logits f32 [m, ne] of x 16-bit [m, d] (x_dtype 0 fp16, 1 bf16) by w bf16 [ne, d]; with the slice sums
+    [8, m, ne] too when with_part."""
+    x = np.ascontiguousarray(x, dtype=np.uint16)
+    w = np.ascontiguousarray(w, dtype=np.uint16)
+    m, d = x.shape
+    ne = w.shape[0]
+    out = np.zeros((m, ne), np.float32)
+    part = np.zeros((8, m, ne), np.float32) if with_part else None
+    lib().or_router(_p(x), x_dtype, d, _p(w), m, d, ne, _p(part), _p(out))
+    return (out, part) if with_part else out
+
 
 def topk8(logits, bias, scale=2.5):
     logits = np.ascontiguousarray(logits, dtype=np.float32)

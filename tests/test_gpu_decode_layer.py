@@ -252,3 +252,38 @@ def test_unsupported_width_poisons_output(ea):
     assert np.isnan(device.download(out)).all()
     assert device.device_status() == 19  # read and cleared
     assert device.device_status() == 0
+
+
+@pytest.mark.parametrize("rows_seq,x_dtype", [([1, 1], 0), ([16, 4], 1)])
+def test_ffn_decode_from_router(ea, rows_seq, x_dtype):
+    """ea_ffn_moe_decode_router: the router's logits (bf16 router weight [256, D], ops.router's ordered slices) written
+    to the caller's buffer and then routed, as forward.zig:2350-2403 does. The logits must be the oracle router's bits,
+    pick / wts the oracle top-8's of them, out within 2e-3 * RMS(out); one and sixteen rows on one scratch."""
+    device, linear, moe, synth = ea
+    E, D, I, seed = 256, 6144, 256, 1300
+    rng = np.random.default_rng(seed)
+    rw = synth.bf16_bits((0.02 * rng.standard_normal((E, D))).astype(np.float32))
+    xs = [synth.activations(seed + 1 + i, R, D, ["f16", "bf16"][x_dtype]) for i, R in enumerate(rows_seq)]
+    _, bias = synth.logits(seed, 1)
+    logits_list = [orc.router(x, rw, x_dtype) for x in xs]
+    host = _layer_for(synth, seed + 10, logits_list, bias, E, D, I, 8, 1)
+    shared = SharedHost(linear, synth, seed + 20, D, I, 8, 1)
+    ex = moe.Routed(host)
+    sc = moe.Scratch(ex, 16, 8)
+    drw, db = device.upload(rw), device.upload(bias)
+    for i, R in enumerate(rows_seq):
+        x = xs[i]
+        print(f"decode from router R={R} x_dtype={x_dtype}", flush=True)
+        dx = device.upload(x)
+        dl = device.zeros((R, E), torch.float32)
+        dp, dw = device.zeros((R, 8), torch.int32), device.zeros((R, 8), torch.float32)
+        out = device.zeros((R, D), torch.float32)
+        moe.ffn_decode_router(device.stream(), dx.data_ptr(), D, drw.data_ptr(), dl.data_ptr(), db.data_ptr(), 2.5,
+                              dp.data_ptr(), dw.data_ptr(), ex, [l.c for l in shared.lin], sc, out.data_ptr(), R,
+                              x_dtype=x_dtype)
+        np.testing.assert_array_equal(device.download(dl).view(np.uint32), logits_list[i].view(np.uint32))
+        want, pick_w, wts_w = _want(host, shared, x, logits_list[i], bias, R, x_dtype == 1)
+        np.testing.assert_array_equal(device.download(dp), pick_w)
+        np.testing.assert_array_equal(device.download(dw), wts_w)
+        assert_close_rms(device.download(out), want, 2e-3, f"ffn decode from router R={R}")
+        assert device.device_status() == 0
