@@ -1036,28 +1036,6 @@ __device__ __forceinline__ int* l1_dcnt(int* s, int u) { return s + (3 * L1_UNIT
 __device__ __forceinline__ int* l1_ccnt(int* s, int cb) { return s + (4 * L1_UNITS + cb) * L1_LINE; }
 static_assert((4 * L1_UNITS + L1_MAXDB) * L1_LINE * 4 <= (int)L1_SYNC_BYTES, "the counters fit their region");
 
-// Agent-scope (coherent across the XCDs) stores and loads of handed-on data, and counting in.
-__device__ __forceinline__ void st_coh(float* p, float v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
-__device__ __forceinline__ void st_coh(uint32_t* p, uint32_t v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void st_coh2(float* p, float2 v) {
-    __hip_atomic_store(reinterpret_cast<uint64_t*>(p), __builtin_bit_cast(uint64_t, v), __ATOMIC_RELAXED,
-                       __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ uint32_t ld_coh(const uint32_t* p) {
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ float2 ld_coh2(const float* p) {
-    return __builtin_bit_cast(float2, __hip_atomic_load(reinterpret_cast<const uint64_t*>(p), __ATOMIC_RELAXED,
-                                                        __HIP_MEMORY_SCOPE_AGENT));
-}
-__device__ __forceinline__ int ld_coh(const int* p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
-__device__ __forceinline__ int count_in(int* c) { return __hip_atomic_fetch_add(c, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
-__device__ __forceinline__ void reset_count(int* c) { __hip_atomic_store(c, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
-// Every store this wave issued has completed (and, being agent-scope, is visible to every block).
-__device__ __forceinline__ void stores_done() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
-
 struct L1Sh {
     int pick[DL_SLOTS];
     float wts[DL_SLOTS];

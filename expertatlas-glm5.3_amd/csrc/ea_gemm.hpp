@@ -146,6 +146,31 @@ __device__ __forceinline__ void wave_tiles(const uint32_t* __restrict__ base, si
 
 __device__ __forceinline__ void record_error(int* status, int code) { atomicCAS(status, 0, code); }
 
+// ---- hand-offs between blocks of one launch ------------------------------------------------------------------------
+// Data handed to another block is written with agent-scope stores (coherent across the XCDs' L2s); the writer waits for
+// its stores (stores_done), meets its block at a barrier, and only then one thread counts in; a reader loads the data
+// with agent-scope loads issued after it has seen the count.
+__device__ __forceinline__ void st_coh(float* p, float v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+__device__ __forceinline__ void st_coh(uint32_t* p, uint32_t v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_coh2(float* p, float2 v) {
+    __hip_atomic_store(reinterpret_cast<uint64_t*>(p), __builtin_bit_cast(uint64_t, v), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint32_t ld_coh(const uint32_t* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float2 ld_coh2(const float* p) {
+    return __builtin_bit_cast(float2, __hip_atomic_load(reinterpret_cast<const uint64_t*>(p), __ATOMIC_RELAXED,
+                                                        __HIP_MEMORY_SCOPE_AGENT));
+}
+__device__ __forceinline__ int ld_coh(const int* p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+__device__ __forceinline__ int count_in(int* c) { return __hip_atomic_fetch_add(c, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+__device__ __forceinline__ void reset_count(int* c) { __hip_atomic_store(c, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+// Every store this wave issued has completed (and, being agent-scope, is visible to every block).
+__device__ __forceinline__ void stores_done() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
 // A product that could not run (a width without a decoder, a bounded wait that gave up) stores NaN in place of its
 // sums, so the call's output shows the failure as well as the status word.
 __device__ __forceinline__ f4v nan4() {

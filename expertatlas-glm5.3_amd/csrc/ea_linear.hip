@@ -40,6 +40,20 @@ __device__ __forceinline__ void finish_store(float v0, float v1, int lane, const
     store_act(y, y_dtype, at + 1, v1);
 }
 
+// The same with svh and bias already loaded: sw, bw hold this lane's two columns (two fp16 each; bias optional).
+__device__ __forceinline__ void finish_store_pre(float v0, float v1, int lane, uint32_t sw, bool has_bias, uint32_t bw,
+                                                 void* y, int y_dtype, size_t at) {
+    fwht128_w64(v0, v1, lane);
+    v0 = v0 * HAD_SCALE * h2f((uint16_t)(sw & 0xffffu));
+    v1 = v1 * HAD_SCALE * h2f((uint16_t)(sw >> 16));
+    if (has_bias) {
+        v0 += h2f((uint16_t)(bw & 0xffffu));
+        v1 += h2f((uint16_t)(bw >> 16));
+    }
+    store_act(y, y_dtype, at, v0);
+    store_act(y, y_dtype, at + 1, v1);
+}
+
 __device__ __forceinline__ float load_coherent(const float* p) {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -125,6 +139,263 @@ __global__ void __launch_bounds__(WK * 64) linear_kernel(ea_jobs jobs, int M, in
     }
 }
 
+// ---- the small-row linear: up to 16 rows, K split, every CU busy ----------------------------------------------------
+// Block (job, group g of 32 columns, split s) with WK waves: wave w multiplies k tiles [s KS + w NKT, + NKT) of the
+// group's two column tiles (KS = WK NKT, the split's tiles), the trellis staged in LDS by 16-byte loads; the waves'
+// sums are added in order into Z[s] (agent-scope stores), and the last of the 4 SK blocks of a 128-column block to
+// count in adds the splits in order and finishes it (FWHT, svh, bias). That is the reference's order of sums (waves,
+// then splits, exl3_linear.cu:231-484) over four times as many blocks as its (column block, split) grid. With ROT
+// the block rotates the activations of its split itself (the Hadamard blocks its k range touches) and the column
+// group 0 blocks also store them to xh, as the separate rotation would.
+constexpr int LS_MAXR = 16;
+constexpr int LS_MAXNKT = 16;
+constexpr int LS_FLAGS = 32;  // flag bytes a 128-column block has in the counters (int32 [8 N / 128], zero between calls)
+
+template <int CB, int K2, int NKT, bool ROT, int XL>
+__global__ void __launch_bounds__(512) lin_small_kernel(ea_jobs jobs, ea_rot_jobs rj, int M, int K, const void* x,
+                                                        int x_bf16, int* status) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    constexpr int TW = 4 * K2;
+    int ji = 0;
+#pragma unroll
+    for (int q = 1; q < EA_MAX_JOBS; ++q)
+        if (q < jobs.n && (int)blockIdx.x >= jobs.j[q].start) ji = q;
+    const ea_job& J = jobs.j[ji];
+    const int WK = blockDim.x >> 6, NT = WK * 64;
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)), lane = threadIdx.x & 63;
+    const int N = J.N, SK = J.SK, G = N >> 5;
+    const int local = (int)blockIdx.x - J.start, g = local % G, split = local / G;
+    const int kh = NKT * WK * 16, lo = split * kh;
+    // the block's activations: rows of the Hadamard blocks [hb0, hb0 + span / 128) that its k range touches (ROT), or
+    // its k range (rotated already)
+    const int hb0 = ROT ? lo >> 7 : 0, span = ROT ? (((lo + kh + 127) >> 7) - hb0) * 128 : kh;
+    const int k_first = ROT ? hb0 * 128 : lo, xoff = lo - k_first, XS = span + 8;  // XS: rows in different banks
+    uint16_t* xs = reinterpret_cast<uint16_t*>(lds);
+    uint16_t* suh_s = xs + M * XS;
+    uint32_t* stage = reinterpret_cast<uint32_t*>(lds + (((size_t)(M + 1) * XS * 2 + 15) & ~(size_t)15));
+    float* red = reinterpret_cast<float*>(stage);  // after the products: [WK][16][32]
+    uint32_t* st = stage + wave * NKT * 2 * TW;
+
+    // the activation rows (and suh) first, 16 bytes a load, every load issued (a thread past the end reads the last
+    // chunk again), so the trellis loads that follow stay in flight while these are written to LDS
+    const uint16_t* xsrc = ROT ? static_cast<const uint16_t*>(x) : dptr<const uint16_t>(J.xh);
+    const int cpr = span >> 3, chunks = M * cpr;  // 16-byte chunks a row, in all
+    u4v xv[XL];
+#pragma unroll
+    for (int i = 0; i < XL; ++i) {
+        const int c = min(i * NT + (int)threadIdx.x, chunks - 1), m = c / cpr, cc = c - m * cpr;
+        xv[i] = *reinterpret_cast<const u4v*>(xsrc + (size_t)m * K + k_first + 8 * cc);
+    }
+    u4v sv = u4v{0u, 0u, 0u, 0u};
+    if constexpr (ROT)
+        sv = *reinterpret_cast<const u4v*>(dptr<const uint16_t>(rj.suh[ji]) + k_first +
+                                           8 * min((int)threadIdx.x, cpr - 1));
+
+    // the wave's trellis: NKT rows of its two adjacent column tiles (strips layout)
+    const int nt0 = 2 * g;
+    TileSpan sp;
+    const int64_t tiles_end = (int64_t)((N >> 7) - 1) * J.stride_nb + (int64_t)(K >> 4) * J.stride_k;
+    sp.r = buffer_rsrc(dptr<const uint32_t>(J.T), (uint32_t)(tiles_end * 4));
+    sp.off = (int)((((int64_t)(lo >> 4) + wave * NKT) * J.stride_k + (nt0 >> 3) * J.stride_nb + (nt0 & 7) * TW) * 4);
+    sp.kstride = (int)(J.stride_k * 4);
+    u4v v[stage_loads_k<NKT, K2>()];
+    stage_issue_k<NKT, K2>(sp, lane, v);
+    // the svh and bias of the lane's two columns of the 128-column block, for whichever block finishes it (loaded by
+    // every block, unconditionally: a load in a branch would make the compiler wait for all loads before the first use)
+    const bool finisher = (g & 3) == 3 && split == SK - 1;  // the highest-index block of the 4 SK
+    const int col = (g >> 2) * 128 + 2 * lane;
+    const uint16_t* svh = dptr<const uint16_t>(J.svh);
+    const uint16_t* bias = dptr<const uint16_t>(J.bias);
+    const uint32_t svw = *reinterpret_cast<const uint32_t*>(svh + col);
+    const uint32_t bw = *reinterpret_cast<const uint32_t*>((bias ? bias : svh) + col);
+    issued();
+#pragma unroll
+    for (int i = 0; i < XL; ++i) hold(xv[i]);
+    hold(sv);
+#pragma unroll
+    for (int i = 0; i < XL; ++i) {
+        const int c = i * NT + (int)threadIdx.x;
+        if (c < chunks) {
+            const int m = c / cpr, cc = c - m * cpr;
+            *reinterpret_cast<u4v*>(xs + m * XS + 8 * cc) = xv[i];
+        }
+    }
+    if (ROT && (int)threadIdx.x < cpr) *reinterpret_cast<u4v*>(suh_s + 8 * threadIdx.x) = sv;
+    __syncthreads();
+    if constexpr (ROT) {
+        // rotate in place: a wave a (row, Hadamard block), two values a lane (exl3_linear.cu:152-173)
+        uint16_t* xh = dptr<uint16_t>(rj.xh[ji]);
+        const int nhb = span >> 7;
+        for (int item = wave; item < M * nhb; item += WK) {
+            const int m = item / nhb, hb = item - m * nhb;
+            uint32_t* p = reinterpret_cast<uint32_t*>(xs + m * XS + hb * 128 + 2 * lane);
+            const uint32_t xw = *p, sw = *reinterpret_cast<const uint32_t*>(suh_s + hb * 128 + 2 * lane);
+            const uint16_t x0 = (uint16_t)(xw & 0xffffu), x1 = (uint16_t)(xw >> 16);
+            float v0 = (x_bf16 ? bf2f(x0) : h2f(x0)) * h2f((uint16_t)(sw & 0xffffu));
+            float v1 = (x_bf16 ? bf2f(x1) : h2f(x1)) * h2f((uint16_t)(sw >> 16));
+            fwht128_w64(v0, v1, lane);
+            const uint32_t h = (uint32_t)f2h(v0 * HAD_SCALE) | ((uint32_t)f2h(v1 * HAD_SCALE) << 16);
+            *p = h;
+            if (g == 0 && xh) *reinterpret_cast<uint32_t*>(xh + (size_t)m * K + (hb0 + hb) * 128 + 2 * lane) = h;
+        }
+        __syncthreads();
+    }
+    stage_store_k<NKT, K2>(st, lane, v);
+
+    // the product: A rows are the activation rows (zero past M), B the decoded tiles
+    const LaneQuad lq = lane_quad_k<K2>(lane);
+    const uint32_t* wa = st + lq.w0;
+    const uint32_t* wb = st + lq.w1;
+    const int row = lane & 15;
+    const uint16_t* xr = row < M ? xs + row * XS + xoff + wave * NKT * 16 : nullptr;
+    f4v acc[2] = {f4v{0.f, 0.f, 0.f, 0.f}, f4v{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+    for (int t = 0; t < NKT; t += 2) {
+        const h8v a = load_a8(xr, t * 16, lane);
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int t0 = (2 * t + j) * TW, t1 = (2 * (t + 1) + j) * TW;
+            const u2v b0 = decode_quad<K2, CB>(wa[t0], wb[t0], lq.sh);
+            const u2v b1 = decode_quad<K2, CB>(wa[t1], wb[t1], lq.sh);
+            const h8v bb = __builtin_bit_cast(h8v, (u4v{b0.x, b0.y, b1.x, b1.y}));
+            acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bb, acc[j], 0, 0, 0);
+        }
+    }
+    __syncthreads();  // every wave is done with the staged trellis: the wave sums take its place
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) red[(wave * 16 + 4 * (lane >> 4) + i) * 32 + j * 16 + row] = acc[j][i];
+    __syncthreads();
+    float* Z = dptr<float>(J.Z);
+    for (int idx = threadIdx.x; idx < M * 32; idx += WK * 64) {
+        const int m = idx >> 5, c = idx & 31;
+        float sum = red[m * 32 + c];
+        for (int w = 1; w < WK; ++w) sum += red[(w * 16 + m) * 32 + c];
+        st_coh(Z + ((size_t)split * M + m) * N + g * 32 + c, sum);
+    }
+    stores_done();
+    __syncthreads();
+    __shared__ int last;
+    if (4 * SK <= LS_FLAGS) {
+        // flags: each of the 4 SK blocks of the 128-column block sets its byte in the column block's eight counter
+        // words (zero between calls); the block of highest index among them (the last dispatched) waits for all of
+        // them, then finishes and clears them. Nothing contends for one address.
+        uint8_t* flags = reinterpret_cast<uint8_t*>(dptr<int>(J.counters) + (g >> 2) * (LS_FLAGS / 4));
+        if (threadIdx.x == 0) __hip_atomic_store(flags + (g & 3) + 4 * split, (uint8_t)1, __ATOMIC_RELAXED,
+                                                 __HIP_MEMORY_SCOPE_AGENT);
+        if (!finisher) return;
+        if (threadIdx.x < 64) {
+            const int* fw = reinterpret_cast<const int*>(flags);
+            const int words = SK;  // 4 SK flag bytes
+            int n = 0;
+            bool ready = false;
+            while (!ready) {
+                const int v = lane < words ? ld_coh(fw + lane) : 0x01010101;
+                ready = __builtin_amdgcn_ballot_w64(v != 0x01010101) == 0;
+                if (!ready && ++n > (1 << 20)) break;
+                if (!ready) __builtin_amdgcn_s_sleep(1);
+            }
+            if (lane < words) reset_count(const_cast<int*>(fw) + lane);
+            if (lane == 0) {
+                last = ready ? 1 : 2;
+                if (!ready) record_error(status, DEV_SYNC_TIMEOUT);
+            }
+        }
+        __syncthreads();
+    } else {
+        int* counter = dptr<int>(J.counters) + (g >> 2);
+        if (threadIdx.x == 0) {
+            last = count_in(counter) == 4 * SK - 1;
+            if (last) reset_count(counter);
+        }
+        __syncthreads();
+        if (!last) return;
+    }
+    // the last block of the 128-column block: the splits in order, then finish
+    for (int m = wave; m < M; m += WK) {
+        float2 acc2 = ld_coh2(Z + (size_t)m * N + col);
+        for (int q = 1; q < SK; ++q) {
+            const float2 z = ld_coh2(Z + ((size_t)q * M + m) * N + col);
+            acc2.x += z.x;
+            acc2.y += z.y;
+        }
+        if (last == 2) acc2 = float2{__builtin_nanf(""), __builtin_nanf("")};  // a writer never arrived
+        finish_store_pre(acc2.x, acc2.y, lane, svw, bias != nullptr, bw, dptr<void>(J.y), J.y_dtype,
+                         (size_t)m * N + col);
+    }
+}
+
+// LDS of a small-row block: the activation rows and suh, and the staged trellis (then the wave sums).
+static size_t lin_small_lds(int M, int K2, int NKT, int WK, bool rot) {
+    const int kh = NKT * WK * 16, span = rot ? kh + 256 : kh;
+    const size_t xs = (((size_t)(M + 1) * (span + 8) * 2) + 15) & ~(size_t)15;
+    const size_t stage = (size_t)WK * NKT * 2 * 4 * K2 * 4, red = (size_t)WK * 16 * 32 * 4;
+    return xs + (stage > red ? stage : red);
+}
+
+template <int CB, int K2, bool ROT, int XL>
+static void launch_small_xl(const ea_jobs& jobs, const ea_rot_jobs& rj, int blocks, hipStream_t s, int M, int K, int wk,
+                            int nkt, const void* x, int x_bf16, size_t lds, int* status) {
+#define EA_LS(NKT_)                                                                                              \
+    if (nkt == NKT_) {                                                                                           \
+        lin_small_kernel<CB, K2, NKT_, ROT, XL><<<blocks, wk * 64, lds, s>>>(jobs, rj, M, K, x, x_bf16, status); \
+        return;                                                                                                  \
+    }
+    EA_LS(2) EA_LS(4) EA_LS(6) EA_LS(8) EA_LS(10) EA_LS(12) EA_LS(14) EA_LS(16)
+#undef EA_LS
+}
+
+template <int CB, int K2, bool ROT>
+static bool launch_small_k2(const ea_jobs& jobs, const ea_rot_jobs& rj, int blocks, hipStream_t s, int M, int K,
+                            int wk, int nkt, const void* x, int x_bf16, int* status) {
+    const size_t lds = lin_small_lds(M, K2, nkt, wk, ROT);
+    if (lds > 64 * 1024) return false;
+    // 16-byte activation loads a thread: the rows' span over the block's threads
+    const int kh = nkt * wk * 16, span_max = ROT ? kh + 256 : kh;
+    const int xl = (M * (span_max / 8) + wk * 64 - 1) / (wk * 64);
+    if (xl <= 1) launch_small_xl<CB, K2, ROT, 1>(jobs, rj, blocks, s, M, K, wk, nkt, x, x_bf16, lds, status);
+    else if (xl <= 2) launch_small_xl<CB, K2, ROT, 2>(jobs, rj, blocks, s, M, K, wk, nkt, x, x_bf16, lds, status);
+    else if (xl <= 4) launch_small_xl<CB, K2, ROT, 4>(jobs, rj, blocks, s, M, K, wk, nkt, x, x_bf16, lds, status);
+    else if (xl <= 8) launch_small_xl<CB, K2, ROT, 8>(jobs, rj, blocks, s, M, K, wk, nkt, x, x_bf16, lds, status);
+    else return false;
+    return true;
+}
+
+// The small-row kernel when it applies (m <= 16, every job split (SK > 1) with the same even per-wave tile count up to
+// 16, a width the staged decode takes, 16-bit activations when rotating); false otherwise, and nothing is launched.
+static bool launch_small(const ea_jobs& jobs, const ea_rot_jobs* rj, hipStream_t s, int M, int K, uint32_t k2,
+                         uint32_t cb, int wk, const void* x, int x_dtype, int* status) {
+    if (M > LS_MAXR || k2 > (uint32_t)STAGE_MAXK2) return false;
+    if (rj && x_dtype != F16 && x_dtype != BF16) return false;
+    const uintptr_t align = rj ? reinterpret_cast<uintptr_t>(x) | (uintptr_t)K * 2 : (uintptr_t)K * 2;
+    if (align & 15) return false;  // 16-byte activation loads
+    const int nkt = (K >> 4) / jobs.j[0].SK / wk;
+    for (int i = 0; i < jobs.n; ++i) {
+        const ea_job& j = jobs.j[i];
+        if (j.SK < 2 || (K >> 4) % (j.SK * wk) != 0 || (K >> 4) / j.SK / wk != nkt) return false;
+        if (!rj && (!j.xh || (j.xh & 15))) return false;
+        if (rj && ((rj->suh[i] & 15) || (rj->xh[i] & 3))) return false;
+    }
+    if (nkt < 2 || nkt > LS_MAXNKT || (nkt & 1)) return false;
+    // the small-row grid: 32-column groups x splits of every job
+    ea_jobs sj = jobs;
+    int nb = 0;
+    for (int i = 0; i < sj.n; ++i) {
+        sj.j[i].start = nb;
+        nb += (sj.j[i].N >> 5) * sj.j[i].SK;
+    }
+    const ea_rot_jobs r = rj ? *rj : ea_rot_jobs{};
+    const int bf = x_dtype == BF16;
+#define EA_SV(K2_, CB_)                                                                                        \
+    if (k2 == K2_ && cb == CB_)                                                                                \
+        return rj ? launch_small_k2<CB_, K2_, true>(sj, r, nb, s, M, K, wk, nkt, x, bf, status)                \
+                  : launch_small_k2<CB_, K2_, false>(sj, r, nb, s, M, K, wk, nkt, x, bf, status);
+    EA_SV(10, 2) EA_SV(8, 1) EA_SV(8, 2) EA_SV(6, 1) EA_SV(4, 1)
+#undef EA_SV
+    return false;
+}
+
 // the (K2, codebook) pairs this build instantiates: the reference's four (exl3.zig:40) and 3 / 4 bits mcg
 template <int CB, int K2>
 static void launch_wk(const ea_jobs& jobs, int blocks, hipStream_t s, int M, int K, int wk) {
@@ -161,8 +432,11 @@ int launch_lin_rot_in(hipStream_t s, const void* x, int x_dtype, const ea_rot_jo
     return launched();
 }
 
+// One linear launch over 1..3 jobs. rot: the jobs' rotation (suh, xh) when x is the unrotated input; then the
+// small-row kernel rotates in-kernel, and otherwise a rotation launch runs first.
 int launch_linear(hipStream_t s, const ea_jobs* jobs_in, uint32_t m, uint32_t kdim, uint32_t k2, uint32_t cb,
-                  uint32_t wk, uint32_t loads) {
+                  uint32_t wk, uint32_t loads, const ea_rot_jobs* rot = nullptr, const void* x = nullptr,
+                  int x_dtype = 0) {
     EA_REQUIRE_CTX(c);
     if (!jobs_in || jobs_in->n < 1 || jobs_in->n > EA_MAX_JOBS) return EA_BAD_ARGUMENT;
     // only the load walk with bits 1 and 2 set is built (exl3.zig:96-98)
@@ -180,6 +454,11 @@ int launch_linear(hipStream_t s, const ea_jobs* jobs_in, uint32_t m, uint32_t kd
     if (!variant_built(k2, cb, wk)) return EA_UNPORTED_LINEAR_VARIANT;
     if (m == 0 || blocks == 0) return EA_OK;
     if (m > 128) return EA_NOT_GROUPABLE;
+    if (launch_small(jobs, rot, s, (int)m, (int)kdim, k2, cb, (int)wk, x, x_dtype, c->status)) return launched();
+    if (rot) {
+        const int r = launch_lin_rot_in(s, x, x_dtype, rot, (uint32_t)jobs.n, m, kdim);
+        if (r) return r;
+    }
     launch_variant(jobs, blocks, s, (int)m, (int)kdim, k2, cb, (int)wk);
     return launched();
 }
@@ -228,8 +507,11 @@ static bool groupable(const ea_linear* const* ls, uint32_t n) {
 // the kernels' load options the engine uses: bits 1 and 2 (linear.zig:293-295; PDL has no counterpart here)
 static const uint32_t LOADS = 3;
 
-int ea_linear_call_rotated(ea_stream_t stream, const ea_linear_scratch* s, const ea_linear* const* ls, uint32_t nls,
-                           uint32_t m, const uint64_t* outs, const int* out_dtypes) {
+// linear.call / callRotated: jobs over the layers; rot and x given for call (the rotation then happens in the
+// launch or just before it).
+static int linear_call_jobs(hipStream_t stream, const ea_linear_scratch* s, const ea_linear* const* ls, uint32_t nls,
+                            uint32_t m, const uint64_t* outs, const int* out_dtypes, const ea_rot_jobs* rot,
+                            const void* x, int x_dtype) {
     if (!groupable(ls, nls) || m < 1 || m > 128) return EA_NOT_GROUPABLE;
     if (!s || !outs || !out_dtypes) return EA_BAD_ARGUMENT;
     ea_jobs jobs{};
@@ -251,21 +533,26 @@ int ea_linear_call_rotated(ea_stream_t stream, const ea_linear_scratch* s, const
         j.N = (int32_t)l->n;
         j.SK = (int32_t)l->sk;
     }
-    return launch_linear(as_stream(stream), &jobs, m, ls[0]->k, ls[0]->k2, ls[0]->cb, ls[0]->wk, LOADS);
+    return launch_linear(stream, &jobs, m, ls[0]->k, ls[0]->k2, ls[0]->cb, ls[0]->wk, LOADS, rot, x, x_dtype);
+}
+
+int ea_linear_call_rotated(ea_stream_t stream, const ea_linear_scratch* s, const ea_linear* const* ls, uint32_t nls,
+                           uint32_t m, const uint64_t* outs, const int* out_dtypes) {
+    return linear_call_jobs(as_stream(stream), s, ls, nls, m, outs, out_dtypes, nullptr, nullptr, 0);
 }
 
 int ea_linear_call(ea_stream_t stream, const ea_linear_scratch* s, const ea_linear* const* ls, uint32_t nls,
                    const void* x, int x_dtype, uint32_t m, const uint64_t* outs, const int* out_dtypes) {
     if (!groupable(ls, nls) || m < 1 || m > 128) return EA_NOT_GROUPABLE;
     if (!s) return EA_BAD_ARGUMENT;
+    if (ls[0]->k % 128 != 0) return EA_BAD_ROT_IN;
+    if (!x || x_dtype < 0 || x_dtype > 2) return EA_BAD_ARGUMENT;
     ea_rot_jobs rj{};
     for (uint32_t i = 0; i < nls; ++i) {
         rj.suh[i] = ls[i]->suh;
         rj.xh[i] = s->xh[i];
     }
-    int r = launch_lin_rot_in(as_stream(stream), x, x_dtype, &rj, nls, m, ls[0]->k);
-    if (r) return r;
-    return ea_linear_call_rotated(stream, s, ls, nls, m, outs, out_dtypes);
+    return linear_call_jobs(as_stream(stream), s, ls, nls, m, outs, out_dtypes, &rj, x, x_dtype);
 }
 
 }  // extern "C"

@@ -46,6 +46,9 @@ def test_unpack_bit_exact(ea, k2, cb):
     (16, 6144, 256, 10, 2, 2),   # 5-bit mul1 (the real checkpoints' shared expert), 16 rows
     (40, 1024, 640, 8, 2, 0),    # three row passes, fp16 out
     (128, 512, 384, 6, 1, 2),    # the most rows a call takes
+    (4, 6144, 2048, 8, 1, 2),    # config 1's shape at four rows (the small-row kernel: 32-column groups x 8 splits)
+    (7, 2048, 512, 6, 1, 0),     # 3 bits, fp16 out, a ragged row count
+    (2, 1024, 384, 4, 1, 2),     # 2 bits
 ])
 def test_linear_call(ea, M, K, N, k2, cb, y_dtype):
     device, linear, _, _, synth = ea
@@ -70,6 +73,27 @@ def test_linear_call(ea, M, K, N, k2, cb, y_dtype):
             bound = eps * np.abs(y_w) + 1e-4 * np.sqrt(np.mean(y_w.astype(np.float64) ** 2))
             assert np.all(np.abs(got - y_w) <= bound), f"linear M={M}: rounded output off"
         assert int(device.download(lin.counters).sum()) == 0
+
+
+def test_linear_call_rotated_matches_call(ea):
+    """callRotated on the xh a call leaves in the scratch (the small-row kernel reads it instead of rotating) gives
+    the call's result bit for bit; fp16 and bf16 inputs."""
+    device, linear, _, _, synth = ea
+    M, K, N, k2 = 3, 6144, 2048, 8
+    T, suh, svh, x = _case(synth, M, K, N, k2, 90)
+    lin = linear.Linear(T, suh, svh, K, N, k2, 1)
+    sc = linear.Scratch(M, K, lin.sk * M * N)
+    for x_dtype in (0, 1):
+        xb = synth.activations(91 + x_dtype, M, K, ["f16", "bf16"][x_dtype])
+        dx = device.upload(xb)
+        y1, y2 = device.zeros((M, N), torch.float32), device.zeros((M, N), torch.float32)
+        linear.call(device.stream(), sc, [lin], dx.data_ptr(), x_dtype, M, [y1.data_ptr()], [2])
+        np.testing.assert_array_equal(device.download(sc.xh[0][: M * K].view(torch.int16)).reshape(M, K),
+                                      orc.exl3_rot_in(xb, suh, M, K, bf16=x_dtype == 1))
+        linear.call_rotated(device.stream(), sc, [lin], M, [y2.data_ptr()], [2])
+        np.testing.assert_array_equal(device.download(y1), device.download(y2))
+        assert int(device.download(lin.counters).sum()) == 0
+    assert device.device_status() == 0
 
 
 def test_linear_three_jobs_one_launch(ea):
