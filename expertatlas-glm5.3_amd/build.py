@@ -1,5 +1,5 @@
 """Builds libea_exl3.so (the C ABI of include/ea_exl3.h) for gfx950 with hipcc, in-tree next to the ea_exl3
-package. Every .hip file under csrc/ compiles to its own object in parallel, then one link.
+package. Every .hip (device) and .cpp (host) file under csrc/ compiles to its own object in parallel, then one link.
 
     python expertatlas-glm5.3_amd/build.py [--jobs N]
 """
@@ -18,6 +18,8 @@ CSRC = os.path.join(HERE, "csrc")
 OUT = os.path.join(HERE, "ea_exl3", "libea_exl3.so")
 OBJ = os.path.join(HERE, "_build")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+CXX = os.environ.get("CXX", "g++")
+ROCM_INC = "/opt/rocm/include"
 
 FLAGS = [
     "-O3", "--offload-arch=gfx950", "-fPIC", "-std=c++17",
@@ -30,8 +32,11 @@ FLAGS = [
 
 
 def _compile(src: str) -> str:
-    obj = os.path.join(OBJ, os.path.basename(src).replace(".hip", ".o"))
-    cmd = [HIPCC, *FLAGS, "-c", src, "-o", obj]
+    obj = os.path.join(OBJ, os.path.splitext(os.path.basename(src))[0] + ".o")
+    # .hip: device code for gfx950; .cpp: host-only C++ (the bank reader) against the HIP runtime
+    cmd = [HIPCC, *FLAGS, "-c", src, "-o", obj] if src.endswith(".hip") else \
+        [CXX, "-O2", "-fPIC", "-std=c++17", "-Wall", "-D__HIP_PLATFORM_AMD__", "-I" + ROCM_INC,
+         "-I" + os.path.join(ROOT, "include"), "-I" + CSRC, "-c", src, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         sys.stderr.write(r.stdout + r.stderr)
@@ -41,7 +46,7 @@ def _compile(src: str) -> str:
 
 def build(jobs: int | None = None) -> str:
     os.makedirs(OBJ, exist_ok=True)
-    srcs = sorted(glob.glob(os.path.join(CSRC, "*.hip")))
+    srcs = sorted(glob.glob(os.path.join(CSRC, "*.hip")) + glob.glob(os.path.join(CSRC, "*.cpp")))
     jobs = jobs or min(8, len(srcs), os.cpu_count() or 1)
     with cf.ThreadPoolExecutor(jobs) as ex:
         objs = list(ex.map(_compile, srcs))

@@ -149,6 +149,23 @@ const char* ea_strerror(int s) {
         case EA_BAD_ARGUMENT: return "bad argument";
         case EA_UNSUPPORTED_WIDTH: return "an expert width (K2) or codebook this build has no decoder for";
         case EA_SYNC_TIMEOUT: return "a kernel's bounded wait on its block's LDS counters gave up";
+        case EA_BANK_IO: return "a bank or checkpoint file could not be opened or mapped";
+        case EA_BAD_SAFETENSORS: return "BadSafetensors: a safetensors header breaks the format";
+        case EA_BAD_INDEX: return "BadIndex: model.safetensors.index.json has no weight_map of file names";
+        case EA_MISSING_TENSOR: return "MissingTensor: the checkpoint does not hold this tensor (or a stored rank of it)";
+        case EA_NO_SPLIT_RULE: return "NoSplitRule: no tensor-parallel split rule for this tensor name";
+        case EA_STRADDLES_HADAMARD: return "StraddlesHadamard: a rank's share would cut a 128-value Hadamard block";
+        case EA_STORED_WORLD_NOT_MULTIPLE: return "StoredWorldNotMultiple: stored ranks must be a multiple of the ranks";
+        case EA_TOO_MANY_STORED_RANKS: return "TooManyStoredRanks: at most 16 stored ranks joined into one share";
+        case EA_STORED_SHARES_DIFFER: return "StoredSharesDiffer: the stored ranks of one tensor differ in dtype or shape";
+        case EA_BAD_TRELLIS: return "BadTrellis: a trellis must be i16 [K/16, N/16, 8 K2] of the layer's shape";
+        case EA_PACKED_SCALES: return "PackedScalesUnsupported: suh / svh must be fp16 of the layer's shape";
+        case EA_MIXED_CODEBOOKS: return "MixedCodebooks: an expert's codebook differs from expert 0's";
+        case EA_SWAP_CODEBOOK_DIFFERS: return "SwapCodebookDiffers: the bank's codebook differs from the layer's";
+        case EA_SWAP_BAD_TRELLIS: return "SwapBadTrellis: the bank's trellis is not of the layer's shape and width";
+        case EA_SWAP_BAD_SCALES: return "SwapBadScales: the bank's scales are not of the layer's shape";
+        case EA_SWAP_WIDTH_UNSUPPORTED: return "SwapWidthUnsupported: widths of 2 to 8 bits";
+        case EA_SWAP_NO_BANK: return "SwapNoBank: no bank for a width the change asks for";
         default: return "unknown status";
     }
 }

@@ -66,6 +66,14 @@ class LinearScratch(C.Structure):
     _fields_ = [("xh", U64 * MAX_JOBS), ("z", U64 * MAX_JOBS)]
 
 
+class ShareInfo(C.Structure):
+    _fields_ = [("dtype", I32), ("rank", U32), ("shape", U64 * 8), ("bytes", U64)]
+
+
+class SwapStats(C.Structure):
+    _fields_ = [("experts", U32), ("up", U32), ("down", U32), ("read_bytes", U64)]
+
+
 assert C.sizeof(Job) == 88 and C.sizeof(Jobs) == 272 and C.sizeof(RotJobs) == 48  # exl3.zig:30-32
 
 # name -> (restype, argtypes); every entry point of include/ea_exl3.h
@@ -101,6 +109,15 @@ SIGNATURES = {
     "ea_router": (I32, [P, P, I32, U32, P, P, P, U32, U32, U32]),
     "ea_swiglu2": (I32, [P, P, P, P, U32, U32]),
     "ea_add_f32": (I32, [P, P, P, C.c_size_t]),
+    "ea_bank_open": (I32, [C.c_char_p, U32, U32, U32, C.POINTER(P)]),
+    "ea_bank_open_file": (I32, [C.c_char_p, C.c_char_p, U32, U32, U32, C.POINTER(P)]),
+    "ea_bank_close": (None, [P]),
+    "ea_bank_has": (I32, [P, C.c_char_p]),
+    "ea_bank_share": (I32, [P, C.c_char_p, C.POINTER(ShareInfo), P, U64]),
+    "ea_layer_load": (I32, [C.POINTER(P), U32, P, U32, U32, C.POINTER(P)]),
+    "ea_layer_routed": (C.POINTER(Routed), [P]),
+    "ea_layer_free": (None, [P]),
+    "ea_layer_swap": (I32, [P, C.POINTER(P), U32, P, P, C.POINTER(SwapStats)]),
     "ea_profile_enable": (I32, [I32]),
     "ea_profile_stages": (I32, [P, U32]),
     "ea_ffn_moe_decode": (I32, [P, P, I32, U32, P, P, F32, P, P, C.POINTER(Routed), P, C.POINTER(MoeScratch), P, U32]),

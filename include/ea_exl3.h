@@ -45,7 +45,25 @@ typedef enum ea_status {
     EA_NOT_INITIALIZED = 17,          /* a call before ea_init on this device */
     EA_BAD_ARGUMENT = 18,             /* a null pointer or a size outside the documented range */
     EA_UNSUPPORTED_WIDTH = 19,        /* a K2 / codebook this build has no decoder for */
-    EA_SYNC_TIMEOUT = 20              /* a kernel's bounded wait on its block's LDS counters gave up */
+    EA_SYNC_TIMEOUT = 20,             /* a kernel's bounded wait on its block's LDS counters gave up */
+    /* expert banks (weights.zig, split.zig, moe.zig, expert_swap.zig) */
+    EA_BANK_IO = 21,                  /* a file could not be opened or mapped (std.fs errors) */
+    EA_BAD_SAFETENSORS = 22,          /* core/safetensors.zig error.BadSafetensors / UnsupportedDType / RankTooHigh */
+    EA_BAD_INDEX = 23,                /* weights.zig:49 error.BadIndex */
+    EA_MISSING_TENSOR = 24,           /* weights.zig:187 error.MissingTensor */
+    EA_NO_SPLIT_RULE = 25,            /* split.zig:58 error.NoSplitRule */
+    EA_STRADDLES_HADAMARD = 26,       /* split.zig:69,71 error.StraddlesHadamard (UnevenSplit is EA_UNEVEN_SPLIT) */
+    EA_STORED_WORLD_NOT_MULTIPLE = 27,/* weights.zig:41 error.StoredWorldNotMultiple */
+    EA_TOO_MANY_STORED_RANKS = 28,    /* weights.zig:149,220 error.TooManyStoredRanks */
+    EA_STORED_SHARES_DIFFER = 29,     /* weights.zig:155 error.StoredSharesDiffer */
+    EA_BAD_TRELLIS = 30,              /* moe.zig:110 error.BadTrellis */
+    EA_PACKED_SCALES = 31,            /* moe.zig:92 error.PackedScalesUnsupported */
+    EA_MIXED_CODEBOOKS = 32,          /* moe.zig:146 error.MixedCodebooks */
+    EA_SWAP_CODEBOOK_DIFFERS = 33,    /* expert_swap.zig:335,364 error.SwapCodebookDiffers */
+    EA_SWAP_BAD_TRELLIS = 34,         /* expert_swap.zig:383 error.SwapBadTrellis */
+    EA_SWAP_BAD_SCALES = 35,          /* expert_swap.zig:384 error.SwapBadScales */
+    EA_SWAP_WIDTH_UNSUPPORTED = 36,   /* expert_swap.zig:88 error.SwapWidthUnsupported */
+    EA_SWAP_NO_BANK = 37              /* expert_swap.zig:89 error.SwapNoBank */
 } ea_status;
 
 enum { EA_F16 = 0, EA_BF16 = 1, EA_F32 = 2 };
@@ -280,6 +298,61 @@ int ea_ffn_moe_decode_router(ea_stream_t stream, const void* x, int x_dtype, uin
 int ea_ffn_moe_decode_static(ea_stream_t stream, const void* x, int x_dtype, uint32_t x_stride, const float* logits,
                              const float* bias, float scale, int32_t* pick, float* wts, const ea_routed* ex,
                              const ea_linear* const* shared, float* out, uint32_t R);
+
+/* ---- expert banks: a rank's shard of a checkpoint, loading a layer, changing experts' widths ------------------ */
+
+/* weights.Reader (weights.zig:20-240): a checkpoint or bank directory read for tensor-parallel rank `rank` of `world`.
+ * Whole tensors are cut to the rank's share by the split rules (split.zig:18-81: output-split projections cut the
+ * trellis' second axis and svh, input-split ones the trellis' first axis and suh; markers and the other scale whole;
+ * shares never straddle a 128-value Hadamard block); pre-sharded tensors ("...P_proj.rank{s}.S", assemble.py:173-237)
+ * from stored_world ranks are joined stored_world / world at a time. Host-side only (no GPU). */
+typedef struct ea_bank ea_bank;
+/* weights.zig:41-51 Reader.open: dir/model.safetensors.index.json ("weight_map": name -> file). */
+int ea_bank_open(const char* dir, uint32_t rank, uint32_t world, uint32_t stored_world, ea_bank** out);
+/* weights.zig:52-61 Reader.openFile: one safetensors file of dir, every tensor it holds. */
+int ea_bank_open_file(const char* dir, const char* fname, uint32_t rank, uint32_t world, uint32_t stored_world,
+                      ea_bank** out);
+void ea_bank_close(ea_bank* b);
+/* weights.zig:196-202 Reader.has: the tensor is there, whole or as stored ranks (1 / 0). */
+int ea_bank_has(const ea_bank* b, const char* name);
+/* A share's dtype (0 BOOL 1 U8 2 I8 3 U16 4 I16 5 F16 6 BF16 7 U32 8 I32 9 F32 10 U64 11 I64 12 F64), rank, shape (1
+ * past rank) and byte count. */
+typedef struct ea_share_info {
+    int32_t dtype;
+    uint32_t rank;
+    uint64_t shape[8];
+    uint64_t bytes;
+} ea_share_info;
+/* weights.zig:204-225 Reader.get: this rank's share of `name` into host memory dst (cap bytes; dst NULL: info only). */
+int ea_bank_share(ea_bank* b, const char* name, ea_share_info* info, void* dst, uint64_t cap);
+
+/* One MoE layer's routed experts on the current device, loaded from banks: moe.loadFrom (moe.zig:65-151). Every
+ * expert's gate / up / down trellis shares ("model.layers.L.mlp.experts.e.{gate,up,down}_proj.trellis", i16
+ * [K/16, N/16, 8 K2]) back to back in one slab a projection, each 256-byte aligned; int64 pointer and int32 width
+ * tables; fp16 suh / svh stacked [E, K] / [E, N]; the codebook from expert 0's gate marker (.mcg 1, .mul1 2, none 0).
+ * readers: one per bank; pick (E bytes) names each expert's reader, or NULL for readers[0] (then nreaders >= 1);
+ * with a pick, every expert's markers must agree (EA_MIXED_CODEBOOKS). The layer owns its device memory. Set-up call:
+ * allocates and copies synchronously. */
+typedef struct ea_layer ea_layer;
+int ea_layer_load(ea_bank* const* readers, uint32_t nreaders, const uint8_t* pick, uint32_t layer, uint32_t experts,
+                  ea_layer** out);
+/* The layer's ea_routed (its device tables and scales), valid until ea_layer_free. */
+const ea_routed* ea_layer_routed(const ea_layer* l);
+void ea_layer_free(ea_layer* l);
+/* Experts changed (expert_swap.zig swapLayer). */
+typedef struct ea_swap_stats {
+    uint32_t experts, up, down;
+    uint64_t read_bytes;
+} ea_swap_stats;
+/* Change experts' widths between calls (expert_swap.zig:345-467): expert j goes from current[j] to target[j] bits,
+ * read from banks[target[j]] (banks: 9 readers indexed by bits, NULL where none; the reference opens
+ * "experts-layer-NNN.safetensors" of each width's bank dir: expert_swap.zig:301-308). New slabs are made (unchanged
+ * experts copied on the device, changed ones uploaded), the changed experts' scales overwritten, and the ptr / k2 tables
+ * rewritten in place: a captured graph holds the tables' addresses, so its replays run the new widths. The K2 ranges
+ * of the ea_routed only widen. A failure before the device is written leaves the layer as it was. Synchronous; no
+ * kernel may use the layer meanwhile. */
+int ea_layer_swap(ea_layer* l, ea_bank* const* banks, uint32_t layer, const uint8_t* target, const uint8_t* current,
+                  ea_swap_stats* st);
 
 /* ---- benchmark instrumentation (no counterpart in the reference) ------------------------------------------- */
 
