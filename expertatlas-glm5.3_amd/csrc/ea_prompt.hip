@@ -19,13 +19,15 @@ namespace ea {
 // this library's for the register-streaming GEMM of widths above 10 (IPM_WIDE); the staged GEMMs (widths 2..10) take
 // items of up to 48 (three row tiles), which measured 6 % faster at 512 rows and the same at 2048: more blocks of
 // shorter MFMA chains and fewer accumulators, for more decoding of the experts split into several items. A pair's
-// sums do not depend on its item. (An item cap of 48 on the register-streaming path gave wrong results in
-// test_prompt_experts_run[120-32-256-128-12], whose most picked expert then has three items; the cause is not found,
-// so that path keeps the cap it was tested with.)
+// sums do not depend on its item. The register-streaming GEMM is built for 7 row tiles only: routing into items of
+// at most 48 pairs is right with it (checked with that kernel at widths above 10), but the same kernel built for 3
+// row tiles gave wrong sums at width 12 (no register spills, the same index arithmetic, extra wait states after the
+// decoder's fp16 adds changed nothing); that instantiation is not built.
 constexpr int IPM = 48;
 constexpr int IPM_TILES = IPM / 16;
 constexpr int IPM_WIDE = 112;
 constexpr int IPM_WIDE_TILES = IPM_WIDE / 16;
+static_assert(IPM_WIDE_TILES == 7, "the register-streaming item GEMM is verified for 7 row tiles only");
 constexpr uint32_t CHUNK_ROWS = 4096;  // rows a pass at most (prompt_experts.zig:17)
 constexpr int ROUTE_THREADS = 1024;
 

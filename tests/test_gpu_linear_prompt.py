@@ -156,10 +156,17 @@ def _prompt_case(ea, R, E, D, I, k2, seed, x_dtype=1, zipf=True, cb=1):
 
 
 @pytest.mark.parametrize("R,E,D,I,k2", [(130, 64, 512, 256, 8), (300, 256, 1024, 256, "mixed"), (40, 32, 256, 128, 6),
-                                        (120, 32, 256, 128, 12), (300, 32, 256, 128, 12), (300, 32, 256, 128, 8)])
+                                        (120, 32, 256, 128, 12), (300, 32, 256, 128, 12), (300, 32, 256, 128, 8),
+                                        # widths above 10 take the register-streaming GEMM with items of up to 112
+                                        # pairs; Zipf over 32 experts gives the top experts ~300 pairs: three items
+                                        (300, 32, 256, 128, 11), (300, 32, 256, 128, 14), (300, 32, 256, 128, 16),
+                                        (260, 32, 512, 256, "wide-mixed")])
 def test_prompt_experts_run(ea, R, E, D, I, k2):
     device, _, _, pe, synth = ea
-    k2v = synth.mixed_widths(5, E) if k2 == "mixed" else k2
+    if k2 == "wide-mixed":  # every width class on the register-streaming path at once
+        k2v = np.array([(12, 8, 6, 16, 10, 11, 4, 14)[e % 8] for e in range(E)], np.int32)
+    else:
+        k2v = synth.mixed_widths(5, E) if k2 == "mixed" else k2
     host, ex, sc, x, pick, wts, dx, dp, dw = _prompt_case(ea, R, E, D, I, k2v, 100 + R)
     want = orc.prompt_experts(x, pick, wts, oracle_routed(host), R, 8, bf16=True)
     out = device.zeros((R, D), torch.float32)
