@@ -322,10 +322,23 @@ def copy_calibration(torch) -> None:
 
 # ---- the CPU baseline -------------------------------------------------------------------------------------------------
 
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline_decode(seed: int, R: int = 1, mixed: bool = False, budget_s: float = 12.0, layers_per_unit: int = 1,
                         unit: str = "us/layer") -> dict:
-    """The C oracle (OpenMP) on the host cores on the decode layer's work: R rows, 8 routed experts a row (fresh
-    routing per layer) and the shared expert. A bounded sample: whole layers until `budget_s` seconds have passed."""
+    """The tuned CPU layer (oracle/libcpulayer.so: -O3, x86-64-v3, OpenMP over every column tile of every product) on
+    the decode layer's work: R rows, 8 routed experts a row (fresh routing per layer) and the shared expert, here a
+    ninth expert of every row with weight 1 (the same bytes and products; routed-expert arithmetic). A bounded sample:
+    whole layers until `budget_s` seconds have passed."""
     import numpy as np
 
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
@@ -334,46 +347,34 @@ def cpu_baseline_decode(seed: int, R: int = 1, mixed: bool = False, budget_s: fl
 
     rng = np.random.default_rng(seed)
     x = synth.activations(seed, R, D, "f16")
-    shapes = ((D, I), (D, I), (I, D))
-    sh = [synth.trellis(seed, 99, m, 0, k, n, 8) for m, (k, n) in enumerate(shapes)]
-    sh_s = [orc.expert_to_strips(sh[m], k, n, 8) for m, (k, n) in enumerate(shapes)]
-    suh = [synth.scales(seed + m, k, 1.0) for m, k in enumerate((D, D, I))]
-    svh = [synth.scales(seed + 10 + m, n, 0.02) for m, n in enumerate((I, I, D))]
-    tw = 32
-    k2 = synth.mixed_widths(seed, E) if mixed else 8
+    k2 = synth.mixed_widths(seed, E) if mixed else np.full(E, 8, np.int32)
+    k2 = np.concatenate([k2, [8]]).astype(np.int32)  # the shared expert: expert E, 4 bits
 
-    def run(pick, wts, host):
-        r = _oracle_routed(orc, host)
-        out = orc.moe_routed(x, pick, wts, r, R, SLOTS)
-        xh = [orc.exl3_rot_in(x, suh[m], R, D) for m in (0, 1)]
-        sk, wk = orc.linear_plan(D, I)
-        g = orc.exl3_linear(xh[0], sh_s[0], 8 * tw, (D // 16) * 8 * tw, svh[0], R, D, I, 8, 1, sk, wk, y_dtype=1)
-        u = orc.exl3_linear(xh[1], sh_s[1], 8 * tw, (D // 16) * 8 * tw, svh[1], R, D, I, 8, 1, sk, wk, y_dtype=1)
-        act = orc.swiglu2(g, u)
-        xd = orc.exl3_rot_in(act, suh[2], R, I, bf16=True)
-        sk, wk = orc.linear_plan(I, D)
-        sy = orc.exl3_linear(xd, sh_s[2], 8 * tw, (I // 16) * 8 * tw, svh[2], R, I, D, 8, 1, sk, wk)
-        return out + sy
-
-    # host data built outside the clock; one warm-up layer, then whole layers
+    # host data built outside the clock
     cases = []
     for i in range(3):
-        pick = np.stack([np.sort(rng.choice(E, SLOTS, replace=False)) for _ in range(R)]).astype(np.int32)
-        cases.append((pick, synth.routing_weights(seed + i, R, SLOTS),
-                      synth.HostLayer(seed + i, experts=E, dims=D, width=I, k2=k2, only=np.unique(pick))))
-    run(*cases[0])
+        pick = np.stack([np.concatenate([np.sort(rng.choice(E, SLOTS, replace=False)), [E]]) for _ in range(R)])
+        wts = np.concatenate([synth.routing_weights(seed + i, R, SLOTS), np.ones((R, 1), np.float32)], axis=1)
+        host = synth.HostLayer(seed + i, experts=E + 1, dims=D, width=I, k2=k2, only=np.unique(pick))
+        cases.append((pick.astype(np.int32), wts.astype(np.float32), _oracle_routed(orc, host)))
+
+    def run(case):
+        pick, wts, r = case
+        return orc.cpu_moe_routed(x, pick, wts, r, R, SLOTS + 1)
+
+    run(cases[0])
     n, t_total = 0, 0.0
-    while t_total < budget_s and n < 40:
-        case = cases[n % len(cases)]
+    while t_total < budget_s and n < 400:
         t0 = time.perf_counter()
-        run(*case)
+        run(cases[n % len(cases)])
         t_total += time.perf_counter() - t0
         n += 1
     threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
     per_layer = t_total / n * 1e6
     bits = "3/4-bit mixed" if mixed else "4-bit"
     sample = (f"{n} layers of {R} row(s) (8 routed {bits} experts a row + a 4-bit shared expert, D 6144, I 256) "
-              f"through the C oracle with OpenMP, {threads} threads")
+              f"through the tuned CPU layer (oracle/cpu_layer.c: -O3 x86-64-v3, tiles decoded into the products, "
+              f"OpenMP over column tiles), {threads} threads on {cpu_model()}")
     if layers_per_unit > 1:
         sample += f"; the per-layer time x {layers_per_unit} layers"
     return {"value": round(per_layer * layers_per_unit, 1), "unit": unit, "cores": threads, "kind": "port",

@@ -271,6 +271,25 @@ def moe_routed(x, pick, wts, routed: Routed, R, slots, x_stride=None, bf16=False
     return out
 
 
+_cpu = None
+
+
+def cpu_moe_routed(x, pick, wts, routed: Routed, R, slots, x_stride=None, bf16=False):
+    """The tuned CPU baseline (libcpulayer.so, cpu_layer.c) of moe_routed: the same function, decoded straight into
+    the products, OpenMP over column tiles; fp32 sums in a different order than the oracle's."""
+    global _cpu
+    if _cpu is None:
+        L = C.CDLL(os.path.join(os.path.dirname(os.path.abspath(__file__)), "libcpulayer.so"))
+        L.cpu_moe_routed.restype = None
+        L.cpu_moe_routed.argtypes = [P, I, I, P, P, P, I, I, P]
+        _cpu = L
+    x = np.ascontiguousarray(x)
+    out = np.zeros((R, routed.dims), np.float32)
+    _cpu.cpu_moe_routed(_p(x), _x_dtype(x, bf16), x_stride or routed.dims, _p(np.ascontiguousarray(pick, np.int32)),
+                        _p(np.ascontiguousarray(wts, np.float32)), routed.ref(), R, slots, _p(out))
+    return out
+
+
 def route(pick, n, E, ipm, max_items):
     pick = np.ascontiguousarray(pick, dtype=np.int32)
     sorted_ = np.zeros(max(n, 1), np.int32)
