@@ -1,0 +1,137 @@
+"""GPU parity on quantized realistic weights instead of random trellis words: every matrix is drawn N(0, 0.02) in bf16,
+as BASELINE's configs draw them, and quantized to EXL3 tiles (4-bit mcg, random-sign Hadamard on both sides) by this
+build's encoder (ea_exl3/encode.py, pinned to the oracle's decode on the CPU). On those weights:
+
+  - the one-launch decode layer at one row, routed from logits (config 2's path at a reduced D and I): picks and
+    weights bit for bit, out within 2e-3 RMS of the oracle's fp32-accumulated decode path;
+  - the prefill path (prompt_experts.run) over 64 rows whose top-8 of 8 experts picks them all (items of 48 and 16
+    pairs): within 2e-3 RMS of the oracle;
+  - both within the quantization's distance (relative RMS < 0.3) of the same layer computed in fp64 from the
+    unquantized bf16 weights: the format carries realistic weights through the whole path."""
+import numpy as np
+import pytest
+
+import oracle as orc
+from helpers import assert_close_rms, oracle_routed
+
+pytestmark = pytest.mark.gpu
+torch = pytest.importorskip("torch")
+
+D, I, K2, CB = 512, 128, 8, 1
+
+
+@pytest.fixture(scope="module")
+def ea():
+    from ea_exl3 import device, encode, linear, moe, prompt_experts, synth
+
+    device.init(0)
+    return device, encode, linear, moe, prompt_experts, synth
+
+
+def _bf16_normal(synth, rng, shape):
+    return synth.bf16_to_f32(synth.bf16_bits((0.02 * rng.standard_normal(shape)).astype(np.float32)))
+
+
+@pytest.fixture(scope="module")
+def weights(ea):
+    """Nine experts (eight routed and a shared one), each gate / up [D, I] and down [I, D]: the bf16 weights and
+    their EXL3 encodings."""
+    device, encode, linear, moe, pe, synth = ea
+    rng = np.random.default_rng(2024)
+    out = []
+    for e in range(9):
+        mats = []
+        for m, (K, N) in enumerate([(D, I), (D, I), (I, D)]):
+            W = _bf16_normal(synth, rng, (K, N))
+            T, suh, svh = encode.quantize(W, K2, CB, seed=100 * e + m, beam=8)
+            mats.append((W, T, suh, svh))
+        out.append(mats)
+    return out
+
+
+def _host(synth, weights, ids, E):
+    """A HostLayer of E experts whose experts ids[j] hold weights[j] (gate, up, down encodings)."""
+    host = synth.HostLayer(7, experts=E, dims=D, width=I, k2=K2, cb=CB, only=list(ids))
+    for j, e in enumerate(ids):
+        for m in range(3):
+            _, T, suh, svh = weights[j][m]
+            host.trellis[m][e] = np.ascontiguousarray(T, np.uint32)
+        # stacked scales, flat [E * n]
+        host.suh_g[e * D:(e + 1) * D], host.svh_g[e * I:(e + 1) * I] = weights[j][0][2], weights[j][0][3]
+        host.suh_u[e * D:(e + 1) * D], host.svh_u[e * I:(e + 1) * I] = weights[j][1][2], weights[j][1][3]
+        host.suh_d[e * I:(e + 1) * I], host.svh_d[e * D:(e + 1) * D] = weights[j][2][2], weights[j][2][3]
+    return host
+
+
+def _dense_expert(x, mats):
+    """fp64 SwiGLU expert on the unquantized weights."""
+    g, u = x @ mats[0][0], x @ mats[1][0]
+    return (g / (1.0 + np.exp(-g)) * u) @ mats[2][0]
+
+
+def test_decode_layer_on_quantized_weights(ea, weights):
+    device, encode, linear, moe, pe, synth = ea
+    E = 256
+    logits, bias = synth.logits(2100, 1)
+    pick, wts = orc.topk8(logits, bias)
+    host = _host(synth, weights, [int(e) for e in pick[0]], E)
+    sh = weights[8]
+    shapes = [(D, I), (D, I), (I, D)]
+    lin = [linear.Linear(sh[m][1], sh[m][2], sh[m][3], K, N, K2, CB) for m, (K, N) in enumerate(shapes)]
+    x = synth.activations(2101, 1, D, "f16")
+    ex = moe.Routed(host)
+    sc = moe.Scratch(ex, 16, 8)
+    dx, dl, db = device.upload(x), device.upload(logits), device.upload(bias)
+    dp, dw = device.zeros((1, 8), torch.int32), device.zeros((1, 8), torch.float32)
+    out = device.zeros((1, D), torch.float32)
+    moe.ffn_decode(device.stream(), dx.data_ptr(), D, dl.data_ptr(), db.data_ptr(), 2.5, dp.data_ptr(), dw.data_ptr(),
+                   ex, [l.c for l in lin], sc, out.data_ptr(), 1, x_dtype=0)
+    got = device.download(out)
+    np.testing.assert_array_equal(device.download(dp), pick)
+    np.testing.assert_array_equal(device.download(dw), wts)
+    # the oracle: routed part + the shared expert's mlp (bf16 gate / up, swiglu2, fp32 down)
+    want = orc.moe_routed(x, pick, wts, oracle_routed(host), 1, 8)
+    tw = 4 * K2
+    outs = []
+    for m in range(2):
+        xh = orc.exl3_rot_in(x, sh[m][2], 1, D)
+        outs.append(orc.exl3_linear(xh, linear.strips(sh[m][1], D, I, K2), 8 * tw, (D // 16) * 8 * tw, sh[m][3], 1, D,
+                                    I, K2, CB, lin[m].sk, lin[m].wk, y_dtype=1))
+    act = orc.swiglu2(outs[0], outs[1])
+    xh = orc.exl3_rot_in(act, sh[2][2], 1, I, bf16=True)
+    want = want + orc.exl3_linear(xh, linear.strips(sh[2][1], I, D, K2), 8 * tw, (I // 16) * 8 * tw, sh[2][3], 1, I, D,
+                                  K2, CB, lin[2].sk, lin[2].wk, y_dtype=2)
+    assert_close_rms(got, want, 2e-3, "decode layer on quantized weights")
+    assert device.device_status() == 0
+    # the same layer in fp64 on the unquantized weights
+    xf = x.view(np.float16).astype(np.float64)
+    dense = sum(float(wts[0, k]) * _dense_expert(xf, weights[k]) for k in range(8)) + _dense_expert(xf, sh)
+    rel = np.sqrt(np.mean((got.astype(np.float64) - dense) ** 2)) / np.sqrt(np.mean(dense ** 2))
+    assert rel < 0.3, rel
+
+
+def test_prefill_on_quantized_weights(ea, weights):
+    device, encode, linear, moe, pe, synth = ea
+    E, R = 8, 64
+    host = _host(synth, weights, list(range(E)), E)
+    rng = np.random.default_rng(2200)
+    pick = np.stack([rng.permutation(E) for _ in range(R)]).astype(np.int32)  # every row picks all eight
+    wts = synth.routing_weights(2201, R, 8)
+    x = synth.activations(2202, R, D, "bf16")
+    ex = moe.Routed(host)
+    assert pe.supported(ex)
+    sc = pe.Scratch(ex, R, 8)
+    dx, dp, dw = device.upload(x), device.upload(pick), device.upload(wts)
+    out = device.zeros((R, D), torch.float32)
+    pe.run(device.stream(), dx.data_ptr(), D, dp.data_ptr(), dw.data_ptr(), ex, sc, out.data_ptr(), R, do_round=False)
+    got = device.download(out)
+    want = orc.prompt_experts(x, pick, wts, oracle_routed(host), R, 8, bf16=True)
+    assert_close_rms(got, want, 2e-3, "prefill on quantized weights")
+    assert device.device_status() == 0
+    xf = synth.bf16_to_f32(x).astype(np.float64)
+    dense = np.zeros((R, D))
+    for r in range(R):
+        for k in range(8):
+            dense[r] += float(wts[r, k]) * _dense_expert(xf[r:r + 1], weights[int(pick[r, k])])[0]
+    rel = np.sqrt(np.mean((got.astype(np.float64) - dense) ** 2)) / np.sqrt(np.mean(dense ** 2))
+    assert rel < 0.3, rel
