@@ -516,7 +516,7 @@ def run_decode(args, torch, np) -> dict:
 
 
 def run_linear(args, torch, np) -> dict:
-    """Config 1: linear.call of one 4-bit EXL3 linear 6144 x 2048 at one row (rot_in + one linear launch)."""
+    """Config 1: linear.call of one 4-bit EXL3 linear 6144 x 2048 at one row (one launch of the small-row kernel)."""
     from ea_exl3 import device, linear
     from ea_exl3._lib import Linear as _Linear, check, lib
     from ea_exl3.resident import DeviceLinear
@@ -536,22 +536,35 @@ def run_linear(args, torch, np) -> dict:
     scr = C.byref(sc.c)
     xp = x.data_ptr()
 
-    def step(i):
-        r = fn(s, scr, arrs[i % len(arrs)], 1, xp, 0, 1, outs, dts)
+    def step(i, stream=None):
+        r = fn(s if stream is None else stream, scr, arrs[i % len(arrs)], 1, xp, 0, 1, outs, dts)
         if r:
             check(r, "linear.call")
 
-    ms = time_steps(step, args.steps, args.warmup, torch)
+    eager_ms = time_steps(step, args.steps, args.warmup, torch)
+    ms = time_graph(step, args.steps, args.warmup, torch)
     b = lins[0].bytes() + K * 2 + N * 4
     f = 2 * K * N
     us = ms * 1e3
     t_roof = max(b / (HBM_PEAK_GBS * 1e9), f / (FP16_PEAK_TFLOPS * 1e12)) * 1e6
     gbs = b / (us * 1e-6) / 1e9
     config = {"workload": "config 1: one EXL3 4-bit linear K 6144 x N 2048 at one fp16 row, fp32 out (linear.call: "
-                          "rot_in + linear launch)", "linears_resident": args.layers, "step_bytes": b,
-              "step_roofline_us": round(t_roof, 3), "step_hbm_frac": round(t_roof / us, 4)}
-    roofline = {"kernel": "linear.call (whole call: rot_in + linear_kernel)", "bound": "hbm", "achieved": round(gbs, 1),
+                          "one launch of the small-row kernel, rotation in the kernel)", "linears_resident": args.layers,
+              "step_bytes": b, "step_roofline_us": round(t_roof, 3), "step_hbm_frac": round(t_roof / us, 4),
+              "timing": "HIP graph of the timed calls, replayed once between synchronized events",
+              "eager_us": round(eager_ms * 1e3, 3)}
+    roofline = {"kernel": "lin_small_kernel (the whole call)", "bound": "hbm", "achieved": round(gbs, 1),
                 "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None}
+    prof = "lin_small_kernel_config1.md"
+    rp = recorded_figure(prof, "lin_small_kernel_avg_us")
+    if rp:
+        roofline["rocprof_avg_us"] = rp
+        roofline["rocprof_frac"] = round(b / (rp * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)
+        roofline["rocprof_source"] = f"profiles/{prof} (rocprofv3 --kernel-trace --stats)"
+    tr = recorded_figure(prof, "traffic_bytes_per_launch")
+    if tr:
+        roofline["traffic"] = int(tr)
+        roofline["traffic_source"] = f"profiles/{prof} (rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE; copy-calibrated)"
     return _line(args, us, "us/linear", ms, config, roofline, None)
 
 
