@@ -37,12 +37,30 @@ constexpr int DL_RS = 264;                   // LDS row stride of the staged act
 constexpr int DL_MAXKC = 24;                 // k chunks of 256 (D up to 6144)
 constexpr int DL_MAXK2 = STAGE_MAXK2;        // widest trellis (K2) the decode layer runs
 constexpr int DL_STAGE_WORDS = DL_KT * 2 * 4 * DL_MAXK2;  // a wave's staged trellis words: 16 rows of 2 tiles
-constexpr int L1_LINE = 32;                  // ints between two of the one-row launch's counters (a 128-byte line)
-constexpr size_t L1_SYNC_BYTES = 16384;      // the one-row launch's counters
+constexpr size_t L1_SYNC_BYTES = 16384;      // the one-row launch's epoch and check-in words
+
+// The one-row launch's tagged slots (8 bytes each: a value's bits, then the launch's tag), at offsets fixed for every
+// layer shape: sized for the largest one (9 units, I 256, D 6144).
+constexpr int L1_UNITS = 1 + DL_SLOTS;                  // the shared expert and the eight picks
+constexpr int L1_MAXNH = DL_MAXI / 128;                 // gate|up column blocks of 128
+constexpr int L1_MAXDB = 256 * DL_MAXKC / 128;          // output column blocks of 128
+constexpr int L1_MAXB = 1 + L1_UNITS * (L1_MAXNH * 2 * DL_MAXKC + L1_MAXDB);  // blocks of the largest launch
+constexpr int L1_CHK = 64;                              // words before the check-in words (the epoch word's line)
+constexpr size_t L1_TZ = (size_t)L1_UNITS * L1_MAXNH * 2 * DL_MAXKC * 128;  // gate|up partial sums
+constexpr size_t L1_TXD = (size_t)L1_UNITS * DL_MAXI / 2;                   // down inputs, two fp16 a slot
+constexpr size_t L1_TY = (size_t)L1_UNITS * 256 * DL_MAXKC;                 // down outputs
+constexpr size_t L1_TAG_BYTES = (L1_TZ + L1_TXD + L1_TY) * 8;
+constexpr int L1_RT = 1024;                             // u64 slots before the routing slots (byte 8192)
+constexpr int L1_RT_SLOTS = 2 * DL_SLOTS + 3 * DL_SLOTS * 3;  // picks, weights, each pick's three tables
+static_assert((L1_CHK + L1_MAXB + 1) * 4 <= L1_RT * 8, "the check-in words end before the routing slots");
+static_assert((L1_RT + L1_RT_SLOTS) * 8 <= (int)L1_SYNC_BYTES, "the routing slots fit the sync region");
 
 // Scratch of the layer's launches, carved on the host for the scratch's row capacity (any R up to it runs).
 struct DLLayout {
-    int* sync;          // the one-row launch's counters (first in the region; zero between launches)
+    int* sync;          // the one-row launch's epoch word and check-in words (first in the region)
+    uint64_t* tz;       // the one-row launch's tagged slots: [U, NH, 2, KC, 128] gate|up partial sums,
+    uint64_t* txd;      //   [U, I / 2] down inputs,
+    uint64_t* ty;       //   [U, D] down outputs (all right after the sync words)
     float* zp;          // [Q, NH, 2, KC, 128] gate|up partial sums, Q = pairs + rows (the shared expert's rows last)
     uint16_t* xd;       // [Q, I] down inputs
     float* sy;          // [rows, D] the shared expert's output
@@ -1006,35 +1024,83 @@ __global__ void __launch_bounds__(DL_THREADS) combine_kernel(DLArgs a) {
 }
 
 // ---- the one-row layer in one launch ---------------------------------------------------------------------------------
-// One row routed from logits runs as a single launch of DL_THREADS-thread blocks, one item a block, in two index
-// ranges:
-//   [0, U GU): gate|up items (unit, column block nh, matrix, k chunk of 256), the shared expert's (unit 0) first;
-//   [U GU, U GU + U DB): down items (unit, output column block of 128).
-// A gate|up block routes the row up to its unit's pick (the shared expert's items need no routing), stages its 16 k
-// tiles x 2 column tiles a wave of trellis in LDS, rotates the row's activations of its chunk, multiplies on MFMA and
-// stores its partial sums. The block that completes a (unit, nh) -- the last of its 2 KC items to count in -- sums the
-// chunks in order and runs the SwiGLU epilogue of that column block into the unit's down inputs, then counts the
-// column block ready. A down block routes the row, stages its unit's down trellis of its column block and waits until
-// both column blocks of its unit are ready; it multiplies, rotates and stores the unit's output of the column block.
-// The last of the U down blocks of a column block to count in combines it: the slots in order from 0, then the shared
-// expert.
-// Hand-offs need no fence: data handed on is written with agent-scope stores (coherent across the XCDs' L2s), each wave
-// waits for its stores (vmcnt 0), the block meets at a barrier, and only then one thread counts in; readers load with
-// agent-scope loads issued after they have seen the count. A down block waits only for items of lower block index,
-// which the hardware dispatched before it and which never wait, so every wait ends; it is bounded anyway (a give-up is
-// recorded as EA_SYNC_TIMEOUT and the block's output is NaN). Every counter is back at zero when the launch ends: a
-// counter's last arrival resets it, and the last down block of a unit resets the unit's ready count.
+// One row routed from logits runs as a single launch of DL_THREADS-thread blocks, one item a block:
+//   block 0: the router: the row's top-8 from the logits, published with each pick's weight and its three
+//     matrices' trellis addresses and widths (loaded with the logits, a thread an expert);
+//   then U GU gate|up items (unit, column block nh, matrix, k chunk of 256), the shared expert's (unit 0) first;
+//   then U DB down items (unit, output column block of 128).
+// A gate|up block routes the row up to its unit's pick (the shared expert's items need no routing); a down block,
+// which has time until its inputs are ready, waits for its pick's entry from the router (one wave polls four slots),
+// so that the down blocks' top-8 rounds do not compete with the gate|up blocks' at the start of the launch. A gate|up
+// block stages its 16 k tiles x 2 column tiles a wave of trellis in LDS, rotates the row's activations of its chunk,
+// multiplies on MFMA and stores its partial sums. The last item of a (unit, nh) in block order then waits for the other items' sums, adds the
+// chunks in order and runs the SwiGLU epilogue of that column block into the unit's down inputs. A down block stages
+// its unit's down trellis of its column block, waits for both column blocks of its unit's down inputs, multiplies,
+// rotates and stores the unit's output of the column block; the down block of the last unit combines the column
+// block: the slots in order from 0, then the shared expert.
+//
+// Hand-offs are tagged slots: a value handed to another block is stored together with the launch's tag in one 8-byte
+// agent-scope store (the value's bits low, the tag high; coherent across the XCDs' L2s), and the reader polls the slots
+// themselves with agent-scope loads until every tag is the launch's. Once the data has landed, a reader needs one
+// round trip, and a writer never waits for its stores. The tag comes from the epoch word at the start of the region:
+// a block reads it once and checks in by storing the tag in its own word; the last block of the launch, once every
+// other block has checked in, advances the epoch, so the next launch (after this one, on the stream) tags with the
+// next value and no slot is ever cleared. The slots sit at fixed offsets for every layer shape, their tag halves hold
+// nothing but tags, and a scratch's tags only grow (0, what a cleared scratch holds, is never one): a slot not yet
+// written in this launch never carries its tag.
+// Every wait is on blocks of lower index, which the hardware dispatched before the waiting block and which never wait
+// on it, so every wait ends; each is bounded anyway: a give-up is recorded as EA_SYNC_TIMEOUT and the values it would
+// have produced are NaN.
 
-constexpr int L1_UNITS = 1 + DL_SLOTS;  // the shared expert and the eight picks
-constexpr int L1_MAXDB = 256 * DL_MAXKC / 128;  // output column blocks at the largest D
+constexpr int L1_POLLS = 1 << 18;  // polls before a wait gives up
 
-// The counters, one 128-byte line each: gate|up items done per (unit, nh); column blocks ready per unit; down items
-// done per unit; units done per output column block.
-__device__ __forceinline__ int* l1_gcnt(int* s, int u, int nh) { return s + (u * 2 + nh) * L1_LINE; }
-__device__ __forceinline__ int* l1_urdy(int* s, int u) { return s + (2 * L1_UNITS + u) * L1_LINE; }
-__device__ __forceinline__ int* l1_dcnt(int* s, int u) { return s + (3 * L1_UNITS + u) * L1_LINE; }
-__device__ __forceinline__ int* l1_ccnt(int* s, int cb) { return s + (4 * L1_UNITS + cb) * L1_LINE; }
-static_assert((4 * L1_UNITS + L1_MAXDB) * L1_LINE * 4 <= (int)L1_SYNC_BYTES, "the counters fit their region");
+__device__ __forceinline__ uint32_t l1_next(uint32_t e) { return e == 0xffffffffu ? 1u : e + 1u; }
+__device__ __forceinline__ uint32_t* l1_epoch(const DLArgs& a) { return reinterpret_cast<uint32_t*>(a.lay.sync); }
+__device__ __forceinline__ uint32_t* l1_checkin(const DLArgs& a) { return l1_epoch(a) + L1_CHK; }
+__device__ __forceinline__ void st_tag(uint64_t* p, uint32_t bits, uint32_t tag) {
+    __hip_atomic_store(p, ((uint64_t)tag << 32) | bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint64_t ld_tag(const uint64_t* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ bool tag_is(uint64_t v, uint32_t tag) { return (uint32_t)(v >> 32) == tag; }
+__device__ __forceinline__ float tag_val(uint64_t v) { return __uint_as_float((uint32_t)v); }
+__device__ __forceinline__ bool wave_all(bool ok) { return __builtin_amdgcn_ballot_w64(!ok) == 0; }
+// An opaque copy of a pointer: a poll loop then forms its addresses in each pass instead of holding them all.
+template <typename T>
+__device__ __forceinline__ const T* opaque_ptr(const T* p) {
+    asm volatile("" : "+v"(p));
+    return p;
+}
+
+// The epoch, read by thread 0 at the block's start (the other threads' value is unused).
+__device__ __forceinline__ uint32_t l1_epoch_load(const DLArgs& a) {
+    return threadIdx.x == 0 ? ld_coh(l1_epoch(a)) : 0u;
+}
+
+// The last block of the launch: once every other block has checked in with this launch's tag, the epoch advances to
+// it. Run by one wave.
+__device__ __forceinline__ void l1_advance(const DLArgs& a, uint32_t tag, int lane) {
+    constexpr int PER = (L1_MAXB + 63) / 64;
+    const int others = (int)gridDim.x - 1;
+    const uint32_t* chk = l1_checkin(a);
+    for (int n = 0;; ++n) {
+        bool ok = true;
+#pragma unroll
+        for (int k = 0; k < PER; ++k) {
+            const int i = lane + 64 * k;
+            const uint32_t v = ld_coh(chk + i);  // inside the sync words for every i
+            ok &= i >= others || v == tag;
+        }
+        if (wave_all(ok)) break;
+        if (n >= L1_POLLS) {
+            if (lane == 0) record_error(a.status, DEV_SYNC_TIMEOUT);
+            break;
+        }
+        __builtin_amdgcn_s_sleep(2);
+    }
+    if (lane == 0) st_coh(l1_epoch(a), tag);
+}
 
 struct L1Sh {
     int pick[DL_SLOTS];
@@ -1042,35 +1108,126 @@ struct L1Sh {
     uint64_t tp;  // the block's unit: the trellis address and width of the block's matrix, its expert
     int tk, e;
     int flag;
+    uint32_t tag;
     __attribute__((aligned(16))) uint16_t xs[DL_RS];  // the row: its rotated activations, or the unit's down inputs
     union {
         struct {
-            uint64_t tptr[256];
-            int tk2[256];
-        } r;  // every expert's table of the block's matrix, loaded with the logits
+            uint64_t tptr[3][256];
+            int tk2[3][256];
+        } r;  // the router's tables of every expert, loaded with the logits
         __attribute__((aligned(16))) uint32_t stage[DL_WAVES][DL_STAGE_WORDS];
-        float gus[2][128];
+        struct {
+            float half[2][128];  // the gate's and the up's sums over the first half of the chunks
+            float gus[2][128];   // their outputs
+        } ep;
         float ys[128];
     };
 };
 
-// The row's picks up to `need` (need = 8: all of them and their weights) and the tables of matrix `mat` of every
-// expert, a thread an expert (E = 256); then the block's unit u's entry (u >= 1: routed unit u - 1, pick u - 1).
-__device__ __forceinline__ void l1_route(const DLArgs& a, L1Sh& sh, int mat, int u, int need) {
+__device__ __forceinline__ uint64_t* l1_route_slots(const DLArgs& a) {
+    return reinterpret_cast<uint64_t*>(a.lay.sync) + L1_RT;
+}
+
+// Block 0: the row's top-8 and weights, every expert's tables of the three matrices (a thread an expert, E = 256,
+// loaded with the logits), then the routing slots: pick k, weight k, and (matrix m, pick k)'s trellis address (two
+// slots) and width; and the caller's pick / wts.
+__device__ __forceinline__ void l1_router(const DLArgs& a, L1Sh& sh, uint32_t e0) {
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    uint64_t tp[3];
+    int tk[3];
+#pragma unroll
+    for (int m = 0; m < 3; ++m) {
+        tp[m] = (uint64_t)a.ptr[m][t];
+        tk[m] = a.k2t[m][t];
+    }
+    if (wave == 0) topk8_wave(a.logits, a.bias, a.scale, sh.pick, sh.wts, lane);
+#pragma unroll
+    for (int m = 0; m < 3; ++m) {
+        sh.r.tptr[m][t] = tp[m];
+        sh.r.tk2[m][t] = tk[m];
+    }
+    if (t == 0) {
+        const uint32_t tag = l1_next(e0);
+        sh.tag = tag;
+        st_coh(l1_checkin(a) + blockIdx.x, tag);
+    }
+    __syncthreads();
+    if (t < DL_SLOTS) {
+        const uint32_t tag = sh.tag;
+        const int e = sh.pick[t];
+        const float w = sh.wts[t];
+        uint64_t* rt = l1_route_slots(a);
+        st_tag(rt + t, (uint32_t)e, tag);
+        st_tag(rt + DL_SLOTS + t, __float_as_uint(w), tag);
+#pragma unroll
+        for (int m = 0; m < 3; ++m) {
+            const uint64_t p = sh.r.tptr[m][e];
+            uint64_t* q = rt + 2 * DL_SLOTS + (m * DL_SLOTS + t) * 3;
+            st_tag(q, (uint32_t)p, tag);
+            st_tag(q + 1, (uint32_t)(p >> 32), tag);
+            st_tag(q + 2, (uint32_t)sh.r.tk2[m][e], tag);
+        }
+        a.pick[t] = e;
+        a.wts[t] = w;
+    }
+}
+
+// A gate|up item routes the row itself, up to its pick k (k + 1 top-8 rounds), with the tables of matrix `mat` of
+// every expert loaded with the logits; its unit's entry into sh.e / sh.tp / sh.tk. (Waiting for the router's slots
+// instead measured slower for the gate|up items: the slots land 1-2 us after the router stores them.)
+__device__ __forceinline__ void l1_route_self(const DLArgs& a, L1Sh& sh, int mat, int k) {
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const uint64_t tp = (uint64_t)a.ptr[mat][t];
     const int tk = a.k2t[mat][t];
-    if (wave == (int)(blockIdx.x % DL_WAVES)) topk8_wave(a.logits, a.bias, a.scale, sh.pick, sh.wts, lane, need);
-    sh.r.tptr[t] = tp;
-    sh.r.tk2[t] = tk;
+    if (wave == (int)(blockIdx.x % DL_WAVES)) topk8_wave(a.logits, a.bias, a.scale, sh.pick, sh.wts, lane, k + 1);
+    sh.r.tptr[0][t] = tp;
+    sh.r.tk2[0][t] = tk;
     __syncthreads();
     if (t == 0) {
-        const int e = sh.pick[u - 1];
+        const int e = sh.pick[k];
         sh.e = e;
-        sh.tp = sh.r.tptr[e];
-        sh.tk = sh.r.tk2[e];
+        sh.tp = sh.r.tptr[0][e];
+        sh.tk = sh.r.tk2[0][e];
     }
     __syncthreads();
+}
+
+// A down item's wait for the router (wave 0; the caller's barrier follows): pick k's expert and its matrix `mat`'s
+// trellis address and width into sh.e / sh.tp / sh.tk, and with `weights` every pick's weight into sh.wts. Lanes 0..3
+// poll the pick's four slots, lanes 4..11 the weights; a give-up is recorded and leaves expert 0's entry (the
+// product is then NaN through `timed_out`).
+__device__ __forceinline__ bool l1_route_wait(const DLArgs& a, L1Sh& sh, int k, int mat, uint32_t tag, bool weights,
+                                              int lane) {
+    const uint64_t* rt = l1_route_slots(a);
+    const int at = lane == 0 ? k
+                 : lane < 4 ? 2 * DL_SLOTS + (mat * DL_SLOTS + k) * 3 + lane - 1
+                 : lane < 12 ? DL_SLOTS + lane - 4 : 0;
+    const bool used = lane < (weights ? 12 : 4);
+    uint64_t v = 0;
+    bool timed_out = false;
+    for (int n = 0;; ++n) {
+        v = ld_tag(rt + at);
+        if (wave_all(!used || tag_is(v, tag))) break;
+        if (n >= L1_POLLS) {
+            timed_out = true;
+            if (lane == 0) record_error(a.status, DEV_SYNC_TIMEOUT);
+            break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+    }
+    const uint32_t lo = (uint32_t)v;
+    const int e = __builtin_amdgcn_readlane((int)lo, 0);
+    const uint32_t plo = (uint32_t)__builtin_amdgcn_readlane((int)lo, 1);
+    const uint32_t phi = (uint32_t)__builtin_amdgcn_readlane((int)lo, 2);
+    const int k2 = __builtin_amdgcn_readlane((int)lo, 3);
+    if (lane == 0) {
+        const bool ok = !timed_out && e >= 0 && e < a.E;
+        sh.e = ok ? e : 0;
+        sh.tp = ok ? ((uint64_t)phi << 32 | plo) : (uint64_t)a.ptr[mat][0];
+        sh.tk = ok ? k2 : 0;  // no decoder: the product stores NaN
+    }
+    if (weights && lane >= 4 && lane < 12) sh.wts[lane - 4] = __uint_as_float(lo);
+    return timed_out;
 }
 
 // The row's product over NKT k tiles with the wave's two column tiles staged in st: acc[j] (row 0 in lanes 0..15,
@@ -1106,10 +1263,98 @@ __device__ __forceinline__ bool l1_mfma_k2(int k2, const uint32_t* st, const Lan
     return EA_K2_SWITCH(k2, 2, 10, (l1_mfma<CB, K2V, NKT>(st, lq, xs, lane, acc)));
 }
 
-// Gate|up item (unit u, column block nh, matrix mat, chunk c) of the row. q: the unit's member (the pick's slot, or P
-// for the shared expert).
+// A down item's wait for both column blocks of its unit's down inputs: wave 0 polls their slots and moves them to
+// sh.xs; every wave meets at the barrier. True when the wait gave up.
+__device__ __forceinline__ bool l1_down_wait(const DLArgs& a, L1Sh& sh, int u, uint32_t tag, int lane) {
+    const int NH = a.I / 128;
+    if (threadIdx.x < 64) {
+        const uint64_t* xd = a.lay.txd + (size_t)u * (a.I / 2) + lane;
+        uint64_t p[L1_MAXNH];
+        bool timed_out = false;
+        for (int n = 0;; ++n) {
+            bool ok = true;
+#pragma unroll
+            for (int j = 0; j < L1_MAXNH; ++j) {
+                p[j] = ld_tag(xd + j * 64);  // j >= NH: another unit's slot, not used
+                ok &= j >= NH || tag_is(p[j], tag);
+            }
+            if (wave_all(ok)) break;
+            if (n >= L1_POLLS) {
+                timed_out = true;
+                if (lane == 0) record_error(a.status, DEV_SYNC_TIMEOUT);
+                break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+        }
+#pragma unroll
+        for (int j = 0; j < L1_MAXNH; ++j)
+            if (j < NH) reinterpret_cast<uint32_t*>(sh.xs)[j * 64 + lane] = (uint32_t)p[j];
+        if (lane == 0) {
+            sh.flag = timed_out;
+            sh.tag = tag;
+        }
+    }
+    __syncthreads();
+    return sh.flag;
+}
+
+// The down product of a down item, around its wait: the first PRE k-tile pairs of the wave's two column tiles are
+// decoded into MFMA operands (registers) while the unit's down inputs are still being produced; l1_down_wait then
+// brings the inputs to sh.xs, and the MFMAs run, the remaining pairs decoded as they go. Returns the wait's result.
+// The one-row layer pre-decodes every pair (PRE = NKT / 2): once the inputs land, a down item is 16 MFMAs, the FWHT
+// and a store (2.0 us of decode after the wait measured without it; 1.0 us with half of it pre-decoded).
+template <int CB, int K2, int NKT, int PRE>
+__device__ __forceinline__ bool l1_down_product(const DLArgs& a, L1Sh& sh, int u, uint32_t tag, const uint32_t* st,
+                                                const LaneQuad& lq, int lane, f4v (&acc)[2]) {
+    static_assert(PRE <= NKT / 2, "pre-decoded pairs of k tiles");
+    constexpr int TW = 4 * K2;
+    const uint32_t* wa = st + lq.w0;
+    const uint32_t* wb = st + lq.w1;
+    u4v pb[PRE > 0 ? PRE : 1][2];
+#pragma unroll
+    for (int tp = 0; tp < PRE; ++tp)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int t0 = (4 * tp + j) * TW, t1 = (4 * tp + 2 + j) * TW;
+            const u2v b0 = decode_quad<K2, CB>(wa[t0], wb[t0], lq.sh);
+            const u2v b1 = decode_quad<K2, CB>(wa[t1], wb[t1], lq.sh);
+            pb[tp][j] = u4v{b0.x, b0.y, b1.x, b1.y};
+        }
+#pragma unroll
+    for (int tp = 0; tp < PRE; ++tp)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) hold(pb[tp][j]);  // decoded before the wait, not after it
+    const bool r = l1_down_wait(a, sh, u, tag, lane);
+    const bool row0 = (lane & 15) == 0;
+    const uint16_t* xr = sh.xs + 2 * ((lane >> 4) & 3);
+#pragma unroll
+    for (int tp = 0; tp < NKT / 2; ++tp) {
+        const uint16_t* xk = xr + 2 * tp * 16;
+        u4v au = {*reinterpret_cast<const uint32_t*>(xk), *reinterpret_cast<const uint32_t*>(xk + 8),
+                  *reinterpret_cast<const uint32_t*>(xk + 16), *reinterpret_cast<const uint32_t*>(xk + 24)};
+        if (!row0) au = u4v{0u, 0u, 0u, 0u};
+        const h8v a = __builtin_bit_cast(h8v, au);
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            u4v bq;
+            if (tp < PRE) {
+                bq = pb[tp < PRE ? tp : 0][j];
+            } else {
+                const int t0 = (4 * tp + j) * TW, t1 = (4 * tp + 2 + j) * TW;
+                const u2v b0 = decode_quad<K2, CB>(wa[t0], wb[t0], lq.sh);
+                const u2v b1 = decode_quad<K2, CB>(wa[t1], wb[t1], lq.sh);
+                bq = u4v{b0.x, b0.y, b1.x, b1.y};
+            }
+            acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, __builtin_bit_cast(h8v, bq), acc[j], 0, 0, 0);
+        }
+    }
+    return r;
+}
+
+// Gate|up item (unit u, column block nh, matrix mat, chunk c) of the row; e0: the epoch thread 0 read. Its partial
+// sums go to the tagged slots tz[u][nh][mat][c][128].
 template <int CB, bool SHARED>
-__device__ __forceinline__ void l1_gateup(const DLArgs& a, L1Sh& sh, int u, int nh, int mat, int c, int q) {
+__device__ __forceinline__ void l1_gateup(const DLArgs& a, L1Sh& sh, int u, int nh, int mat, int c, uint32_t e0) {
     const int lane = opaque_lane(threadIdx.x & 63), wave = uniform((int)threadIdx.x >> 6);
     const int KC = a.D / 256, NH = a.I / 128, ns = a.I / 16;
     const int nt0 = nh * 8 + 2 * wave, kt0 = c * DL_KT;
@@ -1153,7 +1398,13 @@ __device__ __forceinline__ void l1_gateup(const DLArgs& a, L1Sh& sh, int u, int 
         *reinterpret_cast<uint32_t*>(sh.xs + blk * 128 + 2 * lane) =
             (uint32_t)f2h(v0 * HAD_SCALE) | ((uint32_t)f2h(v1 * HAD_SCALE) << 16);
     }
+    if (threadIdx.x == 0) {  // the launch's tag, and the check-in
+        const uint32_t t = l1_next(e0);
+        sh.tag = t;
+        st_coh(l1_checkin(a) + blockIdx.x, t);
+    }
     __syncthreads();
+    const uint32_t tag = (uint32_t)uniform((int)sh.tag);
     uint32_t* st = sh.stage[wave];
     stage_store<DL_KT>(st, k2, lane, v);
     f4v acc[2] = {f4v{0.f, 0.f, 0.f, 0.f}, f4v{0.f, 0.f, 0.f, 0.f}};
@@ -1162,45 +1413,89 @@ __device__ __forceinline__ void l1_gateup(const DLArgs& a, L1Sh& sh, int u, int 
         if (lane == 0) record_error(a.status, DEV_UNSUPPORTED_WIDTH);
         acc[0] = acc[1] = nan4();
     }
-    // row 0's partial sums of this chunk: zp[q][nh][mat][c][128]
+    // row 0's partial sums of this chunk
     if (lane < 16) {
-        float* z = a.lay.zp + ((((size_t)q * NH + nh) * 2 + mat) * KC + c) * 128;
+        uint64_t* z = a.lay.tz + ((((size_t)u * NH + nh) * 2 + mat) * KC + c) * 128;
 #pragma unroll
-        for (int j = 0; j < 2; ++j) st_coh(z + (2 * wave + j) * 16 + lane, acc[j][0]);
+        for (int j = 0; j < 2; ++j) st_tag(z + (2 * wave + j) * 16 + lane, __float_as_uint(acc[j][0]), tag);
     }
 }
 
-// The SwiGLU epilogue of (unit, column block nh) of the row's member q, after every chunk's partial sums are in:
-// waves 0 and 1 sum the gate's and the up's chunks in order and rotate them (gu_out), wave 0 forms the down inputs.
-__device__ __forceinline__ void l1_epilogue(const DLArgs& a, L1Sh& sh, const UnitView& uv, int nh, int q) {
+// The SwiGLU epilogue of (unit u, column block nh), run by the unit's last gate|up item of nh once its own sums are
+// stored: waves 0 / 2 take the gate's first / second half of the chunks, waves 1 / 3 the up's, each polling its
+// chunks' slots (two columns a lane); the sums run over the chunks in order, the first half's handed on through LDS;
+// then FWHT, svh and SwiGLU into the unit's tagged down inputs.
+__device__ __forceinline__ void l1_epilogue(const DLArgs& a, L1Sh& sh, const UnitView& uv, int u, int nh) {
+    constexpr int HC = DL_MAXKC / 2;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int KC = a.D / 256, NH = a.I / 128;
-    uint32_t sd = 0;
-    if (wave < 2) {
-        const uint32_t sv = svh_pair(a, uv, nh, wave, lane);
-        sd = suhd_pair(a, uv, nh, lane);
-        const float* z = a.lay.zp + (((size_t)q * NH + nh) * 2 + wave) * KC * 128 + 2 * lane;
-        float2 zv[DL_MAXKC];
+    const int mat = wave & 1, h = wave >> 1, half = (KC + 1) >> 1;
+    const int c0 = h ? half : 0, nc = h ? KC - half : half;
+    const uint32_t tag = (uint32_t)uniform((int)sh.tag);
+    const uint32_t sv = svh_pair(a, uv, nh, mat, lane);
+    const uint32_t sd = suhd_pair(a, uv, nh, lane);
+    __syncthreads();  // every wave is done with its staged trellis: the sums take its place
+    const uint64_t* z = a.lay.tz + (((size_t)u * NH + nh) * 2 + mat) * KC * 128 + (size_t)c0 * 128 + 2 * lane;
+    uint64_t p[HC][2];
+    bool timed_out = false;
+    if (nc > 0) {
+        for (int n = 0;; ++n) {
+            bool ok = true;
+            const uint64_t* zb = opaque_ptr(z);  // addresses formed inside the loop, not held across it
 #pragma unroll
-        for (int cc = 0; cc < DL_MAXKC; ++cc) zv[cc] = ld_coh2(z + (cc < KC ? cc : KC - 1) * 128);
-        const float2 o = gu_out(uv, zp_sum(a, zv), sv, lane);
-        *reinterpret_cast<float2*>(&sh.gus[wave][2 * lane]) = o;
+            for (int i = 0; i < HC; ++i) {
+                p[i][0] = ld_tag(zb + i * 128);  // chunks past nc: other slots of the array, not used
+                p[i][1] = ld_tag(zb + i * 128 + 1);
+                ok &= i >= nc || (tag_is(p[i][0], tag) && tag_is(p[i][1], tag));
+            }
+            if (wave_all(ok)) break;
+            if (n >= L1_POLLS) {
+                timed_out = true;
+                if (lane == 0) record_error(a.status, DEV_SYNC_TIMEOUT);
+                break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+        }
+    }
+    float s0 = 0.f, s1 = 0.f;
+    if (h == 0) {
+#pragma unroll
+        for (int i = 0; i < HC; ++i)
+            if (i < nc) {
+                s0 += tag_val(p[i][0]);
+                s1 += tag_val(p[i][1]);
+            }
+        if (timed_out) s0 = s1 = __builtin_nanf("");
+        *reinterpret_cast<float2*>(&sh.ep.half[mat][2 * lane]) = float2{s0, s1};
     }
     __syncthreads();
-    if (wave == 0) {
-        const float2 g = *reinterpret_cast<const float2*>(&sh.gus[0][2 * lane]);
-        const float2 u = *reinterpret_cast<const float2*>(&sh.gus[1][2 * lane]);
-        st_coh(reinterpret_cast<uint32_t*>(a.lay.xd + (size_t)q * a.I + nh * 128 + 2 * lane),
-               act_pair(uv, g, u, sd, lane));
+    if (h == 1) {
+        const float2 f = *reinterpret_cast<const float2*>(&sh.ep.half[mat][2 * lane]);
+        s0 = f.x;
+        s1 = f.y;
+#pragma unroll
+        for (int i = 0; i < HC; ++i)
+            if (i < nc) {
+                s0 += tag_val(p[i][0]);
+                s1 += tag_val(p[i][1]);
+            }
+        if (timed_out) s0 = s1 = __builtin_nanf("");
+        *reinterpret_cast<float2*>(&sh.ep.gus[mat][2 * lane]) = gu_out(uv, float2{s0, s1}, sv, lane);
+    }
+    __syncthreads();
+    if (wave == 2) {
+        const float2 g = *reinterpret_cast<const float2*>(&sh.ep.gus[0][2 * lane]);
+        const float2 up = *reinterpret_cast<const float2*>(&sh.ep.gus[1][2 * lane]);
+        st_tag(a.lay.txd + (size_t)u * (a.I / 2) + nh * 64 + lane, act_pair(uv, g, up, sd, lane), tag);
     }
 }
 
-// Down item (unit u, output column block cb) of the row's member q: its output columns of the unit (y or sy), then
-// whether this block combines the column block.
+// Down item (unit u, output column block cb) of the row; e0: the epoch thread 0 read. Its outputs go to the tagged
+// slots ty[u][D]; the last unit's block combines the column block instead.
 template <int CB, int SCB, int NKT>
-__device__ __forceinline__ void l1_down(const DLArgs& a, L1Sh& sh, const UnitView& uv, int u, int cb, int q) {
+__device__ __forceinline__ void l1_down(const DLArgs& a, L1Sh& sh, const UnitView& uv, int u, int cb, uint32_t e0) {
     const int lane = opaque_lane(threadIdx.x & 63), wave = uniform((int)threadIdx.x >> 6);
-    const int NH = a.I / 128, DB = a.D / 128, KT = a.I / 16, ns = a.D / 16;
+    const int NH = a.I / 128, KT = a.I / 16, ns = a.D / 16;
     const int nt0 = cb * 8 + 2 * wave;
     const int k2 = uv.shared ? a.sh_k2 : uniform(sh.tk), TWB = 16 * k2;
     TileSpan sp;
@@ -1220,29 +1515,21 @@ __device__ __forceinline__ void l1_down(const DLArgs& a, L1Sh& sh, const UnitVie
     stage_issue<NKT>(sp, k2, lane, v);
     issued();
     hold(sd);
-    // both column blocks of the unit's down inputs ready
-    if (threadIdx.x == 0) {
-        int n = 0;
-        while (ld_coh(l1_urdy(a.lay.sync, u)) < NH) {
-            if (++n > (1 << 18)) {
-                record_error(a.status, DEV_SYNC_TIMEOUT);
-                break;
-            }
-            __builtin_amdgcn_s_sleep(2);
-        }
-        sh.flag = n > (1 << 18);
+    const uint32_t tag = l1_next((uint32_t)uniform((int)e0));  // meaningful in wave 0 only (lane 0 is thread 0)
+    if (wave == 0) {
+        if (lane == 0) st_coh(l1_checkin(a) + blockIdx.x, tag);
+        if (blockIdx.x == gridDim.x - 1) l1_advance(a, tag, lane);
     }
-    __syncthreads();
-    const bool timed_out = sh.flag;
-    if (threadIdx.x < a.I / 2)
-        reinterpret_cast<uint32_t*>(sh.xs)[threadIdx.x] =
-            ld_coh(reinterpret_cast<const uint32_t*>(a.lay.xd + (size_t)q * a.I) + threadIdx.x);
-    __syncthreads();
     uint32_t* st = sh.stage[wave];
     stage_store<NKT>(st, k2, lane, v);
     f4v acc[2] = {f4v{0.f, 0.f, 0.f, 0.f}, f4v{0.f, 0.f, 0.f, 0.f}};
-    const bool ok = uv.shared ? l1_mfma_k2<SCB, NKT>(k2, st, lq, sh.xs, lane, acc)
-                              : l1_mfma_k2<CB, NKT>(k2, st, lq, sh.xs, lane, acc);
+    bool timed_out = false;
+    const bool ok =
+        uv.shared ? EA_K2_SWITCH(k2, 2, 10,
+                                 (timed_out = l1_down_product<SCB, K2V, NKT, NKT / 2>(a, sh, u, tag, st, lq, lane, acc)))
+                  : EA_K2_SWITCH(k2, 2, 10,
+                                 (timed_out = l1_down_product<CB, K2V, NKT, NKT / 2>(a, sh, u, tag, st, lq, lane, acc)));
+    if (!ok) timed_out = l1_down_wait(a, sh, u, tag, lane);  // no decoder for the width: the block still meets its barrier
     if (!ok || timed_out) {
         if (lane == 0 && !ok) record_error(a.status, DEV_UNSUPPORTED_WIDTH);
         acc[0] = acc[1] = nan4();
@@ -1253,97 +1540,99 @@ __device__ __forceinline__ void l1_down(const DLArgs& a, L1Sh& sh, const UnitVie
         for (int j = 0; j < 2; ++j) sh.ys[(2 * wave + j) * 16 + lane] = acc[j][0];
     }
     __syncthreads();
-    if (wave == 0) {
-        float v0 = sh.ys[2 * lane], v1 = sh.ys[2 * lane + 1];
-        fwht128_w64(v0, v1, lane);
-        const float s0 = h2f((uint16_t)(sd & 0xffffu)), s1 = h2f((uint16_t)(sd >> 16));
-        float* dst = uv.shared ? a.lay.sy : a.yroute + (size_t)q * a.D;
-        st_coh2(dst + cb * 128 + 2 * lane, float2{v0 * HAD_SCALE * s0, v1 * HAD_SCALE * s1});
+    if (wave != 0) return;
+    float v0 = sh.ys[2 * lane], v1 = sh.ys[2 * lane + 1];
+    fwht128_w64(v0, v1, lane);
+    v0 = v0 * HAD_SCALE * h2f((uint16_t)(sd & 0xffffu));
+    v1 = v1 * HAD_SCALE * h2f((uint16_t)(sd >> 16));
+    const int n = cb * 128 + 2 * lane;
+    if (u != a.U - 1) {
+        uint64_t* y = a.lay.ty + (size_t)u * a.D + n;
+        st_tag(y, __float_as_uint(v0), tag);
+        st_tag(y + 1, __float_as_uint(v1), tag);
+        return;
     }
-    stores_done();
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        const bool last = count_in(l1_ccnt(a.lay.sync, cb)) == a.U - 1;
-        if (last) reset_count(l1_ccnt(a.lay.sync, cb));
-        if (count_in(l1_dcnt(a.lay.sync, u)) == DB - 1) {  // every down block of the unit is past its wait
-            reset_count(l1_urdy(a.lay.sync, u));
-            reset_count(l1_dcnt(a.lay.sync, u));
-        }
-        sh.flag = last;
-    }
-    __syncthreads();
-    if (sh.flag && wave == 0) {
-        // the combine of the column block: the slots in order from 0 (exl3_experts.cu:256-267), then the shared expert
-        const int n = cb * 128 + 2 * lane;
-        float2 y[DL_SLOTS];
+    // the combine of the column block (the last unit is the last slot's): the other units' outputs, then the slots
+    // in order from 0 (exl3_experts.cu:256-267), then the shared expert
+    uint64_t p[L1_UNITS - 1][2];
+    bool timed_out2 = false;
+    for (int it = 0;; ++it) {
+        bool all = true;
+        const uint64_t* yb = opaque_ptr(a.lay.ty + n);
 #pragma unroll
-        for (int k = 0; k < DL_SLOTS; ++k) y[k] = ld_coh2(a.yroute + (size_t)k * a.D + n);
-        float2 sv = a.hs ? ld_coh2(a.lay.sy + n) : float2{0.f, 0.f};
-        float a0 = 0.f, a1 = 0.f;
-#pragma unroll
-        for (int k = 0; k < DL_SLOTS; ++k) {
-            a0 = __builtin_fmaf(sh.wts[k], y[k].x, a0);
-            a1 = __builtin_fmaf(sh.wts[k], y[k].y, a1);
+        for (int w = 0; w < L1_UNITS - 1; ++w) {
+            const uint64_t* y = yb + (size_t)w * a.D;  // w >= U - 1: a slot not used
+            p[w][0] = ld_tag(y);
+            p[w][1] = ld_tag(y + 1);
+            all &= w >= a.U - 1 || (tag_is(p[w][0], tag) && tag_is(p[w][1], tag));
         }
-        if (a.hs) {
-            a0 = a0 + sv.x;
-            a1 = a1 + sv.y;
+        if (wave_all(all)) break;
+        if (it >= L1_POLLS) {
+            timed_out2 = true;
+            if (lane == 0) record_error(a.status, DEV_SYNC_TIMEOUT);
+            break;
         }
-        *reinterpret_cast<float2*>(a.out + n) = float2{a0, a1};
+        __builtin_amdgcn_s_sleep(1);
     }
+    // slot k is unit hs + k (U = hs + 8): slots 0..6 from the tagged slots, slot 7 this block's own
+    const bool hs = a.hs;
+    float a0 = 0.f, a1 = 0.f;
+#pragma unroll
+    for (int k = 0; k < DL_SLOTS - 1; ++k) {
+        a0 = __builtin_fmaf(sh.wts[k], tag_val(hs ? p[k + 1][0] : p[k][0]), a0);
+        a1 = __builtin_fmaf(sh.wts[k], tag_val(hs ? p[k + 1][1] : p[k][1]), a1);
+    }
+    a0 = __builtin_fmaf(sh.wts[DL_SLOTS - 1], v0, a0);
+    a1 = __builtin_fmaf(sh.wts[DL_SLOTS - 1], v1, a1);
+    if (hs) {
+        a0 = a0 + tag_val(p[0][0]);
+        a1 = a1 + tag_val(p[0][1]);
+    }
+    if (timed_out2) a0 = a1 = __builtin_nanf("");
+    *reinterpret_cast<float2*>(a.out + n) = float2{a0, a1};
 }
 
+// Five waves a SIMD: the down items hold their whole pre-decoded product (64 VGPRs) through their wait.
 template <int CB, int SCB>
-__global__ void __launch_bounds__(DL_THREADS) __attribute__((amdgpu_waves_per_eu(6))) layer1_kernel(DLArgs a) {
+__global__ void __launch_bounds__(DL_THREADS) __attribute__((amdgpu_waves_per_eu(5))) layer1_kernel(DLArgs a) {
     __shared__ L1Sh sh;
     const int NH = a.I / 128, KC = a.D / 256, DB = a.D / 128;
     const int GU = NH * 2 * KC;  // gate|up items a unit
-    const int b = blockIdx.x;
+    const uint32_t e0 = l1_epoch_load(a);
+    if (blockIdx.x == 0) {
+        l1_router(a, sh, e0);
+        return;
+    }
+    const int b = blockIdx.x - 1, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     UnitView uv;
     uv.nm = 1;
     uv.mem = nullptr;
     if (b < a.U * GU) {
         const int u = b / GU, rem = b % GU, nh = rem / (2 * KC), mat = (rem / KC) & 1, c = rem % KC;
         uv.shared = a.hs && u == 0;
-        const int q = uv.shared ? DL_SLOTS : u - a.hs;
         if (uv.shared) {
             uv.e = -1;
-            l1_gateup<SCB, true>(a, sh, u, nh, mat, c, q);
+            l1_gateup<SCB, true>(a, sh, u, nh, mat, c, e0);
         } else {
-            const bool publisher = b == a.hs * GU;  // hands pick / wts to the caller
-            l1_route(a, sh, mat, u - a.hs + 1, publisher ? DL_SLOTS : u - a.hs + 1);
-            if (publisher && threadIdx.x < DL_SLOTS) {
-                a.pick[threadIdx.x] = sh.pick[threadIdx.x];
-                a.wts[threadIdx.x] = sh.wts[threadIdx.x];
-            }
+            l1_route_self(a, sh, mat, u - a.hs);
             uv.e = uniform(sh.e);
-            l1_gateup<CB, false>(a, sh, u, nh, mat, c, q);
+            l1_gateup<CB, false>(a, sh, u, nh, mat, c, e0);
         }
-        stores_done();
-        __syncthreads();
-        if (threadIdx.x == 0) {
-            const bool last = count_in(l1_gcnt(a.lay.sync, u, nh)) == 2 * KC - 1;
-            if (last) reset_count(l1_gcnt(a.lay.sync, u, nh));
-            sh.flag = last;
-        }
-        __syncthreads();
-        if (!sh.flag) return;
-        l1_epilogue(a, sh, uv, nh, q);
-        stores_done();
-        __syncthreads();
-        if (threadIdx.x == 0) count_in(l1_urdy(a.lay.sync, u));
+        if (mat == 1 && c == KC - 1) l1_epilogue(a, sh, uv, u, nh);
         return;
     }
     const int d = b - a.U * GU, u = d / DB, cb = d % DB;
     uv.shared = a.hs && u == 0;
-    const int q = uv.shared ? DL_SLOTS : u - a.hs;
-    // every down block routes the whole row: the last of a column block combines all eight slots with their weights
-    l1_route(a, sh, 2, uv.shared ? 1 : u - a.hs + 1, DL_SLOTS);
+    if (!uv.shared) {
+        // the last unit's block combines the column block: it takes every weight
+        if (wave == 0) l1_route_wait(a, sh, u - a.hs, 2, l1_next((uint32_t)uniform((int)e0)), u == a.U - 1, lane);
+        __syncthreads();
+    }
     uv.e = uv.shared ? -1 : uniform(sh.e);
     if (a.I == 256)
-        l1_down<CB, SCB, 16>(a, sh, uv, u, cb, q);
+        l1_down<CB, SCB, 16>(a, sh, uv, u, cb, e0);
     else
-        l1_down<CB, SCB, 8>(a, sh, uv, u, cb, q);
+        l1_down<CB, SCB, 8>(a, sh, uv, u, cb, e0);
 }
 
 // ---- host side ----------------------------------------------------------------------------------------------------
@@ -1352,7 +1641,7 @@ static size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
 
 // Region offsets for a scratch of `rows` rows (capacity), in bytes from the region's base.
 struct DLCarve {
-    size_t sync, zp, xd, sy, ws, total;
+    size_t sync, tags, zp, xd, sy, ws, total;
     size_t U, NH, DB;
 };
 
@@ -1370,6 +1659,7 @@ static DLCarve dl_carve(uint32_t rows, uint32_t D, uint32_t I, uint32_t E) {
         return at;
     };
     c.sync = take(L1_SYNC_BYTES);
+    c.tags = take(L1_TAG_BYTES);
     c.zp = take(Q * c.NH * 2 * KC * 128 * 4);
     c.xd = take(Q * I * 2);
     c.sy = take((size_t)rows * D * 4);
@@ -1392,6 +1682,9 @@ static DLLayout dl_layout(uint64_t base, uint32_t rows, uint32_t D, uint32_t I, 
     const DLCarve c = dl_carve(rows, D, I, E);
     DLLayout l;
     l.sync = dptr<int>(base + c.sync);
+    l.tz = dptr<uint64_t>(base + c.tags);
+    l.txd = l.tz + L1_TZ;
+    l.ty = l.txd + L1_TXD;
     l.zp = dptr<float>(base + c.zp);
     l.xd = dptr<uint16_t>(base + c.xd);
     l.sy = dptr<float>(base + c.sy);
@@ -1450,7 +1743,7 @@ static int dl_launch(hipStream_t s, const DLArgs& a, int cus, int device) {
     }
     if (a.R == 1 && a.logits) {
         // one row routed from logits: the whole layer in one launch (the stage events then all follow it)
-        layer1_kernel<CB, SCB><<<a.U * NH * 2 * KC + a.U * DB, DL_THREADS, 0, s>>>(a);
+        layer1_kernel<CB, SCB><<<1 + a.U * NH * 2 * KC + a.U * DB, DL_THREADS, 0, s>>>(a);
         const int r = launched();
         if (r) return r;
         for (int k = 1; k <= DL_STAGES; ++k) mark_stage(s, device, k);
@@ -1571,10 +1864,10 @@ int decode_layer(hipStream_t s, const void* x, int x_dtype, uint32_t x_stride, c
 // ---- the allocation-free variant's scratch --------------------------------------------------------------------------
 
 // The scratch of ea_ffn_moe_decode_static: the per-pair down outputs and the decode layer's region, carved for
-// DL_MAXR rows of the call's layer shape. The largest shape the decode layer takes (D 6144, I 256) needs 10.7 MB.
+// DL_MAXR rows of the call's layer shape. The largest shape the decode layer takes (D 6144, I 256) needs 12.06 MB.
 // Every call on a device shares that device's copy, which holds the last call's contents: the layer writes every
-// value it reads back within a call, and the one-row launch's counters, which must start at zero, are cleared by
-// ea_init and left at zero by every launch.
+// value it reads back within a call, and the one-row launch's epoch word, check-in words and tagged slots start at
+// zero (ea_init clears the array) and are never cleared again: each launch tags with the next epoch.
 constexpr size_t DL_STATIC_BYTES = (size_t)12 << 20;
 static __device__ __align__(256) uint8_t scratch[DL_STATIC_BYTES];
 

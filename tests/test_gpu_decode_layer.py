@@ -216,6 +216,37 @@ def test_topk8_nan_policy_both_paths(ea):
         np.testing.assert_array_equal(wts, wts_w if rows == R else wts_w[2:3])
 
 
+def test_one_row_topk_ties_and_wide_spread(ea):
+    """The one-row layer's top-8 (a selection: the eighth largest key, then ties by the lower id, then each pick's
+    slot by rank) against the oracle's eight argmax rounds, bit for bit, on rows built to stress it: every expert
+    tied, an exact tie between two strong experts, logits on a coarse grid (many ties at every level), eight equal
+    maxima, the largest choices at the highest ids, and logits spread over many binades."""
+    device, linear, moe, synth = ea
+    E, D, I = 256, 1024, 128
+    logits, bias = synth.logits(1300, 8)
+    logits[0, :] = 0.25
+    logits[1, 10] = logits[1, 20] = 5.0
+    logits[2] = np.round(logits[2] * 2) / 2
+    logits[3, :] = -1.0
+    logits[3, [200, 3, 77, 150, 9, 255, 0, 128]] = 3.0
+    logits[4] = np.linspace(-6, 6, 256, dtype=np.float32)
+    logits[5] = (np.sign(logits[5]) * np.exp2(np.abs(logits[5]) * 20)).astype(np.float32)
+    logits[6, :] = 0.25
+    logits[6, 250:] = 0.5
+    logits[7] = np.round(logits[7])
+    bias0 = np.zeros_like(bias)
+    for b in (bias0, bias):
+        pick_w, wts_w = orc.topk8(logits, b)
+        host = synth.HostLayer(1301, experts=E, dims=D, width=I, k2=8, only=np.unique(pick_w))
+        ex = moe.Routed(host)
+        sc = moe.Scratch(ex, 1, 8)
+        x = synth.activations(1302, 1, D, "f16")
+        for r in range(logits.shape[0]):
+            _, pick, wts = _run(ea, host, None, sc, ex, x, logits[r:r + 1], b, 1, 0)
+            np.testing.assert_array_equal(pick, pick_w[r:r + 1], err_msg=f"row {r}")
+            np.testing.assert_array_equal(wts, wts_w[r:r + 1], err_msg=f"row {r}")
+
+
 def test_unsupported_width_poisons_output(ea):
     """A width table entry the decode layer has no decoder for (an expert at K2 12 in a layer whose host tables claim
     widths 8..8): the kernels record EA_UNSUPPORTED_WIDTH (19) in the status word, which ea_device_status_address
