@@ -1264,7 +1264,8 @@ __device__ __forceinline__ bool l1_mfma_k2(int k2, const uint32_t* st, const Lan
 }
 
 // A down item's wait for both column blocks of its unit's down inputs: wave 0 polls their slots and moves them to
-// sh.xs; every wave meets at the barrier. True when the wait gave up.
+// sh.xs; every wave meets at the barrier. True when the wait gave up. (Every wave polling, staggered by a quarter
+// round trip, measured slower: the waits are bound by the round trip, not by how often a poll is issued.)
 __device__ __forceinline__ bool l1_down_wait(const DLArgs& a, L1Sh& sh, int u, uint32_t tag, int lane) {
     const int NH = a.I / 128;
     if (threadIdx.x < 64) {
@@ -1289,10 +1290,7 @@ __device__ __forceinline__ bool l1_down_wait(const DLArgs& a, L1Sh& sh, int u, u
 #pragma unroll
         for (int j = 0; j < L1_MAXNH; ++j)
             if (j < NH) reinterpret_cast<uint32_t*>(sh.xs)[j * 64 + lane] = (uint32_t)p[j];
-        if (lane == 0) {
-            sh.flag = timed_out;
-            sh.tag = tag;
-        }
+        if (lane == 0) sh.flag = timed_out;
     }
     __syncthreads();
     return sh.flag;
@@ -1325,6 +1323,7 @@ __device__ __forceinline__ bool l1_down_product(const DLArgs& a, L1Sh& sh, int u
 #pragma unroll
         for (int j = 0; j < 2; ++j) hold(pb[tp][j]);  // decoded before the wait, not after it
     const bool r = l1_down_wait(a, sh, u, tag, lane);
+    __builtin_amdgcn_s_setprio(2);  // the pre-decode ran at the lowest priority, beside the gate|up decode
     const bool row0 = (lane & 15) == 0;
     const uint16_t* xr = sh.xs + 2 * ((lane >> 4) & 3);
 #pragma unroll
@@ -1490,10 +1489,10 @@ __device__ __forceinline__ void l1_epilogue(const DLArgs& a, L1Sh& sh, const Uni
     }
 }
 
-// Down item (unit u, output column block cb) of the row; e0: the epoch thread 0 read. Its outputs go to the tagged
+// Down item (unit u, output column block cb) of the row (sh.tag holds the launch's tag). Its outputs go to the tagged
 // slots ty[u][D]; the last unit's block combines the column block instead.
 template <int CB, int SCB, int NKT>
-__device__ __forceinline__ void l1_down(const DLArgs& a, L1Sh& sh, const UnitView& uv, int u, int cb, uint32_t e0) {
+__device__ __forceinline__ void l1_down(const DLArgs& a, L1Sh& sh, const UnitView& uv, int u, int cb) {
     const int lane = opaque_lane(threadIdx.x & 63), wave = uniform((int)threadIdx.x >> 6);
     const int NH = a.I / 128, KT = a.I / 16, ns = a.D / 16;
     const int nt0 = cb * 8 + 2 * wave;
@@ -1515,7 +1514,7 @@ __device__ __forceinline__ void l1_down(const DLArgs& a, L1Sh& sh, const UnitVie
     stage_issue<NKT>(sp, k2, lane, v);
     issued();
     hold(sd);
-    const uint32_t tag = l1_next((uint32_t)uniform((int)e0));  // meaningful in wave 0 only (lane 0 is thread 0)
+    const uint32_t tag = (uint32_t)uniform((int)sh.tag);  // set by thread 0 before the block's first barrier
     if (wave == 0) {
         if (lane == 0) st_coh(l1_checkin(a) + blockIdx.x, tag);
         if (blockIdx.x == gridDim.x - 1) l1_advance(a, tag, lane);
@@ -1612,10 +1611,12 @@ __global__ void __launch_bounds__(DL_THREADS) __attribute__((amdgpu_waves_per_eu
         uv.shared = a.hs && u == 0;
         if (uv.shared) {
             uv.e = -1;
+            __builtin_amdgcn_s_setprio(2);
             l1_gateup<SCB, true>(a, sh, u, nh, mat, c, e0);
         } else {
             l1_route_self(a, sh, mat, u - a.hs);
             uv.e = uniform(sh.e);
+            __builtin_amdgcn_s_setprio(2);  // the gate|up decode is on the layer's critical path
             l1_gateup<CB, false>(a, sh, u, nh, mat, c, e0);
         }
         if (mat == 1 && c == KC - 1) l1_epilogue(a, sh, uv, u, nh);
@@ -1623,16 +1624,16 @@ __global__ void __launch_bounds__(DL_THREADS) __attribute__((amdgpu_waves_per_eu
     }
     const int d = b - a.U * GU, u = d / DB, cb = d % DB;
     uv.shared = a.hs && u == 0;
-    if (!uv.shared) {
-        // the last unit's block combines the column block: it takes every weight
-        if (wave == 0) l1_route_wait(a, sh, u - a.hs, 2, l1_next((uint32_t)uniform((int)e0)), u == a.U - 1, lane);
-        __syncthreads();
-    }
+    if (threadIdx.x == 0) sh.tag = l1_next(e0);
+    // the last unit's block combines the column block: it takes every weight
+    if (!uv.shared && wave == 0)
+        l1_route_wait(a, sh, u - a.hs, 2, l1_next((uint32_t)uniform((int)e0)), u == a.U - 1, lane);  // lane 0 is thread 0
+    __syncthreads();
     uv.e = uv.shared ? -1 : uniform(sh.e);
     if (a.I == 256)
-        l1_down<CB, SCB, 16>(a, sh, uv, u, cb, e0);
+        l1_down<CB, SCB, 16>(a, sh, uv, u, cb);
     else
-        l1_down<CB, SCB, 8>(a, sh, uv, u, cb, e0);
+        l1_down<CB, SCB, 8>(a, sh, uv, u, cb);
 }
 
 // ---- host side ----------------------------------------------------------------------------------------------------
