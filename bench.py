@@ -604,11 +604,12 @@ def run_prefill(args, torch, np, R: int, steps: int | None = None, warmup: int |
     sc = prompt_experts.Scratch(ex, R, SLOTS)
     s = device.stream()
 
-    def step(i):
-        prompt_experts.run(s, x.data_ptr(), D, dp.data_ptr(), dw.data_ptr(), ex, sc, out.data_ptr(), R,
-                           do_round=False, x_dtype=0)
+    def step(i, stream=None):
+        prompt_experts.run(s if stream is None else stream, x.data_ptr(), D, dp.data_ptr(), dw.data_ptr(), ex, sc,
+                           out.data_ptr(), R, do_round=False, x_dtype=0)
 
     ms = time_steps(step, steps, warmup, torch)
+    graph_ms = time_graph(step, steps, warmup, torch)
     distinct = sorted(set(int(e) for e in pick.reshape(-1)))
     b = sum(lay.expert_bytes(e) for e in distinct) + R * D * 2 + R * D * 4 + R * SLOTS * 8
     f = 2 * R * SLOTS * 3 * D * I
@@ -619,7 +620,11 @@ def run_prefill(args, torch, np, R: int, steps: int | None = None, warmup: int |
                           "routing over 256 4-bit experts", "distinct_experts": len(distinct), "step_bytes": b,
               "step_flops": f, "step_roofline_us": round(max(t_hbm, t_mfma), 3),
               "step_roof_frac": round(max(t_hbm, t_mfma) / us, 4), "step_gbs": round(gbs, 1),
-              "step_tflops": round(tfs, 2), "mfma_frac": round(tfs / FP16_PEAK_TFLOPS, 4)}
+              "step_tflops": round(tfs, 2), "mfma_frac": round(tfs / FP16_PEAK_TFLOPS, 4),
+              "timing": "launched one by one between synchronized events (the two item lists on two streams run "
+                        "side by side)", "graph_us": round(graph_ms * 1e3, 3),
+              "graph_note": "the same layers replayed from a HIP graph: the runtime runs the side stream's branch after "
+                            "the main one, not beside it"}
     roofline = {"kernel": "prompt_experts.run (whole call: route, rot_in, gate|up item GEMMs, epilogue, down item "
                           "GEMMs, combine)", "bound": "hbm" if t_hbm >= t_mfma else "mfma",
                 "achieved": round(gbs, 1) if t_hbm >= t_mfma else round(tfs, 2),
