@@ -497,19 +497,21 @@ __device__ __forceinline__ int member_q(const DLArgs& a, const UnitView& uv, int
 }
 __device__ __forceinline__ int member_row(const UnitView& uv, int m) { return uv.shared ? m : uv.mem[m] / DL_SLOTS; }
 
-// The item's product for one width: prefetch every trellis word, rotate the activations of the k chunk into xs
-// (xs[m][k] = fp16(((x * suh) @ H) * HAD_SCALE), a wave a (row, 128-block)), then the MFMAs.
-template <int CB, int NW>
-__device__ __forceinline__ bool gateup_product(const DLArgs& a, const UnitView& uv, const TileSpan& sp, int k2,
-                                               const uint16_t* suh, int c, uint16_t* xs, uint32_t* st,
-                                               f4v (&acc)[2]) {
-    const int lane = opaque_lane(threadIdx.x & 63), wave = uniform((int)threadIdx.x >> 6);
-    const LaneQuad lq = lane_quad(k2, lane);
-    // activations and suh of this wave's (row, block) tasks, then the trellis: loads complete in order, so the
-    // rotation waits only for the first two while the trellis is in flight. The trellis goes to the wave's LDS region
-    // after the block barrier, so the barrier never waits for it.
-    constexpr int MT = 2 * DL_MAXR / NW;
+// An item's loads in flight: the members' activations and suh of its k chunk (a wave a (row, 128-block) task), then
+// its trellis words.
+template <int NW>
+struct GuFetch {
+    static constexpr int MT = 2 * DL_MAXR / NW;
     uint32_t xv[MT], sv[MT];
+    u4v v[stage_loads<DL_KT>()];
+};
+
+// The item's loads: activations and suh first, then the trellis (loads complete in order, so the rotation waits only
+// for the first ones while the trellis is in flight).
+template <int NW>
+__device__ __forceinline__ void gateup_issue(const DLArgs& a, const UnitView& uv, const TileSpan& sp, int k2,
+                                             const uint16_t* suh, int c, int lane, int wave, GuFetch<NW>& f) {
+    constexpr int MT = GuFetch<NW>::MT;
     const int ntask = 2 * uv.nm;
 #pragma unroll
     for (int i = 0; i < MT; ++i) {
@@ -517,36 +519,56 @@ __device__ __forceinline__ bool gateup_product(const DLArgs& a, const UnitView& 
         const int m = task >> 1, blk = task & 1;
         const int k = c * 256 + blk * 128 + 2 * lane;
         const uint16_t* xr = static_cast<const uint16_t*>(a.x) + (size_t)member_row(uv, m) * a.x_stride;
-        xv[i] = *reinterpret_cast<const uint32_t*>(xr + k);
-        sv[i] = *reinterpret_cast<const uint32_t*>(suh + k);
+        f.xv[i] = *reinterpret_cast<const uint32_t*>(xr + k);
+        f.sv[i] = *reinterpret_cast<const uint32_t*>(suh + k);
     }
-    u4v v[stage_loads<DL_KT>()];
-    stage_issue<DL_KT>(sp, k2, lane, v);
+    stage_issue<DL_KT>(sp, k2, lane, f.v);
     issued();
-#pragma unroll
-    for (int i = 0; i < MT; ++i) {
-        hold(xv[i]);
-        hold(sv[i]);
-    }
+}
+
+// The item's product from its loads: rotate the activations of the k chunk into xs (xs[m][k] = fp16(((x * suh) @ H) *
+// HAD_SCALE)), then, after the block barrier, the trellis into the wave's LDS region and the MFMAs.
+template <int CB, int NW>
+__device__ __forceinline__ bool gateup_consume(const DLArgs& a, const UnitView& uv, int k2, GuFetch<NW>& f,
+                                               uint16_t* xs, uint32_t* st, int lane, int wave, f4v (&acc)[2]) {
+    constexpr int MT = GuFetch<NW>::MT;
+    const LaneQuad lq = lane_quad(k2, lane);
+    const int ntask = 2 * uv.nm;
     const bool bf = a.x_dtype == BF16;
 #pragma unroll
     for (int i = 0; i < MT; ++i) {
         const int task = wave + NW * i;
         if (task < ntask) {
             const int m = task >> 1, blk = task & 1;
-            const uint16_t xl = (uint16_t)(xv[i] & 0xffffu), xh = (uint16_t)(xv[i] >> 16);
+            const uint16_t xl = (uint16_t)(f.xv[i] & 0xffffu), xh = (uint16_t)(f.xv[i] >> 16);
             const float x0 = bf ? bf2f(xl) : h2f(xl);
             const float x1 = bf ? bf2f(xh) : h2f(xh);
-            float v0 = x0 * h2f((uint16_t)(sv[i] & 0xffffu));
-            float v1 = x1 * h2f((uint16_t)(sv[i] >> 16));
+            float v0 = x0 * h2f((uint16_t)(f.sv[i] & 0xffffu));
+            float v1 = x1 * h2f((uint16_t)(f.sv[i] >> 16));
             fwht128_w64(v0, v1, lane);
             *reinterpret_cast<uint32_t*>(xs + m * DL_RS + blk * 128 + 2 * lane) =
                 (uint32_t)f2h(v0 * HAD_SCALE) | ((uint32_t)f2h(v1 * HAD_SCALE) << 16);
         }
     }
     __syncthreads();
-    stage_store<DL_KT>(st, k2, lane, v);
+    stage_store<DL_KT>(st, k2, lane, f.v);
     return mfma_tiles_k2<CB, DL_KT>(k2, st, lq, xs, uv.nm, lane, acc);
+}
+
+// The item's product for one width: its loads, then (the trellis still in flight) the rotation and the MFMAs.
+template <int CB, int NW>
+__device__ __forceinline__ bool gateup_product(const DLArgs& a, const UnitView& uv, const TileSpan& sp, int k2,
+                                               const uint16_t* suh, int c, uint16_t* xs, uint32_t* st,
+                                               f4v (&acc)[2]) {
+    const int lane = opaque_lane(threadIdx.x & 63), wave = uniform((int)threadIdx.x >> 6);
+    GuFetch<NW> f;
+    gateup_issue<NW>(a, uv, sp, k2, suh, c, lane, wave, f);
+#pragma unroll
+    for (int i = 0; i < GuFetch<NW>::MT; ++i) {
+        hold(f.xv[i]);
+        hold(f.sv[i]);
+    }
+    return gateup_consume<CB, NW>(a, uv, k2, f, xs, st, lane, wave, acc);
 }
 
 // The unit of block u as the later launches see it, from the grouping the gate|up launch published. Every field loads
@@ -678,61 +700,131 @@ __global__ void __launch_bounds__(DL_THREADS) epilogue_kernel(DLArgs a) {
 // NW = 2 * DL_WAVES (more than one row, I = 256): the block covers both column blocks of the unit, waves from
 // DL_WAVES on the second (nh is then the wave's), and rotates the members' activations once for both; st is the
 // wave's trellis staging.
-template <int CB, bool SHARED, int NW = DL_WAVES>
-__device__ __forceinline__ void gateup_item(const DLArgs& a, RouteSh& sh, int u, int nh, int mat, int c,
-                                            uint16_t* xs, uint32_t* st) {
-    static_assert(NW == DL_WAVES || NW == 2 * DL_WAVES, "one or both column blocks of 128");
-    const int lane = threadIdx.x & 63, wave = uniform((int)threadIdx.x >> 6);
-    const int KC = a.D / 256, NH = a.I / 128;
-    const int wl = wave & (DL_WAVES - 1);  // the wave within its column block
-    if (NW != DL_WAVES) nh = wave / DL_WAVES;
+// A gate|up item: its unit, the wave's column tiles and where its matrix's tiles are.
+struct GuItem {
     UnitView uv;
-    uv.shared = SHARED;
+    TileSpan sp;
+    int k2, nh, mat, c, wl;
+    const uint16_t* suh;
+};
+template <bool SHARED, int NW>
+__device__ __forceinline__ GuItem gateup_describe(const DLArgs& a, RouteSh& sh, int u, int nh, int mat, int c) {
+    static_assert(NW == DL_WAVES || NW == 2 * DL_WAVES, "one or both column blocks of 128");
+    const int wave = uniform((int)threadIdx.x >> 6);
+    GuItem it;
+    it.wl = wave & (DL_WAVES - 1);  // the wave within its column block
+    if (NW != DL_WAVES) nh = wave / DL_WAVES;
+    it.nh = nh;
+    it.mat = mat;
+    it.c = c;
+    it.uv.shared = SHARED;
     const int ur = u - a.hs;
-    uv.nm = SHARED ? a.R : uniform(sh.mcount[ur]);
-    uv.e = SHARED ? -1 : uniform(sh.uids[ur]);
-    uv.mem = SHARED ? nullptr : sh.members[ur];
+    it.uv.nm = SHARED ? a.R : uniform(sh.mcount[ur]);
+    it.uv.e = SHARED ? -1 : uniform(sh.uids[ur]);
+    it.uv.mem = SHARED ? nullptr : sh.members[ur];
     // wave w: n tiles nh * 8 + 2w, + 1 over the 16 k tiles of chunk c
-    const int nt0 = nh * 8 + 2 * wl, kt0 = c * DL_KT;
-    f4v acc[2] = {f4v{0.f, 0.f, 0.f, 0.f}, f4v{0.f, 0.f, 0.f, 0.f}};
+    const int nt0 = nh * 8 + 2 * it.wl, kt0 = c * DL_KT;
     // matrix D x I: routed in the expert layout (tile (kt, nt) at (kt * I / 16 + nt) * TW words), the shared expert
     // in strips ([I / 128][D / 16][8][TW])
     const int ns = a.I / 16;
-    TileSpan sp;
-    int k2;
-    const uint16_t* suh;
     if constexpr (SHARED) {
-        k2 = a.sh_k2;
-        const int TWB = 16 * k2;  // bytes a tile
-        sp.r = buffer_rsrc(mat ? a.sh_w[1] : a.sh_w[0], (uint32_t)((a.D / 16) * ns * TWB));
-        sp.off = ((nt0 >> 3) * (a.D / 16) * 8 + kt0 * 8 + (nt0 & 7)) * TWB;
-        sp.kstride = 8 * TWB;
-        suh = mat ? a.sh_suh[1] : a.sh_suh[0];
+        it.k2 = a.sh_k2;
+        const int TWB = 16 * it.k2;  // bytes a tile
+        it.sp.r = buffer_rsrc(mat ? a.sh_w[1] : a.sh_w[0], (uint32_t)((a.D / 16) * ns * TWB));
+        it.sp.off = ((nt0 >> 3) * (a.D / 16) * 8 + kt0 * 8 + (nt0 & 7)) * TWB;
+        it.sp.kstride = 8 * TWB;
+        it.suh = mat ? a.sh_suh[1] : a.sh_suh[0];
     } else {
-        k2 = uniform(sh.uk2[ur][mat]);
+        it.k2 = uniform(sh.uk2[ur][mat]);
         const uint32_t* T = uniform(reinterpret_cast<const uint32_t*>(sh.uptr[ur][mat]));
-        const int TWB = 16 * k2;
-        sp.r = buffer_rsrc(T, (uint32_t)((a.D / 16) * ns * TWB));
-        sp.off = (kt0 * ns + nt0) * TWB;
-        sp.kstride = ns * TWB;
-        suh = (mat ? a.suh_u : a.suh_g) + (size_t)uv.e * a.D;
+        const int TWB = 16 * it.k2;
+        it.sp.r = buffer_rsrc(T, (uint32_t)((a.D / 16) * ns * TWB));
+        it.sp.off = (kt0 * ns + nt0) * TWB;
+        it.sp.kstride = ns * TWB;
+        it.suh = (mat ? a.suh_u : a.suh_g) + (size_t)it.uv.e * a.D;
     }
-    const bool ok = gateup_product<CB, NW>(a, uv, sp, k2, suh, c, xs, st, acc);
+    return it;
+}
+
+// The item's partial sums of its chunk: zp[q][nh][mat][c][128] (NaN when the width had no decoder).
+__device__ __forceinline__ void gateup_store(const DLArgs& a, const GuItem& it, bool ok, f4v (&acc)[2], int lane) {
+    const int KC = a.D / 256, NH = a.I / 128;
     if (!ok) {
         if (lane == 0) record_error(a.status, DEV_UNSUPPORTED_WIDTH);
         acc[0] = acc[1] = nan4();
     }
-    // partial sums of this chunk: zp[q][nh][mat][c][128]
 #pragma unroll
     for (int j = 0; j < 2; ++j)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int m = 4 * (lane >> 4) + i;
-            if (m < uv.nm) {
-                const int col = (2 * wl + j) * 16 + (lane & 15);
-                a.lay.zp[((((size_t)member_q(a, uv, m) * NH + nh) * 2 + mat) * KC + c) * 128 + col] = acc[j][i];
+            if (m < it.uv.nm) {
+                const int col = (2 * it.wl + j) * 16 + (lane & 15);
+                a.lay.zp[((((size_t)member_q(a, it.uv, m) * NH + it.nh) * 2 + it.mat) * KC + it.c) * 128 + col] =
+                    acc[j][i];
             }
         }
+}
+
+template <int CB, bool SHARED, int NW = DL_WAVES>
+__device__ __forceinline__ void gateup_item(const DLArgs& a, RouteSh& sh, int u, int nh, int mat, int c,
+                                            uint16_t* xs, uint32_t* st) {
+    const int lane = threadIdx.x & 63;
+    const GuItem it = gateup_describe<SHARED, NW>(a, sh, u, nh, mat, c);
+    f4v acc[2] = {f4v{0.f, 0.f, 0.f, 0.f}, f4v{0.f, 0.f, 0.f, 0.f}};
+    const bool ok = gateup_product<CB, NW>(a, it.uv, it.sp, it.k2, it.suh, c, xs, st, acc);
+    gateup_store(a, it, ok, acc, lane);
+}
+
+// A block's routed items it, it + G, it + 2G, ... (G = gridDim.x) over both column blocks (NW = 2 DL_WAVES), each
+// item's loads issued before the previous item's product runs, so an item's load latency hides behind its
+// predecessor's decode and MFMAs instead of standing between them.
+template <int CB, int NW>
+__device__ __forceinline__ void gateup_routed_pipelined(const DLArgs& a, RouteSh& sh, int it, int items, int units,
+                                                        uint16_t* xs, uint32_t* st, int& dirty) {
+    const int lane = opaque_lane(threadIdx.x & 63), wave = uniform((int)threadIdx.x >> 6);
+    const int KC = a.D / 256, per_unit = 2 * KC, G = (int)gridDim.x;
+    auto valid = [&](int i) { return i < items && i / per_unit < units; };
+    auto describe = [&](int i) {
+        const int rem = i % per_unit;
+        return gateup_describe<false, NW>(a, sh, i / per_unit, 0, rem / KC, rem % KC);
+    };
+    auto run = [&](const GuItem& cur, GuFetch<NW>& f) __attribute__((always_inline)) {
+        const int nm = cur.uv.nm;
+        if (nm < dirty) zero_rows<64 * NW>(xs, nm, dirty);
+        f4v acc[2] = {f4v{0.f, 0.f, 0.f, 0.f}, f4v{0.f, 0.f, 0.f, 0.f}};
+        // the lane id made opaque in every item: the widths' lane constants are then formed in the item, not held
+        // across the loop
+        const int ln = opaque_lane(threadIdx.x & 63);
+        const bool ok = gateup_consume<CB, NW>(a, cur.uv, cur.k2, f, xs, st, ln, wave, acc);
+        gateup_store(a, cur, ok, acc, ln);
+        dirty = nm;
+        __syncthreads();
+    };
+    if (!valid(it)) return;
+    GuFetch<NW> fa, fb;
+    GuItem ca = describe(it), cb;
+    gateup_issue<NW>(a, ca.uv, ca.sp, ca.k2, ca.suh, ca.c, lane, wave, fa);
+    for (;;) {
+        int nx = it + G;
+        bool more = valid(nx);
+        if (more) {
+            cb = describe(nx);
+            gateup_issue<NW>(a, cb.uv, cb.sp, cb.k2, cb.suh, cb.c, lane, wave, fb);
+        }
+        run(ca, fa);
+        if (!more) break;
+        it = nx;
+        nx = it + G;
+        more = valid(nx);
+        if (more) {
+            ca = describe(nx);
+            gateup_issue<NW>(a, ca.uv, ca.sp, ca.k2, ca.suh, ca.c, lane, wave, fa);
+        }
+        run(cb, fb);
+        if (!more) break;
+        it = nx;
+    }
 }
 
 template <int CB, int SCB>
@@ -790,7 +882,7 @@ gateup_kernel(DLArgs a) {
 // waves, the routing read from route_kernel's output. Each item rotates its members' activations once for both column
 // blocks (a block of DL_WAVES waves per column block rotates them twice).
 template <int CB, int SCB>
-__global__ void __launch_bounds__(2 * DL_THREADS) __attribute__((amdgpu_waves_per_eu(2)))
+__global__ void __launch_bounds__(2 * DL_THREADS) __attribute__((amdgpu_waves_per_eu(4)))
 gateup_wide_kernel(DLArgs a) {
     constexpr int NW = 2 * DL_WAVES, NT = 64 * NW;
     __shared__ RouteSh sh;
@@ -811,16 +903,7 @@ gateup_wide_kernel(DLArgs a) {
     }
     if (it >= items) return;
     route_read(a, sh);
-    const int units = a.hs + sh.ucount;
-    for (; it < items; it += gridDim.x) {
-        const int u = it / per_unit, rem = it % per_unit;
-        if (u >= units) break;
-        const int nm = sh.mcount[u - a.hs];
-        if (nm < dirty) zero_rows<NT>(xs, nm, dirty);
-        gateup_item<CB, false, NW>(a, sh, u, 0, rem / KC, rem % KC, xs, st);
-        dirty = nm;
-        __syncthreads();
-    }
+    gateup_routed_pipelined<CB, NW>(a, sh, it, items, a.hs + sh.ucount, xs, st, dirty);
 }
 
 // ---- down ---------------------------------------------------------------------------------------------------------
