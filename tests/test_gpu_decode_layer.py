@@ -2,8 +2,8 @@
 routed experts, the shared expert's mlp and their sum) is checked against the oracle's composition of the same
 reference steps (forward.zig:2361-2403): ops.topk -> moe.routed -> gate / up EXL3 linears with bf16 outputs ->
 swiglu2 -> down linear (fp32) -> addF32. pick / wts must match bit for bit; out within 2e-3 * RMS(out), the north
-star's bar. Calls repeat on one scratch with changing row counts, which exercises the launch-generation flags and
-the counters the kernel leaves at zero."""
+star's bar. Calls repeat on one scratch with changing row counts, layer shapes and epochs, which exercises the
+one-launch layer's tagged hand-off slots (a new tag every launch, never a cleared slot)."""
 import numpy as np
 import pytest
 
@@ -214,6 +214,65 @@ def test_topk8_nan_policy_both_paths(ea):
         _, pick, wts = _run(ea, host, None, sc, ex, x, lg, bias, rows, 0)
         np.testing.assert_array_equal(pick, pick_w if rows == R else pick_w[2:3])
         np.testing.assert_array_equal(wts, wts_w if rows == R else wts_w[2:3])
+
+
+def _epoch_word(sc):
+    """The one-row launch's epoch word: the first word of the scratch's decode-layer region."""
+    return sc.c.fused - sc.buf.data_ptr()
+
+
+def test_one_row_epoch_wraps(ea):
+    """The epoch word set just below its wrap: three launches tag with 0xFFFFFFFF, then 1 (0, a cleared slot's tag, is
+    skipped), then 2; each launch's output meets the oracle, and the word holds the last launch's tag."""
+    device, linear, moe, synth = ea
+    E, D, I = 256, 1024, 128
+    logits_list, bias = [], None
+    for i in range(3):
+        l, b = synth.logits(1400 + i, 1)
+        bias = b if bias is None else bias
+        logits_list.append(l)
+    host = _layer_for(synth, 1410, logits_list, bias, E, D, I, 8, 1)
+    shared = SharedHost(linear, synth, 1420, D, I, 8, 1)
+    ex = moe.Routed(host)
+    sc = moe.Scratch(ex, 1, 8)
+    off = _epoch_word(sc)
+    torch.cuda.synchronize()
+    sc.buf[off:off + 4] = torch.tensor([0xFE, 0xFF, 0xFF, 0xFF], dtype=torch.uint8, device="cuda")
+    tags = []
+    for i in range(3):
+        x = synth.activations(1430 + i, 1, D, "f16")
+        out, pick, wts = _run(ea, host, shared, sc, ex, x, logits_list[i], bias, 1, 0)
+        want, pick_w, wts_w = _want(host, shared, x, logits_list[i], bias, 1, False)
+        np.testing.assert_array_equal(pick, pick_w)
+        assert_close_rms(out, want, 2e-3, f"launch {i} across the epoch's wrap")
+        tags.append(int(sc.buf[off:off + 4].cpu().numpy().view(np.uint32)[0]))
+    assert tags == [0xFFFFFFFF, 1, 2], tags
+
+
+def test_one_row_scratch_across_layer_shapes(ea):
+    """One scratch (made for the larger layer) used by two layer shapes in turn, D 2048 / I 256 and D 1024 / I 128: the
+    tagged slots sit at the same offsets for every shape and a slot's tag half only ever holds tags, so no launch
+    takes another shape's stale values for its own."""
+    device, linear, moe, synth = ea
+    E = 256
+    layers = []
+    for j, (D, I) in enumerate(((2048, 256), (1024, 128))):
+        ls, bias = [], None
+        for i in range(2):
+            l, b = synth.logits(1500 + 10 * j + i, 1)
+            bias = b if bias is None else bias
+            ls.append(l)
+        host = _layer_for(synth, 1520 + j, ls, bias, E, D, I, 8, 1)
+        layers.append((D, I, host, moe.Routed(host), SharedHost(linear, synth, 1530 + j, D, I, 8, 1), ls, bias))
+    sc = moe.Scratch(layers[0][3], 1, 8)
+    for n, j in enumerate((0, 1, 0, 1)):
+        D, I, host, ex, shared, ls, bias = layers[j]
+        x = synth.activations(1540 + n, 1, D, "f16")
+        lg = ls[n // 2]
+        out, pick, wts = _run(ea, host, shared, sc, ex, x, lg, bias, 1, 0)
+        want, pick_w, wts_w = _want(host, shared, x, lg, bias, 1, False)
+        np.testing.assert_array_equal(pick, pick_w)
+        assert_close_rms(out, want, 2e-3, f"call {n}: D {D}, I {I}")
 
 
 def test_one_row_topk_ties_and_wide_spread(ea):
