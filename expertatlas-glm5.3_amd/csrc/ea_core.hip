@@ -207,8 +207,8 @@ int ea_fini(void) {
     std::lock_guard<std::mutex> lk(g_mu);
     for (auto& c : g_ctx)
         if (c.ready) {
-            hipSetDevice(c.device);
-            hipFree(c.status);
+            (void)hipSetDevice(c.device);
+            (void)hipFree(c.status);
             c.status = nullptr;
             if (c.side) (void)hipStreamDestroy(c.side);
             if (c.fork) (void)hipEventDestroy(c.fork);
