@@ -238,19 +238,21 @@ __global__ void __launch_bounds__(NW * 64) grouped_kernel(
 // ---- gate/up epilogue -----------------------------------------------------------------------------------------
 // Wave (pair p, 128-block): splits summed in order, FWHT, * HAD_SCALE * svh, SwiGLU (act_mode 0: bf16 roundings,
 // 1: fp32; limit clamps), * suh_d, FWHT, xd = fp16(* HAD_SCALE) (exl3_experts.cu:142-184). A pair marked in pclass
-// takes its splits from Z's split 0 and Zp's planes ([SKP - 1][2][P][N]), in split order.
+// takes its splits from Z's split 0 and Zp's planes ([SKP - 1][2][P][N]), in split order. With only >= 0 a pair
+// whose class (pclass[p] != 0) is not `only` is left alone.
 __global__ void __launch_bounds__(64) gateup_epilogue_kernel(const float* __restrict__ Z, const int* __restrict__ pick,
                                                              const uint16_t* __restrict__ svh_g,
                                                              const uint16_t* __restrict__ svh_u,
                                                              const uint16_t* __restrict__ suh_d,
                                                              uint16_t* __restrict__ xd, int P, int N, int SK, int E,
                                                              float limit, int act_mode, const int* __restrict__ pclass,
-                                                             const float* __restrict__ Zp, int SKP) {
+                                                             const float* __restrict__ Zp, int SKP, int only) {
     const int p = blockIdx.x, blk = blockIdx.y, lane = threadIdx.x;
     const int e = pick[p];
     if (e < 0 || e >= E) return;
     const int n = blk * 128 + 2 * lane;
     const bool part = pclass && pclass[p];
+    if (only >= 0 && (int)part != only) return;
     float g[2], u[2];
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
@@ -442,14 +444,14 @@ int launch_grouped(hipStream_t s, const ea_grouped_args& a) {
 int launch_gateup_epilogue(hipStream_t s, const float* z, const int* pick, const uint16_t* svh_g,
                            const uint16_t* svh_u, const uint16_t* suh_d, uint16_t* xd, uint32_t rows, uint32_t p,
                            uint32_t n, uint32_t sk, uint32_t slots, uint32_t experts, float limit, uint32_t act_mode,
-                           const int* pclass, const float* zp, uint32_t skp) {
+                           const int* pclass, const float* zp, uint32_t skp, int only) {
     EA_REQUIRE_CTX(c);
     if (n % 128 != 0) return EA_BAD_WIDTH;
     if (!z || !pick || !svh_g || !svh_u || !suh_d || !xd) return EA_BAD_ARGUMENT;
     if (rows * slots == 0 || n == 0) return EA_OK;
     dim3 grid(rows * slots, n / 128);
     gateup_epilogue_kernel<<<grid, 64, 0, s>>>(z, pick, svh_g, svh_u, suh_d, xd, (int)p, (int)n, (int)sk,
-                                               (int)experts, limit, (int)act_mode, pclass, zp, (int)skp);
+                                               (int)experts, limit, (int)act_mode, pclass, zp, (int)skp, only);
     return launched();
 }
 

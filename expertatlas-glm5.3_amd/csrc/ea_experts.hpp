@@ -15,11 +15,12 @@ int launch_rot_in(hipStream_t s, const void* x, int x_dtype, uint32_t x_stride, 
                   uint32_t experts);
 int launch_grouped(hipStream_t s, const ea_grouped_args& a);
 // With pclass: a pair with pclass[pair] != 0 sums z's split 0 and then zp's planes 1 .. skp - 1 ([skp - 1][2][p][n])
-// instead of z's sk splits.
+// instead of z's sk splits; only >= 0 (with pclass) takes just the pairs of that class (0 or 1).
 int launch_gateup_epilogue(hipStream_t s, const float* z, const int* pick, const uint16_t* svh_g,
                            const uint16_t* svh_u, const uint16_t* suh_d, uint16_t* xd, uint32_t rows, uint32_t p,
                            uint32_t n, uint32_t sk, uint32_t slots, uint32_t experts, float limit, uint32_t act_mode,
-                           const int* pclass = nullptr, const float* zp = nullptr, uint32_t skp = 1);
+                           const int* pclass = nullptr, const float* zp = nullptr, uint32_t skp = 1,
+                           int only = -1);
 int launch_down_combine(hipStream_t s, const float* z, const int* pick, const uint16_t* svh_d, float* y,
                         const float* wts, float* out, uint32_t rows, uint32_t p, uint32_t d, uint32_t sk,
                         uint32_t slots, uint32_t experts, bool skip_invalid = false);

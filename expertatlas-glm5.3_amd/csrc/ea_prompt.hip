@@ -795,61 +795,76 @@ static void item_gemm(hipStream_t s, const uint16_t* X0, const uint16_t* X1, con
                                                                        Z, K, N, P, big, (int)max_items, status);
 }
 
-// Both item lists at once: the larger items on the side stream, the small ones on s (the two kernels fill each
-// other's idle CUs: the small items' blocks leave room on many CUs, the larger items' blocks are few and long). The
-// down matrix takes the resident-activation kernels when its K and N fit, anything else the chunked ones, with the
-// larger items' K split into Zp when Zp is given.
+// What one item list's pass reads and writes: the rotated activations, the three matrices' trellis tables and
+// widths, the items, the pair classes and the per-pair planes (z and zp: gate|up partial sums, xd: down inputs,
+// plane: down outputs). The two lists' pairs are disjoint, so their passes touch disjoint rows of every plane.
+struct ListPass {
+    const uint16_t *xg, *xu;
+    const int64_t* tp[3];
+    const int* k2[3];
+    const int *sorted, *items, *count, *pclass, *pick;
+    const uint16_t *svh_g, *svh_u, *suh_d;
+    float *z, *zp, *plane;
+    uint16_t* xd;
+    int D, I, P, rows, slots, E, mi;
+    int* status;
+};
+
+// One item list from its gate|up product to its down product, in order on q: big = 1 takes the larger items (the
+// gate|up K split into zp; the down matrix by blocks of DNG_BIG column blocks), big = 0 the items of at most
+// SMALL_ROWS pairs (the ring kernel; DNG column blocks). The down matrix takes the resident-activation kernel when
+// its K and N fit, the chunked ones otherwise. The two lists run on two streams: the small items' blocks leave room
+// on many CUs, the larger items' blocks are few and long, and each list's down product starts when its own
+// epilogue is done.
 template <int CB>
-static int item_gemm_staged(hipStream_t s, const uint16_t* X0, const uint16_t* X1, const int64_t* TP0,
-                            const int64_t* TP1, const int* B0, const int* B1, const int* sorted, const int* items,
-                            const int* count, float* Z, float* Zp, int K, int N, int P, int mats, uint32_t max_items,
-                            int* status) {
-    const int mi = (int)max_items;
-    if (mats == 1 && K <= 2 * PK * 16 && (N / 128) % DNG == 0) {  // the down matrix
-        return fork_join(
-            s,
-            [&](hipStream_t q) {
-                item_dn_kernel<CB, IPM_TILES, DNG_BIG><<<dim3(max_items, N / 128 / DNG_BIG, 1), PW * 64, 0, q>>>(
-                    X0, TP0, B0, sorted, items, count, Z, K, N, P, mi, status);
-                return launched();
-            },
-            [&](hipStream_t q) {
-                item_dn_kernel<CB, SMALL_ROWS / 16, DNG><<<dim3(max_items, N / 128 / DNG, 1), PW * 64, 0, q>>>(
-                    X0, TP0, B0, sorted, items, count, Z, K, N, P, mi, status);
-                return launched();
-            });
+static int list_pass(hipStream_t q, const ListPass& a, int big) {
+    const int ns = gu_splits(a.D);
+    if (big)
+        item_gu_kernel<CB><<<dim3(a.mi, a.I / (16 * 2 * PW), 2 * ns), PW * 64, 0, q>>>(
+            a.xg, a.xu, a.tp[0], a.tp[1], a.k2[0], a.k2[1], a.sorted, a.items, a.count, a.z, a.zp, a.D, a.I, a.P, ns,
+            a.mi, a.status);
+    else  // blocks of 4 waves over 128 columns (8 waves over 256 measured 1 % slower at 512 rows, the same at 2048)
+        item_ring_kernel<CB, 4><<<dim3(a.mi, a.I / 128, 2), 4 * 64, 0, q>>>(
+            a.xg, a.xu, a.tp[0], a.tp[1], a.k2[0], a.k2[1], a.sorted, a.items, a.count, a.z, a.D, a.I, a.P, ns, a.mi,
+            a.status);
+    int r = launched();
+    if (r) return r;
+    r = launch_gateup_epilogue(q, a.z, a.pick, a.svh_g, a.svh_u, a.suh_d, a.xd, (uint32_t)a.rows, (uint32_t)a.P,
+                               (uint32_t)a.I, 1, (uint32_t)a.slots, (uint32_t)a.E, __builtin_inff(), 1, a.pclass, a.zp,
+                               (uint32_t)ns, big);
+    if (r) return r;
+    if (a.I <= 2 * PK * 16 && (a.D / 128) % DNG == 0) {
+        if (big)
+            item_dn_kernel<CB, IPM_TILES, DNG_BIG><<<dim3(a.mi, a.D / 128 / DNG_BIG, 1), PW * 64, 0, q>>>(
+                a.xd, a.tp[2], a.k2[2], a.sorted, a.items, a.count, a.plane, a.I, a.D, a.P, a.mi, a.status);
+        else
+            item_dn_kernel<CB, SMALL_ROWS / 16, DNG><<<dim3(a.mi, a.D / 128 / DNG, 1), PW * 64, 0, q>>>(
+                a.xd, a.tp[2], a.k2[2], a.sorted, a.items, a.count, a.plane, a.I, a.D, a.P, a.mi, a.status);
+    } else if (big) {
+        item_gu_kernel<CB><<<dim3(a.mi, a.D / (16 * 2 * PW), 1), PW * 64, 0, q>>>(
+            a.xd, a.xd, a.tp[2], a.tp[2], a.k2[2], a.k2[2], a.sorted, a.items, a.count, a.plane, nullptr, a.I, a.D,
+            a.P, 1, a.mi, a.status);
+    } else {
+        item_ring_kernel<CB, 4><<<dim3(a.mi, a.D / 128, 1), 4 * 64, 0, q>>>(
+            a.xd, a.xd, a.tp[2], a.tp[2], a.k2[2], a.k2[2], a.sorted, a.items, a.count, a.plane, a.I, a.D, a.P, 1,
+            a.mi, a.status);
     }
-    const int ns = Zp ? gu_splits(K) : 1;
-    return fork_join(
-        s,
-        [&](hipStream_t q) {
-            item_gu_kernel<CB><<<dim3(max_items, N / (16 * 2 * PW), mats * ns), PW * 64, 0, q>>>(
-                X0, X1, TP0, TP1, B0, B1, sorted, items, count, Z, Zp, K, N, P, ns, mi, status);
-            return launched();
-        },
-        [&](hipStream_t q) {
-            // blocks of 4 waves over 128 columns (8 waves over 256 measured 1 % slower at 512 rows, the same at 2048)
-            item_ring_kernel<CB, 4><<<dim3(max_items, N / 128, mats), 4 * 64, 0, q>>>(
-                X0, X1, TP0, TP1, B0, B1, sorted, items, count, Z, K, N, P, ns, mi, status);
-            return launched();
-        });
+    return launched();
 }
 
-// Widths up to 10 take the staged GEMM; wider ones (three trellis words a lane) the register-streaming one.
-static int item_gemm_dispatch(hipStream_t s, uint32_t cb, bool wide, const uint16_t* X0, const uint16_t* X1,
-                              const int64_t* TP0, const int64_t* TP1, const int* B0, const int* B1, const int* sorted,
-                              const int* items, const int* count, float* Z, float* Zp, int K, int N, int P, int mats,
-                              uint32_t max_items, int* status) {
-    if (!wide) {
-        if (cb == 1)
-            return item_gemm_staged<1>(s, X0, X1, TP0, TP1, B0, B1, sorted, items, count, Z, Zp, K, N, P, mats,
-                                       max_items, status);
-        if (cb == 2)
-            return item_gemm_staged<2>(s, X0, X1, TP0, TP1, B0, B1, sorted, items, count, Z, Zp, K, N, P, mats,
-                                       max_items, status);
-        return item_gemm_staged<0>(s, X0, X1, TP0, TP1, B0, B1, sorted, items, count, Z, Zp, K, N, P, mats, max_items,
-                                   status);
-    }
+// Both lists at once: the larger items on the side stream, the small ones on s, joined once before the combine.
+static int list_passes(hipStream_t s, uint32_t cb, const ListPass& a) {
+    auto pass = [&](hipStream_t q, int big) {
+        return cb == 1 ? list_pass<1>(q, a, big) : cb == 2 ? list_pass<2>(q, a, big) : list_pass<0>(q, a, big);
+    };
+    return fork_join(
+        s, [&](hipStream_t q) { return pass(q, 1); }, [&](hipStream_t q) { return pass(q, 0); });
+}
+
+// Widths above 10 (three trellis words a lane): the register-streaming GEMM, both lists in turn on s.
+static void wide_gemm(hipStream_t s, uint32_t cb, const uint16_t* X0, const uint16_t* X1, const int64_t* TP0,
+                      const int64_t* TP1, const int* B0, const int* B1, const int* sorted, const int* items,
+                      const int* count, float* Z, int K, int N, int P, int mats, uint32_t max_items, int* status) {
     if (cb == 1) {
         item_gemm<1, 2, 16>(s, X0, X1, TP0, TP1, B0, B1, sorted, items, count, Z, K, N, P, mats, max_items, status);
     } else if (cb == 2) {
@@ -857,7 +872,6 @@ static int item_gemm_dispatch(hipStream_t s, uint32_t cb, bool wide, const uint1
     } else {
         item_gemm<0, 2, 16>(s, X0, X1, TP0, TP1, B0, B1, sorted, items, count, Z, K, N, P, mats, max_items, status);
     }
-    return launched();
 }
 
 }  // namespace ea
@@ -945,23 +959,54 @@ int ea_prompt_experts_run(ea_stream_t stream, const void* x, int x_dtype, uint32
         r = launch_rot_in(s, xs, x_dtype, xstride, pk, dptr<const uint16_t>(ex->suh_g), dptr<const uint16_t>(ex->suh_u),
                           dptr<uint16_t>(sc->xg), dptr<uint16_t>(sc->xu), n, D, S, E);
         if (r) return r;
-        r = item_gemm_dispatch(s, ex->cb, wide, dptr<const uint16_t>(sc->xg), dptr<const uint16_t>(sc->xu),
-                           dptr<const int64_t>(ex->ptr[0]), dptr<const int64_t>(ex->ptr[1]),
-                           dptr<const int>(ex->k2[0]), dptr<const int>(ex->k2[1]), dptr<const int>(sc->sorted),
-                           dptr<const int>(sc->items), dptr<const int>(sc->count), dptr<float>(sc->z),
-                           wide ? nullptr : dptr<float>(sc->zp), (int)D, (int)I, (int)pairs, 2, max_items, c->status);
-        if (r) return r;
-        r = launch_gateup_epilogue(s, dptr<const float>(sc->z), pk, dptr<const uint16_t>(ex->svh_g),
-                                   dptr<const uint16_t>(ex->svh_u), dptr<const uint16_t>(ex->suh_d),
-                                   dptr<uint16_t>(sc->xd), n, pairs, I, 1, S, E, __builtin_inff(), 1,
-                                   wide ? nullptr : dptr<const int>(sc->pclass), dptr<const float>(sc->zp),
-                                   (uint32_t)gu_splits((int)D));
-        if (r) return r;
-        r = item_gemm_dispatch(s, ex->cb, wide, dptr<const uint16_t>(sc->xd), dptr<const uint16_t>(sc->xd),
-                           dptr<const int64_t>(ex->ptr[2]), dptr<const int64_t>(ex->ptr[2]),
-                           dptr<const int>(ex->k2[2]), dptr<const int>(ex->k2[2]), dptr<const int>(sc->sorted),
-                           dptr<const int>(sc->items), dptr<const int>(sc->count), dptr<float>(sc->plane), nullptr,
-                           (int)I, (int)D, (int)pairs, 1, max_items, c->status);
+        if (!wide) {
+            ListPass a{};
+            a.xg = dptr<const uint16_t>(sc->xg);
+            a.xu = dptr<const uint16_t>(sc->xu);
+            for (int m = 0; m < 3; ++m) {
+                a.tp[m] = dptr<const int64_t>(ex->ptr[m]);
+                a.k2[m] = dptr<const int>(ex->k2[m]);
+            }
+            a.sorted = dptr<const int>(sc->sorted);
+            a.items = dptr<const int>(sc->items);
+            a.count = dptr<const int>(sc->count);
+            a.pclass = dptr<const int>(sc->pclass);
+            a.pick = pk;
+            a.svh_g = dptr<const uint16_t>(ex->svh_g);
+            a.svh_u = dptr<const uint16_t>(ex->svh_u);
+            a.suh_d = dptr<const uint16_t>(ex->suh_d);
+            a.z = dptr<float>(sc->z);
+            a.zp = dptr<float>(sc->zp);
+            a.plane = dptr<float>(sc->plane);
+            a.xd = dptr<uint16_t>(sc->xd);
+            a.D = (int)D;
+            a.I = (int)I;
+            a.P = (int)pairs;
+            a.rows = (int)n;
+            a.slots = (int)S;
+            a.E = (int)E;
+            a.mi = (int)max_items;
+            a.status = c->status;
+            r = list_passes(s, ex->cb, a);
+        } else {
+            wide_gemm(s, ex->cb, dptr<const uint16_t>(sc->xg), dptr<const uint16_t>(sc->xu),
+                      dptr<const int64_t>(ex->ptr[0]), dptr<const int64_t>(ex->ptr[1]), dptr<const int>(ex->k2[0]),
+                      dptr<const int>(ex->k2[1]), dptr<const int>(sc->sorted), dptr<const int>(sc->items),
+                      dptr<const int>(sc->count), dptr<float>(sc->z), (int)D, (int)I, (int)pairs, 2, max_items,
+                      c->status);
+            r = launched();
+            if (r) return r;
+            r = launch_gateup_epilogue(s, dptr<const float>(sc->z), pk, dptr<const uint16_t>(ex->svh_g),
+                                       dptr<const uint16_t>(ex->svh_u), dptr<const uint16_t>(ex->suh_d),
+                                       dptr<uint16_t>(sc->xd), n, pairs, I, 1, S, E, __builtin_inff(), 1);
+            if (r) return r;
+            wide_gemm(s, ex->cb, dptr<const uint16_t>(sc->xd), dptr<const uint16_t>(sc->xd),
+                      dptr<const int64_t>(ex->ptr[2]), dptr<const int64_t>(ex->ptr[2]), dptr<const int>(ex->k2[2]),
+                      dptr<const int>(ex->k2[2]), dptr<const int>(sc->sorted), dptr<const int>(sc->items),
+                      dptr<const int>(sc->count), dptr<float>(sc->plane), (int)I, (int)D, (int)pairs, 1, max_items,
+                      c->status);
+            r = launched();
+        }
         if (r) return r;
         // slots without an expert add nothing (the reference's route skips them); fp16 sums go through an fp32
         // staging buffer (xg, free by now)
