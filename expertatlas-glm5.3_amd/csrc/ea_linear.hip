@@ -147,11 +147,24 @@ __global__ void __launch_bounds__(WK * 64) linear_kernel(ea_jobs jobs, int M, in
 // then splits, exl3_linear.cu:231-484) over four times as many blocks as its (column block, split) grid. With ROT
 // the block rotates the activations of its split itself (the Hadamard blocks its k range touches) and the column
 // group 0 blocks also store them to xh, as the separate rotation would.
+//
+// Tagged form (TAG; the split count even, at most 2 LS_MAXTS, and the block's LDS within bounds): the caller's Z
+// (fp32 [SK, M, N]) holds SK / 2 splits of 8-byte slots instead, each block twice the k range on twice the waves, and
+// a block stores each sum with the tag LS_TAG in the slot's high half in one 8-byte agent-scope store; the
+// finisher polls the slots themselves until every tag is LS_TAG, adds the splits in order, and stores zero into every
+// slot it read. So a writer never waits for its stores, and the finisher needs one round trip once the data has
+// landed, where the flag form needs the writer's store acknowledgement, the flag's round trip and then a second
+// round trip for the data. The tag is a signalling-NaN bit pattern: no fp32 result has it (arithmetic quiets NaNs),
+// so partial sums the flag form left in the same buffer are never taken for tagged slots, and Z needs no clearing
+// between the two forms. A Z buffer must not hold the tag when first used (zero, as the counters start, is fine).
 constexpr int LS_MAXR = 16;
 constexpr int LS_MAXNKT = 16;
 constexpr int LS_FLAGS = 32;  // flag bytes a 128-column block has in the counters (int32 [8 N / 128], zero between calls)
+constexpr int LS_MAXTS = 8;   // tagged splits the finisher polls at once (two slots a lane each)
+constexpr uint32_t LS_TAG = 0x7FB5EA1Du;
+constexpr int LS_POLLS = 1 << 20;  // polls before the finisher gives up (tens of milliseconds)
 
-template <int CB, int K2, int NKT, bool ROT, int XL>
+template <int CB, int K2, int NKT, bool ROT, int XL, bool TAG>
 __global__ void __launch_bounds__(512) lin_small_kernel(ea_jobs jobs, ea_rot_jobs rj, int M, int K, const void* x,
                                                         int x_bf16, int* status) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
@@ -267,6 +280,70 @@ __global__ void __launch_bounds__(512) lin_small_kernel(ea_jobs jobs, ea_rot_job
 #pragma unroll
         for (int i = 0; i < 4; ++i) red[(wave * 16 + 4 * (lane >> 4) + i) * 32 + j * 16 + row] = acc[j][i];
     __syncthreads();
+    if constexpr (TAG) {
+        // the block's sums into its tagged slots; the finisher keeps its own in red's first rows (its slots are
+        // never written, so nothing it does not read carries the tag)
+        uint64_t* Zt = dptr<uint64_t>(J.Z);
+        for (int idx = threadIdx.x; idx < M * 32; idx += WK * 64) {
+            const int m = idx >> 5, c = idx & 31;
+            float sum = red[m * 32 + c];
+            for (int w = 1; w < WK; ++w) sum += red[(w * 16 + m) * 32 + c];
+            red[m * 32 + c] = sum;
+            if (!finisher)
+                __hip_atomic_store(Zt + ((size_t)split * M + m) * N + g * 32 + c,
+                                   ((uint64_t)LS_TAG << 32) | __float_as_uint(sum), __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+        }
+        if (!finisher) return;
+        __syncthreads();
+        // the finisher: a wave a row, two columns a lane; its own split's slots of its own 32 columns (lanes 48..63)
+        // come from red, the others are polled; every read slot is set back to zero
+        const bool own = lane >= 48;
+        for (int m = wave; m < M; m += WK) {
+            uint64_t p[LS_MAXTS][2];
+            bool timed_out = false;
+            for (int n = 0;; ++n) {
+                bool ok = true;
+#pragma unroll
+                for (int q = 0; q < LS_MAXTS; ++q)
+                    if (q < SK && !(own && q == SK - 1)) {
+                        const uint64_t* at = Zt + ((size_t)q * M + m) * N + col;
+                        p[q][0] = __hip_atomic_load(at, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        p[q][1] = __hip_atomic_load(at + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        ok &= (uint32_t)(p[q][0] >> 32) == LS_TAG && (uint32_t)(p[q][1] >> 32) == LS_TAG;
+                    }
+                if (__builtin_amdgcn_ballot_w64(!ok) == 0) break;
+                if (n >= LS_POLLS) {
+                    timed_out = true;
+                    if (lane == 0) record_error(status, DEV_SYNC_TIMEOUT);
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(1);
+            }
+            if (own) {
+                const int c = 2 * lane - 96;
+                p[SK - 1][0] = __float_as_uint(red[m * 32 + c]);
+                p[SK - 1][1] = __float_as_uint(red[m * 32 + c + 1]);
+            }
+            float2 acc2 = float2{__uint_as_float((uint32_t)p[0][0]), __uint_as_float((uint32_t)p[0][1])};
+#pragma unroll
+            for (int q = 1; q < LS_MAXTS; ++q)
+                if (q < SK) {
+                    acc2.x += __uint_as_float((uint32_t)p[q][0]);
+                    acc2.y += __uint_as_float((uint32_t)p[q][1]);
+                }
+            for (int q = 0; q < SK; ++q)
+                if (!(own && q == SK - 1)) {
+                    uint64_t* at = Zt + ((size_t)q * M + m) * N + col;
+                    __hip_atomic_store(at, (uint64_t)0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    __hip_atomic_store(at + 1, (uint64_t)0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
+            if (timed_out) acc2 = float2{__builtin_nanf(""), __builtin_nanf("")};  // a writer never arrived
+            finish_store_pre(acc2.x, acc2.y, lane, svw, bias != nullptr, bw, dptr<void>(J.y), J.y_dtype,
+                             (size_t)m * N + col);
+        }
+        return;
+    }
     float* Z = dptr<float>(J.Z);
     for (int idx = threadIdx.x; idx < M * 32; idx += WK * 64) {
         const int m = idx >> 5, c = idx & 31;
@@ -334,19 +411,19 @@ static size_t lin_small_lds(int M, int K2, int NKT, int WK, bool rot) {
     return xs + (stage > red ? stage : red);
 }
 
-template <int CB, int K2, bool ROT, int XL>
+template <int CB, int K2, bool ROT, int XL, bool TAG>
 static void launch_small_xl(const ea_jobs& jobs, const ea_rot_jobs& rj, int blocks, hipStream_t s, int M, int K, int wk,
                             int nkt, const void* x, int x_bf16, size_t lds, int* status) {
-#define EA_LS(NKT_)                                                                                              \
-    if (nkt == NKT_) {                                                                                           \
-        lin_small_kernel<CB, K2, NKT_, ROT, XL><<<blocks, wk * 64, lds, s>>>(jobs, rj, M, K, x, x_bf16, status); \
-        return;                                                                                                  \
+#define EA_LS(NKT_)                                                                                                   \
+    if (nkt == NKT_) {                                                                                                \
+        lin_small_kernel<CB, K2, NKT_, ROT, XL, TAG><<<blocks, wk * 64, lds, s>>>(jobs, rj, M, K, x, x_bf16, status); \
+        return;                                                                                                       \
     }
     EA_LS(2) EA_LS(4) EA_LS(6) EA_LS(8) EA_LS(10) EA_LS(12) EA_LS(14) EA_LS(16)
 #undef EA_LS
 }
 
-template <int CB, int K2, bool ROT>
+template <int CB, int K2, bool ROT, bool TAG>
 static bool launch_small_k2(const ea_jobs& jobs, const ea_rot_jobs& rj, int blocks, hipStream_t s, int M, int K,
                             int wk, int nkt, const void* x, int x_bf16, int* status) {
     const size_t lds = lin_small_lds(M, K2, nkt, wk, ROT);
@@ -354,12 +431,22 @@ static bool launch_small_k2(const ea_jobs& jobs, const ea_rot_jobs& rj, int bloc
     // 16-byte activation loads a thread: the rows' span over the block's threads
     const int kh = nkt * wk * 16, span_max = ROT ? kh + 256 : kh;
     const int xl = (M * (span_max / 8) + wk * 64 - 1) / (wk * 64);
-    if (xl <= 1) launch_small_xl<CB, K2, ROT, 1>(jobs, rj, blocks, s, M, K, wk, nkt, x, x_bf16, lds, status);
-    else if (xl <= 2) launch_small_xl<CB, K2, ROT, 2>(jobs, rj, blocks, s, M, K, wk, nkt, x, x_bf16, lds, status);
-    else if (xl <= 4) launch_small_xl<CB, K2, ROT, 4>(jobs, rj, blocks, s, M, K, wk, nkt, x, x_bf16, lds, status);
-    else if (xl <= 8) launch_small_xl<CB, K2, ROT, 8>(jobs, rj, blocks, s, M, K, wk, nkt, x, x_bf16, lds, status);
+    if (xl <= 1) launch_small_xl<CB, K2, ROT, 1, TAG>(jobs, rj, blocks, s, M, K, wk, nkt, x, x_bf16, lds, status);
+    else if (xl <= 2) launch_small_xl<CB, K2, ROT, 2, TAG>(jobs, rj, blocks, s, M, K, wk, nkt, x, x_bf16, lds, status);
+    else if (xl <= 4) launch_small_xl<CB, K2, ROT, 4, TAG>(jobs, rj, blocks, s, M, K, wk, nkt, x, x_bf16, lds, status);
+    else if (xl <= 8) launch_small_xl<CB, K2, ROT, 8, TAG>(jobs, rj, blocks, s, M, K, wk, nkt, x, x_bf16, lds, status);
     else return false;
     return true;
+}
+
+// The small-row grid of a job set: 32-column groups x splits of every job, each job's first block in `start`.
+static int small_grid(ea_jobs& sj) {
+    int nb = 0;
+    for (int i = 0; i < sj.n; ++i) {
+        sj.j[i].start = nb;
+        nb += (sj.j[i].N >> 5) * sj.j[i].SK;
+    }
+    return nb;
 }
 
 // The small-row kernel when it applies (m <= 16, every job split (SK > 1) with the same even per-wave tile count up to
@@ -378,19 +465,24 @@ static bool launch_small(const ea_jobs& jobs, const ea_rot_jobs* rj, hipStream_t
         if (rj && ((rj->suh[i] & 15) || (rj->xh[i] & 3))) return false;
     }
     if (nkt < 2 || nkt > LS_MAXNKT || (nkt & 1)) return false;
-    // the small-row grid: 32-column groups x splits of every job
-    ea_jobs sj = jobs;
-    int nb = 0;
-    for (int i = 0; i < sj.n; ++i) {
-        sj.j[i].start = nb;
-        nb += (sj.j[i].N >> 5) * sj.j[i].SK;
-    }
     const ea_rot_jobs r = rj ? *rj : ea_rot_jobs{};
     const int bf = x_dtype == BF16;
-#define EA_SV(K2_, CB_)                                                                                        \
-    if (k2 == K2_ && cb == CB_)                                                                                \
-        return rj ? launch_small_k2<CB_, K2_, true>(sj, r, nb, s, M, K, wk, nkt, x, bf, status)                \
-                  : launch_small_k2<CB_, K2_, false>(sj, r, nb, s, M, K, wk, nkt, x, bf, status);
+    // the tagged form when every job's split count is even and at most 2 LS_MAXTS (half the splits, twice the
+    // waves, 8-byte slots in the same Z); the flag form otherwise, or when the tagged block's LDS does not fit
+    bool tag = 2 * wk <= 8;
+    for (int i = 0; i < jobs.n; ++i) tag = tag && jobs.j[i].SK % 2 == 0 && jobs.j[i].SK <= 2 * LS_MAXTS;
+    ea_jobs tj = jobs;
+    for (int i = 0; i < tj.n; ++i) tj.j[i].SK /= 2;
+    ea_jobs sj = jobs;
+    const int tb = small_grid(tj), nb = small_grid(sj);
+#define EA_SV(K2_, CB_)                                                                                            \
+    if (k2 == K2_ && cb == CB_) {                                                                                  \
+        if (tag && (rj ? launch_small_k2<CB_, K2_, true, true>(tj, r, tb, s, M, K, 2 * wk, nkt, x, bf, status)     \
+                       : launch_small_k2<CB_, K2_, false, true>(tj, r, tb, s, M, K, 2 * wk, nkt, x, bf, status)))  \
+            return true;                                                                                           \
+        return rj ? launch_small_k2<CB_, K2_, true, false>(sj, r, nb, s, M, K, wk, nkt, x, bf, status)             \
+                  : launch_small_k2<CB_, K2_, false, false>(sj, r, nb, s, M, K, wk, nkt, x, bf, status);           \
+    }
     EA_SV(10, 2) EA_SV(8, 1) EA_SV(8, 2) EA_SV(6, 1) EA_SV(4, 1)
 #undef EA_SV
     return false;

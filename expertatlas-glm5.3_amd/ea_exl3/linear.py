@@ -46,11 +46,12 @@ class Linear:
 
 
 class Scratch:
-    """linear.zig Scratch: xh fp16 [M, K] a layer and Z fp32 [SK, M, N] a layer with SK > 1."""
+    """linear.zig Scratch: xh fp16 [M, K] a layer and Z fp32 [SK, M, N] a layer with SK > 1. Z starts zero, as the
+    counters do: the small-row kernel's tagged hand-off leaves every slot it used zero again."""
 
     def __init__(self, max_rows: int, max_k: int, max_zn: int):
         self.xh = [device.empty(max_rows * max_k, torch.float16) for _ in range(MAX_JOBS)]
-        self.z = [device.empty(max(max_zn, 1), torch.float32) for _ in range(MAX_JOBS)]
+        self.z = [device.zeros(max(max_zn, 1), torch.float32) for _ in range(MAX_JOBS)]
         self.c = LinearScratch()
         for i in range(MAX_JOBS):
             self.c.xh[i] = self.xh[i].data_ptr()

@@ -223,6 +223,10 @@ typedef struct ea_linear {
     uint64_t words, suh, svh, counters;  /* counters: int32 [8 * N / 128], zero; left zero by the kernel */
     uint32_t k, n, k2, cb, sk, wk;
 } ea_linear;
+/* linear.zig:140-155 Scratch: xh fp16 [M, K] and z fp32 [SK, M, N] a layer. z must not hold the small-row kernel's
+ * tag when first used (zero it once at allocation, as the counters are): calls of up to about 8 rows with an even
+ * split count hand their partial sums over in z as tagged 8-byte slots and leave every slot they used zero. Two calls
+ * that run at once on one z race, as in the reference. */
 typedef struct ea_linear_scratch {
     uint64_t xh[EA_MAX_JOBS], z[EA_MAX_JOBS];
 } ea_linear_scratch;

@@ -46,6 +46,30 @@ def test_config1_linear_6144x2048_one_row(ea):
         np.testing.assert_array_equal(device.download(sc.xh[0][: M * K].view(torch.int16)).reshape(M, K), xh)
         assert_close_rms(device.download(y), want, 1e-4, f"config 1 linear rep {rep}")
         assert int(device.download(lin.counters).sum()) == 0
+        # one row takes the tagged hand-off: every slot it used is zero again
+        assert not np.any(device.download(sc.z[0]).view(np.uint32)), "tagged slots left behind"
+    assert device.device_status() == 0
+
+
+def test_config1_linear_flag_and_tagged_forms_share_z(ea):
+    """16 rows take the flag form (fp32 partial sums left in Z), then 1 and 4 rows the tagged form on the same Z: the
+    stale partial sums are never taken for tagged slots (the tag is a NaN pattern no fp32 result has)."""
+    device, linear, _, _, synth = ea
+    K, N, k2, cb = 6144, 2048, 8, 1
+    T = synth.trellis(1011, 0, 0, 0, K, N, k2)
+    suh, svh = synth.scales(1012, K, 1.0), synth.scales(1013, N, 0.02)
+    lin = linear.Linear(T, suh, svh, K, N, k2, cb)
+    tw = 4 * k2
+    sc = linear.Scratch(16, K, lin.sk * 16 * N)
+    for M in (16, 1, 4, 16, 1):
+        x = synth.activations(1014 + M, M, K, "f16")
+        want = orc.exl3_linear(orc.exl3_rot_in(x, suh, M, K), linear.strips(T, K, N, k2), 8 * tw, (K // 16) * 8 * tw,
+                               svh, M, K, N, k2, cb, lin.sk, lin.wk, y_dtype=2)
+        dx = device.upload(x)
+        y = device.zeros((M, N), torch.float32)
+        linear.call(device.stream(), sc, [lin], dx.data_ptr(), 0, M, [y.data_ptr()], [2])
+        assert_close_rms(device.download(y), want, 1e-4, f"config 1 shape, {M} rows after other row counts")
+        assert int(device.download(lin.counters).sum()) == 0
     assert device.device_status() == 0
 
 
