@@ -165,7 +165,7 @@ constexpr uint32_t LS_TAG = 0x7FB5EA1Du;
 constexpr int LS_POLLS = 1 << 20;  // polls before the finisher gives up (tens of milliseconds)
 
 template <int CB, int K2, int NKT, bool ROT, int XL, bool TAG>
-__global__ void __launch_bounds__(512) lin_small_kernel(ea_jobs jobs, ea_rot_jobs rj, int M, int K, const void* x,
+__global__ void __launch_bounds__(1024) lin_small_kernel(ea_jobs jobs, ea_rot_jobs rj, int M, int K, const void* x,
                                                         int x_bf16, int* status) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     constexpr int TW = 4 * K2;
@@ -189,8 +189,20 @@ __global__ void __launch_bounds__(512) lin_small_kernel(ea_jobs jobs, ea_rot_job
     float* red = reinterpret_cast<float*>(stage);  // after the products: [WK][16][32]
     uint32_t* st = stage + wave * NKT * 2 * TW;
 
-    // the activation rows (and suh) first, 16 bytes a load, every load issued (a thread past the end reads the last
-    // chunk again), so the trellis loads that follow stay in flight while these are written to LDS
+    // the wave's trellis first: NKT rows of its two adjacent column tiles (strips layout). The tiles decode into
+    // registers as soon as they land, while the activations (loaded next) are still in flight: the decode needs only
+    // the trellis, and the MFMAs wait for the rotated activations.
+    const int nt0 = 2 * g;
+    TileSpan sp;
+    const int64_t tiles_end = (int64_t)((N >> 7) - 1) * J.stride_nb + (int64_t)(K >> 4) * J.stride_k;
+    sp.r = buffer_rsrc(dptr<const uint32_t>(J.T), (uint32_t)(tiles_end * 4));
+    sp.off = (int)((((int64_t)(lo >> 4) + wave * NKT) * J.stride_k + (nt0 >> 3) * J.stride_nb + (nt0 & 7) * TW) * 4);
+    sp.kstride = (int)(J.stride_k * 4);
+    u4v v[stage_loads_k<NKT, K2>()];
+    stage_issue_k<NKT, K2>(sp, lane, v);
+
+    // then the activation rows (and suh), 16 bytes a load, every load issued (a thread past the end reads the last
+    // chunk again)
     const uint16_t* xsrc = ROT ? static_cast<const uint16_t*>(x) : dptr<const uint16_t>(J.xh);
     const int cpr = span >> 3, chunks = M * cpr;  // 16-byte chunks a row, in all
     u4v xv[XL];
@@ -203,16 +215,6 @@ __global__ void __launch_bounds__(512) lin_small_kernel(ea_jobs jobs, ea_rot_job
     if constexpr (ROT)
         sv = *reinterpret_cast<const u4v*>(dptr<const uint16_t>(rj.suh[ji]) + k_first +
                                            8 * min((int)threadIdx.x, cpr - 1));
-
-    // the wave's trellis: NKT rows of its two adjacent column tiles (strips layout)
-    const int nt0 = 2 * g;
-    TileSpan sp;
-    const int64_t tiles_end = (int64_t)((N >> 7) - 1) * J.stride_nb + (int64_t)(K >> 4) * J.stride_k;
-    sp.r = buffer_rsrc(dptr<const uint32_t>(J.T), (uint32_t)(tiles_end * 4));
-    sp.off = (int)((((int64_t)(lo >> 4) + wave * NKT) * J.stride_k + (nt0 >> 3) * J.stride_nb + (nt0 & 7) * TW) * 4);
-    sp.kstride = (int)(J.stride_k * 4);
-    u4v v[stage_loads_k<NKT, K2>()];
-    stage_issue_k<NKT, K2>(sp, lane, v);
     // the svh and bias of the lane's two columns of the 128-column block, for whichever block finishes it (loaded by
     // every block, unconditionally: a load in a branch would make the compiler wait for all loads before the first use)
     const bool finisher = (g & 3) == 3 && split == SK - 1;  // the highest-index block of the 4 SK
@@ -225,6 +227,28 @@ __global__ void __launch_bounds__(512) lin_small_kernel(ea_jobs jobs, ea_rot_job
 #pragma unroll
     for (int i = 0; i < XL; ++i) hold(xv[i]);
     hold(sv);
+    // the trellis into the wave's LDS region (it waits only for the trellis loads), then every tile decoded into its
+    // MFMA operand
+    stage_store_k<NKT, K2>(st, lane, v);
+    const LaneQuad lq = lane_quad_k<K2>(lane);
+    u4v bq[NKT / 2][2];
+    {
+        const uint32_t* wa = st + lq.w0;
+        const uint32_t* wb = st + lq.w1;
+#pragma unroll
+        for (int t = 0; t < NKT; t += 2)
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const int t0 = (2 * t + j) * TW, t1 = (2 * (t + 1) + j) * TW;
+                const u2v b0 = decode_quad<K2, CB>(wa[t0], wb[t0], lq.sh);
+                const u2v b1 = decode_quad<K2, CB>(wa[t1], wb[t1], lq.sh);
+                bq[t >> 1][j] = u4v{b0.x, b0.y, b1.x, b1.y};
+            }
+    }
+#pragma unroll
+    for (int t = 0; t < NKT / 2; ++t)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) hold(bq[t][j]);  // decoded before the activations are waited for
 #pragma unroll
     for (int i = 0; i < XL; ++i) {
         const int c = i * NT + (int)threadIdx.x;
@@ -253,12 +277,8 @@ __global__ void __launch_bounds__(512) lin_small_kernel(ea_jobs jobs, ea_rot_job
         }
         __syncthreads();
     }
-    stage_store_k<NKT, K2>(st, lane, v);
 
     // the product: A rows are the activation rows (zero past M), B the decoded tiles
-    const LaneQuad lq = lane_quad_k<K2>(lane);
-    const uint32_t* wa = st + lq.w0;
-    const uint32_t* wb = st + lq.w1;
     const int row = lane & 15;
     const uint16_t* xr = row < M ? xs + row * XS + xoff + wave * NKT * 16 : nullptr;
     f4v acc[2] = {f4v{0.f, 0.f, 0.f, 0.f}, f4v{0.f, 0.f, 0.f, 0.f}};
@@ -266,13 +286,8 @@ __global__ void __launch_bounds__(512) lin_small_kernel(ea_jobs jobs, ea_rot_job
     for (int t = 0; t < NKT; t += 2) {
         const h8v a = load_a8(xr, t * 16, lane);
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const int t0 = (2 * t + j) * TW, t1 = (2 * (t + 1) + j) * TW;
-            const u2v b0 = decode_quad<K2, CB>(wa[t0], wb[t0], lq.sh);
-            const u2v b1 = decode_quad<K2, CB>(wa[t1], wb[t1], lq.sh);
-            const h8v bb = __builtin_bit_cast(h8v, (u4v{b0.x, b0.y, b1.x, b1.y}));
-            acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bb, acc[j], 0, 0, 0);
-        }
+        for (int j = 0; j < 2; ++j)
+            acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, __builtin_bit_cast(h8v, bq[t >> 1][j]), acc[j], 0, 0, 0);
     }
     __syncthreads();  // every wave is done with the staged trellis: the wave sums take its place
 #pragma unroll
@@ -475,10 +490,17 @@ static bool launch_small(const ea_jobs& jobs, const ea_rot_jobs* rj, hipStream_t
     for (int i = 0; i < tj.n; ++i) tj.j[i].SK /= 2;
     ea_jobs sj = jobs;
     const int tb = small_grid(tj), nb = small_grid(sj);
+    // the tagged form on sixteen waves a block (four a SIMD) when its waves' k tiles halve evenly once more: the
+    // same decode over twice the waves (config 1: 8.64 -> 8.55 us)
+    int tw = 2 * wk, tn = nkt;
+    if (tn % 4 == 0 && 2 * tw <= 16) {
+        tw *= 2;
+        tn /= 2;
+    }
 #define EA_SV(K2_, CB_)                                                                                            \
     if (k2 == K2_ && cb == CB_) {                                                                                  \
-        if (tag && (rj ? launch_small_k2<CB_, K2_, true, true>(tj, r, tb, s, M, K, 2 * wk, nkt, x, bf, status)     \
-                       : launch_small_k2<CB_, K2_, false, true>(tj, r, tb, s, M, K, 2 * wk, nkt, x, bf, status)))  \
+        if (tag && (rj ? launch_small_k2<CB_, K2_, true, true>(tj, r, tb, s, M, K, tw, tn, x, bf, status)          \
+                       : launch_small_k2<CB_, K2_, false, true>(tj, r, tb, s, M, K, tw, tn, x, bf, status)))       \
             return true;                                                                                           \
         return rj ? launch_small_k2<CB_, K2_, true, false>(sj, r, nb, s, M, K, wk, nkt, x, bf, status)             \
                   : launch_small_k2<CB_, K2_, false, false>(sj, r, nb, s, M, K, wk, nkt, x, bf, status);           \
