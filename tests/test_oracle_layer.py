@@ -224,3 +224,60 @@ def test_swiglu2_against_float64_and_closed_forms():
     np.testing.assert_array_equal(orc.swiglu2(big, u[:8]), synth.bf16_bits(24.0 * synth.bf16_to_f32(u[:8])))
     neg = synth.bf16_bits(-synth.bf16_to_f32(u))
     np.testing.assert_array_equal(synth.bf16_to_f32(orc.swiglu2(g, neg)), -synth.bf16_to_f32(orc.swiglu2(g, u)))
+
+
+# ---- the gate / up epilogue's activation modes, against float64 ------------------------------------------------------
+
+def _epilogue_fp64(Z, pick, svh_g, svh_u, suh_d, P, N, SK, limit):
+    """xd [P, N] in float64: splits summed, H / sqrt(128) per 128 columns, svh, SwiGLU with the limit's clamps, suh_d,
+    H / sqrt(128) again (exl3_experts.cu:142-184, no roundings)."""
+    Hb = _block_h(N)
+    out = np.full((P, N), np.nan)
+    for p in range(P):
+        e = int(pick.reshape(-1)[p])
+        if e < 0:
+            continue
+        g = Z[0, :, p, :].astype(np.float64).sum(axis=0) @ Hb * h2f(svh_g[e]).astype(np.float64)
+        u = Z[1, :, p, :].astype(np.float64).sum(axis=0) @ Hb * h2f(svh_u[e]).astype(np.float64)
+        g = np.minimum(g, limit)
+        u = np.clip(u, -limit, limit)
+        act = g / (1.0 + np.exp(-g)) * u
+        out[p] = (act * h2f(suh_d[e]).astype(np.float64)) @ Hb
+    return out
+
+
+def test_gateup_epilogue_act_modes_against_fp64():
+    """The oracle's epilogue in both activation modes against a float64 restatement built from the Sylvester matrix:
+    act_mode 1 (fp32) within fp16 output rounding, act_mode 0 within its three bf16 roundings, and act_mode 0 apart
+    from act_mode 1 by about those roundings (so they happen). A dropped or swapped clamp, g and u exchanged, or a
+    missing Hadamard fails by far more; the limit is small enough that about a fifth of the values are clamped."""
+    from types import SimpleNamespace
+
+    rng = np.random.default_rng(5)
+    R, E, N, SK, slots = 3, 16, 256, 4, 8
+    P = R * slots
+    pick = synth.picks_uniform(21, R, E, slots)
+    pick[0, 3] = -1
+    Z = (rng.standard_normal((2, SK, P, N)) * 2.0).astype(np.float32)
+    svh_g, svh_u, suh_d = (synth.scales(31 + i, E * N, 1.0).reshape(E, N) for i in range(3))
+    r = SimpleNamespace(svh_g=svh_g, svh_u=svh_u, suh_d=suh_d)
+    limit = 5.0
+    want = _epilogue_fp64(Z, pick, svh_g, svh_u, suh_d, P, N, SK, limit)
+    ok = pick.reshape(-1) >= 0
+    ref = want[ok]
+    rms = float(np.sqrt(np.mean(ref ** 2)))
+    # how much the clamps bite: the same activation without them differs by far more than the bars below
+    g_all = np.concatenate([Z[0, :, p, :].sum(axis=0) @ _block_h(N) * h2f(svh_g[int(pick.reshape(-1)[p])])
+                            for p in np.nonzero(ok)[0]])
+    assert 0.1 < float(np.mean(np.abs(g_all) > limit)) < 0.4
+    got = {}
+    for mode in (1, 0):
+        xd = orc.gateup_epilogue(Z, pick, r, R, P, N, SK, slots, E, limit, mode)
+        got[mode] = h2f(xd).astype(np.float64)[ok]
+    d1 = got[1] - ref
+    assert np.all(np.abs(d1) <= 2.0 ** -10 * np.abs(ref) + 1e-5 * rms), "act_mode 1 off the float64 epilogue"
+    d0 = got[0] - ref
+    assert float(np.sqrt(np.mean(d0 ** 2))) < 0.01 * rms, "act_mode 0 off the float64 epilogue"
+    assert float(np.max(np.abs(d0))) < 0.08 * rms
+    sep = float(np.sqrt(np.mean((got[0] - got[1]) ** 2)))
+    assert 2e-4 * rms < sep < 0.01 * rms, f"act_mode 0 vs 1: {sep / rms:.2e} of RMS (the bf16 roundings)"
