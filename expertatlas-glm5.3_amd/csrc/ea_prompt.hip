@@ -17,13 +17,13 @@ namespace ea {
 
 // Routed pairs an item at most. The reference's items hold up to 112 (prompt_experts.cu:55-58, TF_PE_GPM), as do
 // this library's for the register-streaming GEMM of widths above 10 (IPM_WIDE); the staged GEMMs (widths 2..10) take
-// items of up to 48 (three row tiles), which measured 6 % faster at 512 rows and the same at 2048: more blocks of
-// shorter MFMA chains and fewer accumulators, for more decoding of the experts split into several items. A pair's
-// sums do not depend on its item. The register-streaming GEMM is built for 7 row tiles only: routing into items of
+// items of up to 80 (five row tiles): against 48 the same at 512 rows and 3-4 % faster at 2048 (a heavy expert
+// decoded in fewer items), against 112 (seven row tiles, more accumulators) faster at both; 64 and 96 measured between.
+// A pair's sums do not depend on its item. The register-streaming GEMM is built for 7 row tiles only: routing into items of
 // at most 48 pairs is right with it (checked with that kernel at widths above 10), but the same kernel built for 3
 // row tiles gave wrong sums at width 12 (no register spills, the same index arithmetic, extra wait states after the
 // decoder's fp16 adds changed nothing); that instantiation is not built.
-constexpr int IPM = 48;
+constexpr int IPM = 80;
 constexpr int IPM_TILES = IPM / 16;
 constexpr int IPM_WIDE = 112;
 constexpr int IPM_WIDE_TILES = IPM_WIDE / 16;
