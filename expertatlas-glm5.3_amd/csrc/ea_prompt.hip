@@ -204,6 +204,8 @@ constexpr int PW = 4;                             // waves a block: 8 column til
 constexpr int PSTAGE = PK * 2 * 4 * STAGE_MAXK2;  // a wave's staged trellis words a chunk
 constexpr int DNG = 16;  // down matrix: column blocks of 128 a block, small items (8, 24 and 48 measured slower at 512 rows)
 constexpr int DNG_BIG = 2;  // the same for the larger items: more blocks for fewer items (4: 1 % slower at 512 rows)
+constexpr int DNG_BIG_LONG = 4;   // passes of more than LONG_ROWS rows: 1.5 % faster at 2048 rows
+constexpr int LONG_ROWS = 1024;
 constexpr int GU_SPLIT = 2;                       // K splits of a larger item's gate|up (4 and 8 measured slower)
 // The number of K splits of a larger item's gate|up over K (at most one a chunk).
 static int gu_splits(int K) { return K / (PK * 16) < GU_SPLIT ? K / (PK * 16) : GU_SPLIT; }
@@ -834,7 +836,10 @@ static int list_pass(hipStream_t q, const ListPass& a, int big) {
                                (uint32_t)ns, big);
     if (r) return r;
     if (a.I <= 2 * PK * 16 && (a.D / 128) % DNG == 0) {
-        if (big)
+        if (big && a.rows > LONG_ROWS && (a.D / 128) % DNG_BIG_LONG == 0)
+            item_dn_kernel<CB, IPM_TILES, DNG_BIG_LONG><<<dim3(a.mi, a.D / 128 / DNG_BIG_LONG, 1), PW * 64, 0, q>>>(
+                a.xd, a.tp[2], a.k2[2], a.sorted, a.items, a.count, a.plane, a.I, a.D, a.P, a.mi, a.status);
+        else if (big)
             item_dn_kernel<CB, IPM_TILES, DNG_BIG><<<dim3(a.mi, a.D / 128 / DNG_BIG, 1), PW * 64, 0, q>>>(
                 a.xd, a.tp[2], a.k2[2], a.sorted, a.items, a.count, a.plane, a.I, a.D, a.P, a.mi, a.status);
         else
