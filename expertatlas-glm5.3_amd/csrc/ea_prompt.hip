@@ -30,6 +30,7 @@ constexpr int IPM_WIDE_TILES = IPM_WIDE / 16;
 static_assert(IPM_WIDE_TILES == 7, "the register-streaming item GEMM is verified for 7 row tiles only");
 constexpr uint32_t CHUNK_ROWS = 4096;  // rows a pass at most (prompt_experts.zig:17)
 constexpr int ROUTE_THREADS = 1024;
+constexpr int ROUTE_HELD = 16;  // picks a route thread holds in registers: 16,384 pairs (2,048 rows of 8 slots)
 
 constexpr int SMALL_ROWS = 16;     // items of at most this many pairs: the kernels holding one row tile
 
@@ -60,8 +61,19 @@ __global__ void __launch_bounds__(ROUTE_THREADS) route_kernel(const int* __restr
     int* start = sh + 2 * E;  // [E]
     __shared__ int wsum[ROUTE_THREADS / 64][3];
     for (int e = threadIdx.x; e < E; e += ROUTE_THREADS) cnt[e] = 0;
+    // the first ROUTE_HELD * ROUTE_THREADS picks are loaded once, all loads in flight together, and held in
+    // registers for both passes (a load then an atomic a pair waited for every load in turn); later ones are re-read
+    int held[ROUTE_HELD];
+#pragma unroll
+    for (int j = 0; j < ROUTE_HELD; ++j) {
+        const int i = j * ROUTE_THREADS + (int)threadIdx.x;
+        held[j] = i < n ? pick[i] : -1;
+    }
     __syncthreads();
-    for (int i = threadIdx.x; i < n; i += ROUTE_THREADS) {
+#pragma unroll
+    for (int j = 0; j < ROUTE_HELD; ++j)
+        if (held[j] >= 0 && held[j] < E) atomicAdd(&cnt[held[j]], 1);
+    for (int i = ROUTE_HELD * ROUTE_THREADS + threadIdx.x; i < n; i += ROUTE_THREADS) {
         const int e = pick[i];
         if (e >= 0 && e < E) atomicAdd(&cnt[e], 1);
     }
@@ -127,8 +139,7 @@ __global__ void __launch_bounds__(ROUTE_THREADS) route_kernel(const int* __restr
         off += c;
     }
     __syncthreads();
-    for (int i = threadIdx.x; i < n; i += ROUTE_THREADS) {
-        const int e = pick[i];
+    auto place = [&](int i, int e) __attribute__((always_inline)) {
         int big = 0;
         if (e >= 0 && e < E) {
             const int at = atomicAdd(&cur[e], 1);
@@ -137,7 +148,13 @@ __global__ void __launch_bounds__(ROUTE_THREADS) route_kernel(const int* __restr
             big = min(ipm, cnt[e] - f) > SMALL_ROWS;
         }
         pclass[i] = big;
+    };
+#pragma unroll
+    for (int j = 0; j < ROUTE_HELD; ++j) {
+        const int i = j * ROUTE_THREADS + (int)threadIdx.x;
+        if (i < n) place(i, held[j]);
     }
+    for (int i = ROUTE_HELD * ROUTE_THREADS + threadIdx.x; i < n; i += ROUTE_THREADS) place(i, pick[i]);
 }
 
 // Block (item, n block of NW * NTW tiles, matrix): wave w covers NTW n tiles over the whole K range for all of the
