@@ -352,8 +352,24 @@ __device__ __forceinline__ void gu_loop(__amdgpu_buffer_rsrc_t xrs, const uint32
     if (c < nch) step(c, ta);  // uniform
 }
 
-// Block (item of the larger items' list, 128 columns, (matrix, K split)): the item's rows (up to IPM_TILES row
-// tiles) times its expert's matrix over split s of K's chunks of 128 (splits [s nch / nsplit, (s + 1) nch / nsplit)).
+// Block b of a launch over (items, C column blocks, Z slices) in XCD order. Blocks are dispatched to the 8 XCDs in
+// turn (block b on XCD b mod 8); group g = item Z + slice takes blocks on XCD g mod 8 for all C of its column blocks
+// (the item's activations of the slice come into that XCD's L2 once), and slice z of an expert's consecutive items
+// lands on the XCDs (i Z + z) mod 8, 8 / gcd(Z, 8) of them (two for Z = 4 or 12), whose L2s then hold its trellis
+// for the expert's later items. 2048 rows: 719 -> 691 us a layer (item order: a slice's blocks on all 8 XCDs, each
+// fetching the slice). Blocks: ceil(items Z / 8) 8 C, those past the list's count return at once.
+__device__ __forceinline__ void xcd_order(int b, int C, int Z, int& item, int& cb, int& z) {
+    const int q = b >> 3;
+    cb = q % C;
+    const int g = (q / C) * 8 + (b & 7);
+    item = g / Z;
+    z = g % Z;
+}
+static unsigned xcd_blocks(int items, int C, int Z) { return (unsigned)((items * Z + 7) / 8 * 8 * C); }
+
+// Block (item of the larger items' list, 128 columns, (matrix, K split)), in XCD order: the item's rows (up to
+// IPM_TILES row tiles) times its expert's matrix over split s of K's chunks of 128 (splits [s nch / nsplit,
+// (s + 1) nch / nsplit)).
 // A chunk's activations go to LDS once for the block's four waves; each wave's two column tiles of the chunk come in
 // as 16-byte loads staged in the wave's own LDS region. Only the item's occupied row tiles are loaded and multiplied;
 // rows past the item's count read the item's first pair and are not stored (MFMA rows do not mix). Split 0 goes to
@@ -363,12 +379,14 @@ __global__ void __launch_bounds__(PW * 64) __attribute__((amdgpu_waves_per_eu(2)
 item_gu_kernel(const uint16_t* __restrict__ X0, const uint16_t* __restrict__ X1, const int64_t* __restrict__ TP0,
                const int64_t* __restrict__ TP1, const int* __restrict__ K2_0, const int* __restrict__ K2_1,
                const int* __restrict__ sorted, const int* __restrict__ items, const int* __restrict__ item_count,
-               float* __restrict__ Z, float* __restrict__ Zp, int K, int N, int P, int nsplit, int max_items,
+               float* __restrict__ Z, float* __restrict__ Zp, int K, int N, int P, int nsplit, int mats, int max_items,
                int* __restrict__ status) {
     constexpr int MT = IPM_TILES;
     int e, first, cnt;
-    if (!item_at(items, item_count, 1, max_items, blockIdx.x, e, first, cnt)) return;
-    const int mat = blockIdx.z / nsplit, split = blockIdx.z % nsplit;
+    int item, cb, zs;
+    xcd_order((int)blockIdx.x, N / (16 * 2 * PW), mats * nsplit, item, cb, zs);
+    if (!item_at(items, item_count, 1, max_items, item, e, first, cnt)) return;
+    const int mat = zs / nsplit, split = zs % nsplit;
     const uint16_t* X = mat ? X1 : X0;
     const uint32_t* T = reinterpret_cast<const uint32_t*>(mat ? TP1[e] : TP0[e]);
     const int k2 = mat ? K2_1[e] : K2_0[e];
@@ -393,7 +411,7 @@ item_gu_kernel(const uint16_t* __restrict__ X0, const uint16_t* __restrict__ X1,
         lofs[i] = row * PXS;
     }
     const __amdgpu_buffer_rsrc_t xrs = buffer_rsrc(X, (uint32_t)((size_t)P * K * 2));
-    const int nt0 = blockIdx.y * (2 * PW) + 2 * wave;
+    const int nt0 = cb * (2 * PW) + 2 * wave;
     const int ns = N >> 4, TWB = 16 * k2;
     TileSpan sp;
     sp.r = buffer_rsrc(T, (uint32_t)((K >> 4) * ns * TWB));
@@ -647,7 +665,14 @@ item_dn_kernel(const uint16_t* __restrict__ X, const int64_t* __restrict__ TP, c
                const int* __restrict__ sorted, const int* __restrict__ items, const int* __restrict__ item_count,
                float* __restrict__ Z, int K, int N, int P, int max_items, int* __restrict__ status) {
     int e, first, cnt;
-    if (!item_at(items, item_count, MT > 2, max_items, blockIdx.x, e, first, cnt)) return;
+    // the larger items' blocks in XCD order (a column group's slice of an expert on the same XCDs for all of the
+    // expert's items); the small items' (one item an expert) item by item
+    int item = blockIdx.x, grp = blockIdx.y;
+    if constexpr (MT > 2) {
+        int cb_unused;
+        xcd_order((int)blockIdx.x, 1, N / 128 / NG, item, cb_unused, grp);
+    }
+    if (!item_at(items, item_count, MT > 2, max_items, item, e, first, cnt)) return;
     const uint32_t* T = reinterpret_cast<const uint32_t*>(TP[e]);
     const int k2 = K2T[e];
     // the wave index in a scalar register: the trellis offsets built from it are then scalar (a buffer load's soffset)
@@ -680,7 +705,7 @@ item_dn_kernel(const uint16_t* __restrict__ X, const int64_t* __restrict__ TP, c
                 if (c < nch && i < mts) put_a(xa + (i * 16 + (tid >> 4)) * DXS + c * PK * 16, tid & 15, av[c][i]);
     }
     const int ns = N >> 4, TWB = 16 * k2;
-    const int nb0 = blockIdx.y * NG;  // first column block
+    const int nb0 = grp * NG;  // first column block
     TileSpan sp;
     sp.r = buffer_rsrc(T, (uint32_t)((K >> 4) * ns * TWB));
     sp.off = (nb0 * 8 + 2 * wave) * TWB;
@@ -839,9 +864,9 @@ template <int CB>
 static int list_pass(hipStream_t q, const ListPass& a, int big) {
     const int ns = gu_splits(a.D);
     if (big)
-        item_gu_kernel<CB><<<dim3(a.mi, a.I / (16 * 2 * PW), 2 * ns), PW * 64, 0, q>>>(
+        item_gu_kernel<CB><<<xcd_blocks(a.mi, a.I / (16 * 2 * PW), 2 * ns), PW * 64, 0, q>>>(
             a.xg, a.xu, a.tp[0], a.tp[1], a.k2[0], a.k2[1], a.sorted, a.items, a.count, a.z, a.zp, a.D, a.I, a.P, ns,
-            a.mi, a.status);
+            2, a.mi, a.status);
     else  // blocks of 4 waves over 128 columns (8 waves over 256 measured 1 % slower at 512 rows, the same at 2048)
         item_ring_kernel<CB, 4><<<dim3(a.mi, a.I / 128, 2), 4 * 64, 0, q>>>(
             a.xg, a.xu, a.tp[0], a.tp[1], a.k2[0], a.k2[1], a.sorted, a.items, a.count, a.z, a.D, a.I, a.P, ns, a.mi,
@@ -854,18 +879,18 @@ static int list_pass(hipStream_t q, const ListPass& a, int big) {
     if (r) return r;
     if (a.I <= 2 * PK * 16 && (a.D / 128) % DNG == 0) {
         if (big && a.rows > LONG_ROWS && (a.D / 128) % DNG_BIG_LONG == 0)
-            item_dn_kernel<CB, IPM_TILES, DNG_BIG_LONG><<<dim3(a.mi, a.D / 128 / DNG_BIG_LONG, 1), PW * 64, 0, q>>>(
+            item_dn_kernel<CB, IPM_TILES, DNG_BIG_LONG><<<xcd_blocks(a.mi, 1, a.D / 128 / DNG_BIG_LONG), PW * 64, 0, q>>>(
                 a.xd, a.tp[2], a.k2[2], a.sorted, a.items, a.count, a.plane, a.I, a.D, a.P, a.mi, a.status);
         else if (big)
-            item_dn_kernel<CB, IPM_TILES, DNG_BIG><<<dim3(a.mi, a.D / 128 / DNG_BIG, 1), PW * 64, 0, q>>>(
+            item_dn_kernel<CB, IPM_TILES, DNG_BIG><<<xcd_blocks(a.mi, 1, a.D / 128 / DNG_BIG), PW * 64, 0, q>>>(
                 a.xd, a.tp[2], a.k2[2], a.sorted, a.items, a.count, a.plane, a.I, a.D, a.P, a.mi, a.status);
         else
             item_dn_kernel<CB, SMALL_ROWS / 16, DNG><<<dim3(a.mi, a.D / 128 / DNG, 1), PW * 64, 0, q>>>(
                 a.xd, a.tp[2], a.k2[2], a.sorted, a.items, a.count, a.plane, a.I, a.D, a.P, a.mi, a.status);
     } else if (big) {
-        item_gu_kernel<CB><<<dim3(a.mi, a.D / (16 * 2 * PW), 1), PW * 64, 0, q>>>(
+        item_gu_kernel<CB><<<xcd_blocks(a.mi, a.D / (16 * 2 * PW), 1), PW * 64, 0, q>>>(
             a.xd, a.xd, a.tp[2], a.tp[2], a.k2[2], a.k2[2], a.sorted, a.items, a.count, a.plane, nullptr, a.I, a.D,
-            a.P, 1, a.mi, a.status);
+            a.P, 1, 1, a.mi, a.status);
     } else {
         item_ring_kernel<CB, 4><<<dim3(a.mi, a.D / 128, 1), 4 * 64, 0, q>>>(
             a.xd, a.xd, a.tp[2], a.tp[2], a.k2[2], a.k2[2], a.sorted, a.items, a.count, a.plane, a.I, a.D, a.P, 1,
