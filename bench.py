@@ -661,6 +661,11 @@ def run_prefill(args, torch, np, R: int, steps: int | None = None, warmup: int |
                 "frac": round(max(t_hbm, t_mfma) / us, 4), "traffic": None,
                 "mfma": {"achieved": round(tfs, 2), "peak": FP16_PEAK_TFLOPS, "unit": "TFLOP/s",
                          "frac": round(tfs / FP16_PEAK_TFLOPS, 4)}}
+    prof = "prefill_config4.md"
+    tr = recorded_figure(prof, "traffic_bytes_per_layer" + ("" if R == 512 else f"_{R}"))
+    if tr is not None:  # HBM bytes of the whole layer (every kernel's FETCH_SIZE + WRITE_SIZE, copy-calibrated)
+        roofline["traffic"] = int(tr)
+        roofline["traffic_source"] = f"profiles/{prof} (rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE; copy-calibrated)"
     return _line(args, us, "us/layer", ms, config, roofline, None) | {"steps": steps, "warmup": warmup}
 
 
