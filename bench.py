@@ -409,6 +409,65 @@ def cpu_baseline_decode(seed: int, R: int = 1, mixed: bool = False, budget_s: fl
             "sample": sample}
 
 
+def _timed(fn, budget_s: float, max_n: int) -> tuple[int, float]:
+    """Calls of fn until budget_s seconds have passed (at least two, at most max_n), after one untimed call."""
+    fn(0)
+    n, t_total = 0, 0.0
+    while n < 2 or (t_total < budget_s and n < max_n):
+        t0 = time.perf_counter()
+        fn(n)
+        t_total += time.perf_counter() - t0
+        n += 1
+    return n, t_total
+
+
+def cpu_baseline_linear(seed: int, budget_s: float = 10.0) -> dict:
+    """Config 1 on the host: the tuned CPU linear (oracle/libcpulayer.so, cpu_exl3_linear: rot_in, the product decoded
+    straight into the sums with OpenMP over column tiles, the output rotation) at K 6144 x N 2048, one fp16 row, fp32
+    out, over four distinct 4-bit linears in turn."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as orc
+    from ea_exl3 import linear, synth
+
+    K, N, k2 = 6144, 2048, 8
+    lins = [(linear.strips(synth.trellis(seed + 10 * i, 0, 0, 0, K, N, k2), K, N, k2),
+             synth.scales(seed + 10 * i + 1, K, 1.0), synth.scales(seed + 10 * i + 2, N, 0.02)) for i in range(4)]
+    x = synth.activations(seed + 3, 1, K, "f16")
+
+    def call(i):
+        S, suh, svh = lins[i % len(lins)]
+        orc.cpu_exl3_linear(x, suh, S, svh, 1, K, N, k2, 1)
+
+    n, t = _timed(call, budget_s, 5000)
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    return {"value": round(t / n * 1e6, 1), "unit": "us/linear", "cores": threads, "kind": "port",
+            "sample": f"{n} calls of one 4-bit EXL3 linear (K 6144 x N 2048, one fp16 row, fp32 out; four distinct "
+                      f"linears in turn) through the tuned CPU linear (oracle/cpu_layer.c: -O3 x86-64-v3, tiles "
+                      f"decoded into the sums, OpenMP over column tiles), {threads} threads on {cpu_model()}"}
+
+
+def cpu_baseline_prefill(seed: int, R: int, budget_s: float = 10.0) -> dict:
+    """Config 4 on the host: the tuned CPU layer (cpu_moe_routed, the prefill's function: the routed experts' sum of
+    every row) over R rows with the bench's Zipf(1.1) top-8 routing, 4-bit experts, each expert's tiles decoded once
+    for all of its rows."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import numpy as np
+    import oracle as orc
+    from ea_exl3 import synth
+
+    pick = synth.picks_zipf(seed + 1, R, 1.1, E, SLOTS)
+    wts = synth.routing_weights(seed + 2, R, SLOTS)
+    host = synth.HostLayer(seed + 4, experts=E, dims=D, width=I, k2=8, only=np.unique(pick))
+    r = _oracle_routed(orc, host)
+    x = synth.activations(seed + 3, R, D, "f16")
+    n, t = _timed(lambda i: orc.cpu_moe_routed(x, pick, wts, r, R, SLOTS), budget_s, 50)
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    return {"value": round(t / n * 1e6, 1), "unit": "us/layer", "cores": threads, "kind": "port",
+            "sample": f"{n} layers of {R} rows (Zipf(1.1) top-8 over 256 4-bit experts, D 6144, I 256) through the "
+                      f"tuned CPU layer (oracle/cpu_layer.c: -O3 x86-64-v3, each expert's tiles decoded once into "
+                      f"the sums of all of its rows, OpenMP over column tiles), {threads} threads on {cpu_model()}"}
+
+
 def _oracle_routed(orc, host):
     import numpy as np
 
@@ -604,7 +663,8 @@ def run_linear(args, torch, np) -> dict:
     if tr:
         roofline["traffic"] = int(tr)
         roofline["traffic_source"] = f"profiles/{prof} (rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE; copy-calibrated)"
-    return _line(args, us, "us/linear", ms, config, roofline, None)
+    cpu = None if args.no_cpu_baseline else cpu_baseline_linear(args.seed)
+    return _line(args, us, "us/linear", ms, config, roofline, cpu)
 
 
 def run_prefill(args, torch, np, R: int, steps: int | None = None, warmup: int | None = None) -> dict:
@@ -666,7 +726,8 @@ def run_prefill(args, torch, np, R: int, steps: int | None = None, warmup: int |
     if tr is not None:  # HBM bytes of the whole layer (every kernel's FETCH_SIZE + WRITE_SIZE, copy-calibrated)
         roofline["traffic"] = int(tr)
         roofline["traffic_source"] = f"profiles/{prof} (rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE; copy-calibrated)"
-    return _line(args, us, "us/layer", ms, config, roofline, None) | {"steps": steps, "warmup": warmup}
+    cpu = None if args.no_cpu_baseline else cpu_baseline_prefill(args.seed, R)
+    return _line(args, us, "us/layer", ms, config, roofline, cpu) | {"steps": steps, "warmup": warmup}
 
 
 def main() -> int:
@@ -694,7 +755,7 @@ def main() -> int:
         # warm-up (a layer is ~0.33 ms, so the timed region stays well under a second)
         pf = run_prefill(args, torch, np, 512)
         result["prefill512"] = {k: pf[k] for k in ("value", "unit", "steps", "warmup", "ms_per_step", "config",
-                                                   "roofline")}
+                                                   "roofline", "cpu_baseline")}
     result["library"] = library_identity()
     result["device"] = device_identity(torch)
     print(json.dumps(result))

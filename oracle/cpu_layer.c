@@ -1,5 +1,5 @@
-/* The CPU baseline of the routed-expert decode layer: test infrastructure, timed by bench.py's cpu_baseline leg and
- * checked against the oracle by tests/test_cpu_layer.py. Never loaded by the product path.
+/* The CPU baselines of the routed-expert decode layer and of one EXL3 linear: test infrastructure, timed by bench.py's
+ * cpu_baseline leg and checked against the oracle by tests/test_cpu_layer.py. Never loaded by the product path.
  *
  * The same function as the oracle's moe.routed (moe.zig:279-293: rotate-in, gate / up GEMV, SwiGLU epilogue, down
  * GEMV, slot-ordered combine; exl3_experts.cu:116-268), organised for host cores: no matrix is dequantised into
@@ -187,4 +187,55 @@ void cpu_moe_routed(const void* x, int x_dtype, int x_stride, const int* pick, c
     free(z);
     free(xd);
     free(y);
+}
+
+/* One EXL3 linear, y [M, N] fp32 = FWHT(rot_in(x) . W) * HS * svh: the oracle's or_exl3_rot_in then or_exl3_linear
+ * (exl3_linear.cu:150-173 rotation, :231-484 product, finish :69-81), with W in linear.zig's strips layout (tile
+ * (kt, nt) at (nt / 8) stride_nb + kt stride_k + (nt % 8) TW words, linear.zig:99-107). For host cores: the rows are
+ * rotated in parallel, then each task (a column tile) decodes its k tiles in ascending order straight into the sums of
+ * every row, so one row keeps every core busy; then the output rotation a (row, column block). The sums run over k in
+ * order in fp32, so the result differs from the oracle's only by summation order (the oracle follows the kernel's
+ * K splits). */
+void cpu_exl3_linear(const void* x, int x_dtype, const uint16_t* suh, const uint32_t* T, int64_t stride_k,
+                     int64_t stride_nb, const uint16_t* svh, float* y, int M, int K, int N, int k2, int cb) {
+    tables(cb);
+    const float* lut = LUTF[cb];
+    const int KT = K / 16, NT = N / 16, TW = 4 * k2;
+    float* xh = (float*)malloc(sizeof(float) * (size_t)M * K);
+    float* acc = (float*)calloc((size_t)M * N, sizeof(float));
+#pragma omp parallel for schedule(static)
+    for (int t = 0; t < M * (K / 128); ++t) {
+        const int r = t / (K / 128), blk = t % (K / 128);
+        float v[128];
+        for (int j = 0; j < 128; ++j) {
+            const uint16_t xv = ((const uint16_t*)x)[(size_t)r * K + blk * 128 + j];
+            v[j] = (x_dtype == 1 ? or_bf2f(xv) : or_h2f(xv)) * or_h2f(suh[blk * 128 + j]);
+        }
+        fwht(v);
+        for (int j = 0; j < 128; ++j) xh[(size_t)r * K + blk * 128 + j] = or_h2f(or_f2h(v[j] * HS));
+    }
+#pragma omp parallel for schedule(dynamic, 2)
+    for (int nt = 0; nt < NT; ++nt) {
+        float w[256];
+        const uint32_t* strip = T + (size_t)(nt / 8) * stride_nb + (size_t)(nt % 8) * TW;
+        for (int kt = 0; kt < KT; ++kt) {
+            decode(strip + (size_t)kt * stride_k, k2, lut, w);
+            for (int m = 0; m < M; ++m) {
+                const float* xr = xh + (size_t)m * K + kt * 16;
+                float* a = acc + (size_t)m * N + nt * 16;
+                for (int rr = 0; rr < 16; ++rr)
+                    for (int c = 0; c < 16; ++c) a[c] += xr[rr] * w[rr * 16 + c];
+            }
+        }
+    }
+#pragma omp parallel for schedule(static)
+    for (int t = 0; t < M * (N / 128); ++t) {
+        const int r = t / (N / 128), nb = t % (N / 128);
+        float v[128];
+        memcpy(v, acc + (size_t)r * N + nb * 128, sizeof(v));
+        fwht(v);
+        for (int c = 0; c < 128; ++c) y[(size_t)r * N + nb * 128 + c] = v[c] * HS * or_h2f(svh[nb * 128 + c]);
+    }
+    free(xh);
+    free(acc);
 }

@@ -274,15 +274,22 @@ def moe_routed(x, pick, wts, routed: Routed, R, slots, x_stride=None, bf16=False
 _cpu = None
 
 
-def cpu_moe_routed(x, pick, wts, routed: Routed, R, slots, x_stride=None, bf16=False):
-    """The tuned CPU baseline (libcpulayer.so, cpu_layer.c) of moe_routed: the same function, decoded straight into
-    the products, OpenMP over column tiles; fp32 sums in a different order than the oracle's."""
+def _cpu_lib():
     global _cpu
     if _cpu is None:
         L = C.CDLL(os.path.join(os.path.dirname(os.path.abspath(__file__)), "libcpulayer.so"))
         L.cpu_moe_routed.restype = None
         L.cpu_moe_routed.argtypes = [P, I, I, P, P, P, I, I, P]
+        L.cpu_exl3_linear.restype = None
+        L.cpu_exl3_linear.argtypes = [P, I, P, P, I64, I64, P, P, I, I, I, I, I]
         _cpu = L
+    return _cpu
+
+
+def cpu_moe_routed(x, pick, wts, routed: Routed, R, slots, x_stride=None, bf16=False):
+    """The tuned CPU baseline (libcpulayer.so, cpu_layer.c) of moe_routed: the same function, decoded straight into
+    the products, OpenMP over column tiles; fp32 sums in a different order than the oracle's."""
+    _cpu_lib()
     x = np.ascontiguousarray(x)
     out = np.zeros((R, routed.dims), np.float32)
     _cpu.cpu_moe_routed(_p(x), _x_dtype(x, bf16), x_stride or routed.dims, _p(np.ascontiguousarray(pick, np.int32)),
@@ -315,6 +322,20 @@ def linear_plan(k: int, n: int):
     sk, wk = C.c_int(), C.c_int()
     lib().or_linear_plan(k, n, C.byref(sk), C.byref(wk))
     return sk.value, wk.value
+
+
+def cpu_exl3_linear(x, suh, T_strips, svh, M, K, N, k2, cb, bf16=False):
+    """The tuned CPU baseline (libcpulayer.so, cpu_layer.c) of exl3_rot_in then exl3_linear with fp32 out: the same
+    function on words in the strips layout, OpenMP over column tiles; fp32 sums in a different order than the
+    oracle's."""
+    _cpu_lib()
+    x = np.ascontiguousarray(x)
+    y = np.zeros((M, N), np.float32)
+    tw = 4 * k2
+    _cpu.cpu_exl3_linear(_p(x), _x_dtype(x, bf16), _p(np.ascontiguousarray(suh, dtype=np.uint16)),
+                         _p(np.ascontiguousarray(T_strips, dtype=np.uint32)), 8 * tw, (K // 16) * 8 * tw,
+                         _p(np.ascontiguousarray(svh, dtype=np.uint16)), _p(y), M, K, N, k2, cb)
+    return y
 
 
 def exl3_rot_in(x, suh, M, K, bf16=False):
