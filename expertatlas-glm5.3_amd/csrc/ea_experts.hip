@@ -240,6 +240,7 @@ __global__ void __launch_bounds__(NW * 64) grouped_kernel(
 // 1: fp32; limit clamps), * suh_d, FWHT, xd = fp16(* HAD_SCALE) (exl3_experts.cu:142-184). A pair marked in pclass
 // takes its splits from Z's split 0 and Zp's planes ([SKP - 1][2][P][N]), in split order. With only >= 0 a pair
 // whose class (pclass[p] != 0) is not `only` is left alone.
+constexpr int EPI_SPLITS = 4;  // K splits whose loads the gate / up epilogue issues together (more: in turn)
 __global__ void __launch_bounds__(64) gateup_epilogue_kernel(const float* __restrict__ Z, const int* __restrict__ pick,
                                                              const uint16_t* __restrict__ svh_g,
                                                              const uint16_t* __restrict__ svh_u,
@@ -253,37 +254,61 @@ __global__ void __launch_bounds__(64) gateup_epilogue_kernel(const float* __rest
     const int n = blk * 128 + 2 * lane;
     const bool part = pclass && pclass[p];
     if (only >= 0 && (int)part != only) return;
-    float g[2], u[2];
+    const int ns = part ? SKP : SK;
+    const size_t mstride = part ? (size_t)P * N : (size_t)SK * P * N;
+    auto split = [&](int s) __attribute__((always_inline)) {
+        return (part ? (s ? Zp + (size_t)(s - 1) * 2 * P * N : Z) : Z + (size_t)s * P * N) + (size_t)p * N + n;
+    };
+    // the scales and every split's gate and up values (8-byte loads: a lane's two columns) are all in flight before
+    // the first is used; a loop that loaded a split after adding the previous one waited for each in turn
+    const size_t at = (size_t)e * N + n;
+    const uint32_t sg2 = *reinterpret_cast<const uint32_t*>(svh_g + at);
+    const uint32_t su2 = *reinterpret_cast<const uint32_t*>(svh_u + at);
+    const uint32_t sd2 = *reinterpret_cast<const uint32_t*>(suh_d + at);
+    float g[2] = {0.f, 0.f}, u[2] = {0.f, 0.f};
+    if (ns <= EPI_SPLITS) {
+        float2 zg[EPI_SPLITS], zu[EPI_SPLITS];
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-        float sg = 0.f, su = 0.f;
-        const int ns = part ? SKP : SK;
+        for (int s = 0; s < EPI_SPLITS; ++s)
+            if (s < ns) {
+                zg[s] = *reinterpret_cast<const float2*>(split(s));
+                zu[s] = *reinterpret_cast<const float2*>(split(s) + mstride);
+            }
+#pragma unroll
+        for (int s = 0; s < EPI_SPLITS; ++s)
+            if (s < ns) {  // the splits in order from zero
+                g[0] += zg[s].x;
+                g[1] += zg[s].y;
+                u[0] += zu[s].x;
+                u[1] += zu[s].y;
+            }
+    } else {
         for (int s = 0; s < ns; ++s) {
-            const float* zs = part ? (s ? Zp + (size_t)(s - 1) * 2 * P * N : Z) : Z + (size_t)s * P * N;
-            const size_t mstride = part ? (size_t)P * N : (size_t)SK * P * N;
-            sg += zs[(size_t)p * N + n + j];
-            su += zs[mstride + (size_t)p * N + n + j];
+            const float2 zg = *reinterpret_cast<const float2*>(split(s));
+            const float2 zu = *reinterpret_cast<const float2*>(split(s) + mstride);
+            g[0] += zg.x;
+            g[1] += zg.y;
+            u[0] += zu.x;
+            u[1] += zu.y;
         }
-        g[j] = sg;
-        u[j] = su;
     }
     fwht128_w64(g[0], g[1], lane);
     fwht128_w64(u[0], u[1], lane);
     float v[2];
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
-        const size_t at = (size_t)e * N + n + j;
+        const float svg = h2f((uint16_t)(sg2 >> (16 * j))), svu = h2f((uint16_t)(su2 >> (16 * j)));
         float act;
         if (act_mode == 0) {
-            const float gg = fminf(bf16r(g[j] * HAD_SCALE * h2f(svh_g[at])), limit);
-            const float uu = fminf(fmaxf(bf16r(u[j] * HAD_SCALE * h2f(svh_u[at])), -limit), limit);
+            const float gg = fminf(bf16r(g[j] * HAD_SCALE * svg), limit);
+            const float uu = fminf(fmaxf(bf16r(u[j] * HAD_SCALE * svu), -limit), limit);
             act = bf16r(bf16r(gg / (1.f + expf_path(-gg))) * uu);
         } else {
-            const float gg = fminf(g[j] * HAD_SCALE * h2f(svh_g[at]), limit);
-            const float uu = fminf(fmaxf(u[j] * HAD_SCALE * h2f(svh_u[at]), -limit), limit);
+            const float gg = fminf(g[j] * HAD_SCALE * svg, limit);
+            const float uu = fminf(fmaxf(u[j] * HAD_SCALE * svu, -limit), limit);
             act = gg / (1.f + expf_path(-gg)) * uu;
         }
-        v[j] = act * h2f(suh_d[at]);
+        v[j] = act * h2f((uint16_t)(sd2 >> (16 * j)));
     }
     fwht128_w64(v[0], v[1], lane);
     *reinterpret_cast<uint32_t*>(xd + (size_t)p * N + n) =
