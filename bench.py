@@ -6,21 +6,28 @@
 A step is one pass of the hot path over one batch of synthetic input, with every input already in HBM:
   decode (default): one GLM-5.3 MoE layer of a TP=8 rank at batch 1 -- router top-8 from logits,
       the routed experts (moe.routed), the shared expert (EXL3 linears + SwiGLU) and their sum: ea_ffn_moe_decode,
-      one launch at one row, five above (route, gate|up, epilogue, down, combine); the default line also carries
-      the metric's second half, the 512-token prefill chunk (config 4), as the object "prefill512";
+      one launch at one row, five above (route, gate|up, epilogue, down, combine);
   multi (config 3): the same layer at 16 rows, uniform top-8 (no router bias), 70 % of the experts at 3 bits;
   stack (config 5): 75 resident layers (3-bit for 70 % of the experts), one token through all of them (us / token);
   linear (config 1): one 4-bit EXL3 linear 6144 x 2048 at one row (linear.call);
-  prefill512 / prefill2048 (config 4): prompt_experts.run over 512 / 2048 rows with Zipf(1.1) routing.
+  prefill512 / prefill2048 (config 4): prompt_experts.run over 512 / 2048 rows with Zipf(1.1) routing (a _planes0
+      suffix: without the pair plane, the reference's default atomic mode).
+The default run times config 2 and then, into the same line as objects of their own, the workloads named by --legs
+(the other BASELINE configs). Every GPU leg runs before any CPU work: a leg spins up on its own work (--spin-up
+seconds of untimed calls), runs one layer outside the timed region whose output it keeps, does its W warm-up steps,
+times exactly K steps launched one by one between synchronized events (a HIP graph replay of the same steps is
+reported beside it), and reads the library's device status word afterwards. Then, on the host, the oracle recomputes
+each kept layer (the check: max|diff| <= 2e-3 RMS(out), picks bit-exact; "parity" in the line) and the tuned CPU
+layer is timed on a bounded sample ("cpu_baseline"). The run exits 1 when a check fails or a status word is set.
+
 The decode configs cycle through several distinct resident layers and draw fresh router logits every layer, so the
-touched experts are not sitting in the 256 MB Infinity Cache. Their timed region replays the K steps from a HIP
-graph (as the reference runs decode); the same steps launched one by one are reported beside it. Prints one JSON
-line, with the library's path and hash and the device it ran on.
+touched experts are not sitting in the 256 MB Infinity Cache. Prints one JSON line, with the library's path and hash
+and the device it ran on.
 
 The dominant kernel's roofline is measured live: HIP events around each of its launches (on the stream the launches
 go to) over a further pass identical to the timed one; its algorithmic bytes per launch are the trellis + scales of
 every distinct expert the launch touches, the shared expert, the activations, logits and outputs. Its rocprof kernel
-duration and HBM traffic a launch come from the committed counter summary (profiles/layer1_kernel_config2.md).
+duration and HBM traffic a launch come from the committed counter summaries under profiles/.
 """
 from __future__ import annotations
 
@@ -38,6 +45,7 @@ HBM_PEAK_GBS = 8000.0        # MI355X HBM3E, GB/s
 FP16_PEAK_TFLOPS = 2500.0    # MI355X dense fp16 MFMA, TFLOP/s
 D, I, E, SLOTS = 6144, 256, 256, 8
 ROUTED_SCALE = 2.5           # config.zig:97,165 routed_scaling
+EXTRA_LEGS_DEFAULT = ("prefill512", "prefill2048", "linear", "multi", "stack")
 
 
 def baseline_metric() -> str:
@@ -51,13 +59,22 @@ def parse():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--config", default="decode",
-                    choices=["decode", "multi", "stack", "linear", "prefill512", "prefill2048"])
+                    choices=["decode", "multi", "stack", "linear", "prefill512", "prefill2048", "prefill512_planes0",
+                             "prefill2048_planes0"])
+    ap.add_argument("--legs", default=",".join(EXTRA_LEGS_DEFAULT),
+                    help="decode: the further workloads timed into the same line, each as an object of its own")
+    ap.add_argument("--no-extra", "--no-prefill", dest="no_extra", action="store_true",
+                    help="decode: the config-2 layer alone")
     ap.add_argument("--layers", type=int, default=8, help="distinct resident layers the decode configs cycle through")
     ap.add_argument("--path", default="fused", choices=["fused", "sequence"],
                     help="decode configs: ea_ffn_moe_decode, or the reference's launch sequence (topk, "
                          "moe.routed's six launches, the shared expert's linears, swiglu2, add)")
+    ap.add_argument("--planes", type=int, default=1, choices=[0, 1],
+                    help="prefill legs without a _planes0 suffix: 1 the pair plane and slot-ordered combine, 0 atomics")
+    ap.add_argument("--spin-up", type=float, default=0.3,
+                    help="seconds of untimed calls of each leg's own work before its warm-up steps")
+    ap.add_argument("--cpu-budget", type=float, default=8.0, help="seconds of CPU work each leg's CPU baseline samples")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--no-prefill", action="store_true", help="decode: leave out the 512-token prefill object")
     ap.add_argument("--router", action="store_true",
                     help="decode configs: compute each layer's logits from x by a bf16 router weight "
                          "(ea_ffn_moe_decode_router) instead of reading given logits")
@@ -249,8 +266,11 @@ class DecodeBench:
         return sum(int(lay.bytes[2][e]) for e in distinct) + P * I * 2 + P * D * 4
 
 
-def time_steps(fn, steps: int, warmup: int, torch, first: int = 0) -> float:
-    """Milliseconds a step over `steps` steps after `warmup` untimed ones, between two synchronised events."""
+def time_steps(fn, steps: int, warmup: int, torch, first: int = 0, spin=None) -> float:
+    """Milliseconds a step over `steps` steps after `warmup` untimed ones, between two synchronised events; `spin()`
+    (untimed calls of the leg's own work) runs right before the warm-up, with no idle gap after it."""
+    if spin is not None:
+        spin()
     for i in range(warmup):
         fn(first + i)
     torch.cuda.synchronize()
@@ -288,7 +308,7 @@ def upload_graph(g, stream: int, torch) -> None:
     torch.cuda.synchronize()
 
 
-def time_graph(step, steps: int, warmup: int, torch, first: int = 0) -> float:
+def time_graph(step, steps: int, warmup: int, torch, first: int = 0, spin=None) -> float:
     """Milliseconds a step, the steps replayed from a HIP graph: `warmup` steps captured into one graph and `steps`
     into another (step(i, stream) issues step i on the capture stream); both uploaded to the device (hipGraphUpload:
     the executable's one-time set-up, which a first replay would otherwise include; no step runs), the warm-up graph
@@ -309,6 +329,8 @@ def time_graph(step, steps: int, warmup: int, torch, first: int = 0) -> float:
     torch.cuda.synchronize()
     for g in graphs:
         upload_graph(g, side.cuda_stream, torch)
+    if spin is not None:
+        spin()
     graphs[0].replay()
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -480,6 +502,142 @@ def _oracle_routed(orc, host):
                       host.dims, host.width, host.cb)
 
 
+# ---- the checks of the timed kernels' outputs (run in the CPU phase, after every GPU leg) -----------------------
+
+CHECK_BAR = 2e-3  # max|diff| <= 2e-3 * RMS(out): the north star's bar for layer outputs
+
+
+def spin_up(fn, torch, seconds: float, span: int, max_calls: int = 100000) -> int:
+    """Untimed calls fn(0), fn(1), .. fn(span - 1), fn(0), .. until `seconds` of GPU-bound wall time have passed (at
+    least three calls; a synchronisation every 8 calls keeps the host near the GPU). Called right before a timed
+    region's warm-up steps: after an idle spell the GPU runs the first milliseconds of work slower (512-token prefill,
+    20 timed layers after 5 warm-up ones: 381-391 us a layer, against 322 us over 200), so the clocks come up on the
+    leg's own work, not on the W warm-up steps."""
+    t0 = time.perf_counter()
+    n = 0
+    while n < 3 or (time.perf_counter() - t0 < seconds and n < max_calls):
+        fn(n % max(span, 1))
+        n += 1
+        if n % 8 == 0:
+            torch.cuda.synchronize()
+    torch.cuda.synchronize()
+    return n
+
+
+def _status_after(device) -> int:
+    """The library's device status word after a leg's timed region (0: no kernel recorded an error); clears it."""
+    return int(device.device_status())
+
+
+def _ratio(got, want) -> tuple[float, bool]:
+    import numpy as np
+
+    got = np.asarray(got, np.float64)
+    want = np.asarray(want, np.float64)
+    rms = float(np.sqrt(np.mean(want * want)))
+    err = float(np.max(np.abs(got - want))) if got.size else 0.0
+    finite = bool(np.all(np.isfinite(got)))
+    return (err / rms if rms > 0 else float("inf")), finite
+
+
+def _host_routed(orc, hc: dict):
+    """The oracle's Routed over a layer's host copy; experts not copied point at a zero placeholder the oracle never
+    reads (it touches the picked experts only)."""
+    import numpy as np
+
+    mats = []
+    for m in range(3):
+        copied = hc["trellis"][m]
+        ph = np.zeros_like(next(iter(copied.values())))
+        mats.append([copied.get(e, ph) for e in range(hc["count"])])
+    k2 = hc["k2"]
+    return orc.Routed(mats, [k2, k2, k2], hc["suh_g"], hc["suh_u"], hc["svh_g"], hc["svh_u"], hc["suh_d"],
+                      hc["svh_d"], hc["dims"], hc["width"], hc["cb"])
+
+
+def _shared_oracle(orc, sh: list, x, R: int):
+    """forward.mlp (forward.zig:2328-2341) on the oracle: bf16 gate / up linears, swiglu2, the fp32 down linear."""
+    outs = []
+    for m in range(2):
+        L = sh[m]
+        tw = 4 * L["k2"]
+        xh = orc.exl3_rot_in(x, L["suh"], R, L["k"])
+        outs.append(orc.exl3_linear(xh, L["words"], 8 * tw, (L["k"] // 16) * 8 * tw, L["svh"], R, L["k"], L["n"],
+                                    L["k2"], L["cb"], L["sk"], L["wk"], y_dtype=1))
+    act = orc.swiglu2(outs[0], outs[1])
+    L = sh[2]
+    tw = 4 * L["k2"]
+    xh = orc.exl3_rot_in(act, L["suh"], R, L["k"], bf16=True)
+    return orc.exl3_linear(xh, L["words"], 8 * tw, (L["k"] // 16) * 8 * tw, L["svh"], R, L["k"], L["n"], L["k2"],
+                           L["cb"], L["sk"], L["wk"], y_dtype=2)
+
+
+def decode_check_data(bench, j: int, rows: list[int]) -> dict:
+    """Layer launch j once more, eagerly and outside every timed region, then its outputs and the host copies of
+    everything the oracle needs to recompute the listed rows (a row's output depends on its own activations and
+    logits only)."""
+    import numpy as np
+
+    torch = bench.torch
+    bench.launch(j)
+    torch.cuda.synchronize()
+    l = bench.layer_of(j)
+    d = {"j": j, "rows": rows, "R": bench.R,
+         "x": bench.x.view(torch.int16).cpu().numpy().view(np.uint16)[rows].copy(),
+         "logits": bench.logits[j].cpu().numpy()[rows].copy(), "bias": bench.bias.cpu().numpy().copy(),
+         "out": bench.out.cpu().numpy()[rows].copy(), "pick": bench.pick[j].cpu().numpy()[rows].copy(),
+         "wts": bench.wts[j].cpu().numpy()[rows].copy(), "sequence": bench.path != "fused"}
+    d["layer"] = bench.layers[l].host_copy(np.unique(d["pick"]))
+    d["shared"] = bench.shared[l].host_copy()
+    if bench.router:
+        d["router_w"] = bench.router_w[l].view(torch.int16).cpu().numpy().view(np.uint16).copy()
+    return d
+
+
+def decode_check(orc, d: dict) -> dict:
+    """The oracle's ops.topk -> moe.routed -> forward.mlp -> add on the checked rows against the GPU's layer."""
+    import numpy as np
+
+    R = len(d["rows"])
+    res = {"launch": d["j"], "rows_checked": R, "of_rows": d["R"], "bar": CHECK_BAR}
+    logits = d["logits"]
+    if "router_w" in d:
+        want_logits = orc.router(d["x"], d["router_w"], 0)
+        res["logits_bit_exact"] = bool(np.array_equal(want_logits.view(np.uint32), logits.view(np.uint32)))
+    pick, wts = orc.topk8(logits, d["bias"], ROUTED_SCALE)
+    res["picks_bit_exact"] = bool(np.array_equal(pick, d["pick"]) and
+                                  np.array_equal(wts.view(np.uint32), d["wts"].view(np.uint32)))
+    if not set(np.unique(pick)) <= set(d["layer"]["trellis"][0]):
+        res.update(max_diff_over_rms=None, ok=False)
+        return res
+    want = orc.moe_routed(d["x"], pick, wts, _host_routed(orc, d["layer"]), R, SLOTS)
+    want = want + _shared_oracle(orc, d["shared"], d["x"], R)
+    r, finite = _ratio(d["out"], want)
+    res["max_diff_over_rms"] = float(f"{r:.3e}")
+    res["ok"] = bool(finite and r <= CHECK_BAR and res["picks_bit_exact"] and res.get("logits_bit_exact", True))
+    return res
+
+
+def prefill_check(orc, d: dict) -> dict:
+    """The oracle's prompt_experts.run (fp32 sums, no bf16 rounding) on sampled rows against the GPU's output."""
+    R = len(d["rows"])
+    want = orc.prompt_experts(d["x"], d["pick"], d["wts"], _host_routed(orc, d["layer"]), R, SLOTS)
+    r, finite = _ratio(d["out"], want)
+    return {"rows_checked": R, "of_rows": d["R"], "bar": CHECK_BAR, "max_diff_over_rms": float(f"{r:.3e}"),
+            "ok": bool(finite and r <= CHECK_BAR)}
+
+
+def linear_check(orc, d: dict) -> dict:
+    """The oracle's exl3 rotIn -> linear (fp32 out) against the GPU's linear.call."""
+    L = d["lin"]
+    tw = 4 * L["k2"]
+    xh = orc.exl3_rot_in(d["x"], L["suh"], 1, L["k"])
+    want = orc.exl3_linear(xh, L["words"], 8 * tw, (L["k"] // 16) * 8 * tw, L["svh"], 1, L["k"], L["n"], L["k2"],
+                           L["cb"], L["sk"], L["wk"], y_dtype=2)
+    r, finite = _ratio(d["out"], want)
+    return {"rows_checked": 1, "bar": 1e-4, "max_diff_over_rms": float(f"{r:.3e}"), "ok": bool(finite and r <= 1e-4)}
+
+
 # ---- the workloads' lines ------------------------------------------------------------------------------------------
 
 DATA = ("synthetic: seeded random EXL3 trellis words generated on the GPU (any bit stream is a valid tile), "
@@ -495,12 +653,11 @@ WORKLOADS = {  # name -> (workload, rows, mixed widths, layers a step, unit)
               "shared experts), one token through all of them", 1, True, 75, "us/token"),
 }
 
-
-def _line(args, value, unit, ms, config, roofline, cpu) -> dict:
-    return {"metric": baseline_metric(), "value": round(value, 3), "unit": unit, "n_gpus": 1, "steps": args.steps,
-            "warmup": args.warmup, "ms_per_step": round(ms, 6), "higher_is_better": False, "scaling": "weak",
-            "vs_baseline": None, "dtype": "fp16", "data": DATA, "config": config, "roofline": roofline,
-            "cpu_baseline": cpu}
+def _line(args, value, unit, ms, config, roofline, steps=None, warmup=None) -> dict:
+    return {"metric": baseline_metric(), "value": round(value, 3), "unit": unit, "n_gpus": 1,
+            "steps": args.steps if steps is None else steps, "warmup": args.warmup if warmup is None else warmup,
+            "ms_per_step": round(ms, 6), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+            "dtype": "fp16", "data": DATA, "config": config, "roofline": roofline, "cpu_baseline": None}
 
 
 def recorded_figure(profile: str, key: str) -> float | None:
@@ -515,24 +672,44 @@ def recorded_figure(profile: str, key: str) -> float | None:
     return None
 
 
-def run_decode(args, torch, np) -> dict:
-    workload, R, mixed, per_step, unit = WORKLOADS[args.config]
-    n_layers = 75 if args.config == "stack" else args.layers
+class Leg:
+    """One workload's GPU measurement (its line without cpu_baseline / parity) and the CPU work it leaves for after
+    every GPU leg: the oracle check of the output it kept, and the CPU baseline."""
+
+    def __init__(self, name: str, line: dict, check, cpu):
+        self.name, self.line, self.check, self.cpu = name, line, check, cpu
+
+
+def run_decode(args, torch, np, name: str) -> Leg:
+    from ea_exl3 import device
+    from ea_exl3._lib import check, lib
+
+    workload, R, mixed, per_step, unit = WORKLOADS[name]
+    n_layers = 75 if name == "stack" else args.layers
     total = args.warmup + args.steps
     bench = DecodeBench(R, n_layers, per_step, mixed, args.seed, 3 * total + 2, args.path,
-                        uniform=args.config == "multi", router=args.router)
-    # the timed region: K whole steps replayed from a HIP graph (how the reference runs decode); the same steps
-    # launched one by one from the host are timed beside it
-    graph_ms = time_graph(bench.step, args.steps, args.warmup, torch) if args.path == "fused" else None
-    eager_ms = time_steps(bench.step, args.steps, args.warmup, torch, first=total)
-    ms = graph_ms if graph_ms is not None else eager_ms
+                        uniform=name == "multi", router=args.router)
+    device.device_status()  # clear the status word before this leg
+    # the layer whose output the oracle checks: launch 3 total (none of the timed ones), rows 0 and R - 1 (and two
+    # between at 16 rows)
+    rows = sorted({0, R // 3, (2 * R) // 3, R - 1})
+    chk = decode_check_data(bench, 3 * total * per_step, rows)
+    spun = []
+
+    def spin():
+        spun.append(spin_up(bench.launch, torch, args.spin_up, max(args.warmup * per_step, 1)))
+
+    # the timed region: K steps launched one by one between synchronized events, as a host issues layers; the same
+    # steps replayed from a HIP graph are reported beside it
+    eager_ms = time_steps(bench.step, args.steps, args.warmup, torch, first=total, spin=spin)
+    graph_ms = time_graph(bench.step, args.steps, args.warmup, torch, spin=spin) if args.path == "fused" else None
+    ms = eager_ms
     # the same number of steps again, timing each launch of the dominant kernel on the stream it runs on
     ev = []
+    spin()
     for i in range(args.warmup):
         bench.step(2 * total + i)
     torch.cuda.synchronize()
-    from ea_exl3._lib import check, lib
-
     if args.path == "fused":
         check(lib().ea_profile_enable(1), "profile_enable")
     for i in range(args.steps):
@@ -540,6 +717,7 @@ def run_decode(args, torch, np) -> dict:
     torch.cuda.synchronize()
     if args.path == "fused":
         check(lib().ea_profile_enable(0), "profile_enable")
+    status = _status_after(device)
     picks = bench.pick.cpu().numpy()
     stages = None
     one_launch = args.path == "fused" and R == 1
@@ -555,8 +733,8 @@ def run_decode(args, torch, np) -> dict:
         kernel = ("route_kernel + gateup_wide_kernel (ea_ffn_moe_decode's first two launches, timed together: the "
                   "window's top-8 and grouping once, then the gate and up EXL3 GEMV of every touched routed expert and "
                   "of the shared expert)")
-        stages = {name: round(sum(ms_[k] for _, ms_ in ev) / len(ev) * 1e3, 3)
-                  for k, name in enumerate(("gateup_us", "epilogue_us", "down_us", "combine_us"))}
+        stages = {nm: round(sum(ms_[k] for _, ms_ in ev) / len(ev) * 1e3, 3)
+                  for k, nm in enumerate(("gateup_us", "epilogue_us", "down_us", "combine_us"))}
     else:
         durs = [a.elapsed_time(b) for _, a, b, _ in ev]
         nbytes = [bench.grouped_bytes(j, picks, w) for j, _, _, w in ev]
@@ -565,17 +743,16 @@ def run_decode(args, torch, np) -> dict:
     avg_b = sum(nbytes) / len(nbytes)
     timing = "HIP events recorded on the launch stream around each launch (dispatch included)"
     event_us = None
-    if one_launch and graph_ms is not None:
-        # one launch a layer: the timed region's average (HIP events around the graph replay on the launch stream) is
-        # the kernel's average launch duration, back to back as a model runs it; each launch timed between its own
-        # events (which adds their dispatch) is reported beside it
+    if one_launch:
+        # one launch a layer: the timed region's average is the kernel's average launch duration, back to back as a
+        # model runs it; each launch timed between its own events (which adds their dispatch) is reported beside it
         event_us = round(avg_ms * 1e3, 3)
-        avg_ms = graph_ms
-        timing = ("HIP events around the graph replay of the timed layers, on the launch stream: one launch a layer, "
-                  "so the per-layer time is the kernel's average launch duration (gaps between launches included)")
+        avg_ms = ms / per_step
+        timing = ("HIP events around the timed layers on the launch stream: one launch a layer, so the per-layer "
+                  "time is the kernel's average launch duration (gaps between launches included)")
     achieved = avg_b / (avg_ms * 1e-3) / 1e9
     # the step's own roofline, from the timed steps' launches
-    first = (args.warmup if graph_ms is not None else total + args.warmup) * per_step
+    first = (total + args.warmup) * per_step
     lb = [bench.launch_bytes(first + j, picks) for j in range(args.steps * per_step)]
     step_b = sum(b for b, _ in lb) / args.steps
     step_f = sum(f for _, f in lb) / args.steps
@@ -585,11 +762,15 @@ def run_decode(args, torch, np) -> dict:
                               for j in range(args.steps * per_step)]))
     if args.router:
         workload += "; logits computed from x by a bf16 router weight [256, 6144] (ea_ffn_moe_decode_router)"
-    config = {"workload": workload, "path": args.path, "timing": "hip graph" if graph_ms is not None else "eager",
-              "eager_us": round(eager_ms * 1e3, 3), "layers_resident": n_layers, "distinct_experts_per_layer":
-              round(distinct, 2), "step_bytes": int(step_b), "step_flops": int(step_f),
-              "step_roofline_us": round(t_roof_us, 3), "step_hbm_frac": round(t_roof_us / us, 4),
-              "step_gbs": round(step_b / (us * 1e-6) / 1e9, 1)}
+    config = {"workload": workload, "path": args.path,
+              "timing": "eager: the K steps launched one by one between synchronized events on the launch stream",
+              "graph_us": None if graph_ms is None else round(graph_ms * 1e3, 3),
+              "graph_note": "the same K steps replayed from one HIP graph between synchronized events: the replay "
+                            "carries a fixed start-up cost (about 25 us) that 200 steps amortize and 20 do not",
+              "spin_up_calls": spun, "layers_resident": n_layers, "distinct_experts_per_layer": round(distinct, 2),
+              "step_bytes": int(step_b), "step_flops": int(step_f), "step_roofline_us": round(t_roof_us, 3),
+              "step_hbm_frac": round(t_roof_us / us, 4), "step_gbs": round(step_b / (us * 1e-6) / 1e9, 1),
+              "device_status": status}
     roofline = {"kernel": kernel, "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None, "avg_launch_us": round(avg_ms * 1e3, 3),
                 "bytes_per_launch": int(avg_b), "launches_timed": len(durs), "timing": timing}
@@ -597,10 +778,11 @@ def run_decode(args, torch, np) -> dict:
         roofline["event_us_per_launch"] = event_us
     if stages:
         roofline["layer_stages"] = stages
-    if args.config == "decode" and one_launch:
-        prof = "layer1_kernel_config2.md"
-        rp = recorded_figure(prof, "layer1_kernel_avg_us")
-        if rp:
+    prof = {"decode": "layer1_kernel_config2.md", "multi": "decode_layer_config3.md"}.get(name)
+    if prof and args.path == "fused" and not args.router:
+        key = "layer1_kernel" if one_launch else "gateup_wide_kernel"
+        rp = recorded_figure(prof, f"{key}_avg_us")
+        if rp and one_launch:
             roofline["rocprof_avg_us"] = rp
             roofline["rocprof_frac"] = round(avg_b / (rp * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)
             roofline["rocprof_source"] = f"profiles/{prof} (rocprofv3 --kernel-trace --stats)"
@@ -608,12 +790,17 @@ def run_decode(args, torch, np) -> dict:
         if tr:
             roofline["traffic"] = int(tr)
             roofline["traffic_source"] = f"profiles/{prof} (rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE; copy-calibrated)"
-    cpu = None if args.no_cpu_baseline else cpu_baseline_decode(args.seed, R, mixed, layers_per_unit=per_step,
-                                                                unit=unit)
-    return _line(args, us, unit, ms, config, roofline, cpu)
+    line = _line(args, us, unit, ms, config, roofline)
+    del bench
+    torch.cuda.empty_cache()
+
+    def cpu():
+        return cpu_baseline_decode(args.seed, R, mixed, budget_s=args.cpu_budget, layers_per_unit=per_step, unit=unit)
+
+    return Leg(name, line, lambda orc: decode_check(orc, chk), cpu)
 
 
-def run_linear(args, torch, np) -> dict:
+def run_linear(args, torch, np) -> Leg:
     """Config 1: linear.call of one 4-bit EXL3 linear 6144 x 2048 at one row (one launch of the small-row kernel)."""
     from ea_exl3 import device, linear
     from ea_exl3._lib import Linear as _Linear, check, lib
@@ -639,8 +826,19 @@ def run_linear(args, torch, np) -> dict:
         if r:
             check(r, "linear.call")
 
-    eager_ms = time_steps(step, args.steps, args.warmup, torch)
-    ms = time_graph(step, args.steps, args.warmup, torch)
+    device.device_status()
+    step(0)
+    torch.cuda.synchronize()
+    chk = {"x": x.view(torch.int16).cpu().numpy().view(np.uint16).copy(), "out": y.cpu().numpy().copy(),
+           "lin": lins[0].host_copy()}
+    spun = []
+
+    def spin():
+        spun.append(spin_up(step, torch, args.spin_up, len(lins)))
+
+    ms = time_steps(step, args.steps, args.warmup, torch, spin=spin)
+    graph_ms = time_graph(step, args.steps, args.warmup, torch, spin=spin)
+    status = _status_after(device)
     b = lins[0].bytes() + K * 2 + N * 4
     f = 2 * K * N
     us = ms * 1e3
@@ -649,10 +847,12 @@ def run_linear(args, torch, np) -> dict:
     config = {"workload": "config 1: one EXL3 4-bit linear K 6144 x N 2048 at one fp16 row, fp32 out (linear.call: "
                           "one launch of the small-row kernel, rotation in the kernel)", "linears_resident": args.layers,
               "step_bytes": b, "step_roofline_us": round(t_roof, 3), "step_hbm_frac": round(t_roof / us, 4),
-              "timing": "HIP graph of the timed calls, replayed once between synchronized events",
-              "eager_us": round(eager_ms * 1e3, 3)}
-    roofline = {"kernel": "lin_small_kernel (the whole call)", "bound": "hbm", "achieved": round(gbs, 1),
-                "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None}
+              "timing": "eager: the K calls launched one by one between synchronized events on the launch stream",
+              "graph_us": round(graph_ms * 1e3, 3), "spin_up_calls": spun, "device_status": status}
+    roofline = {"kernel": "lin_small_kernel (the whole call: one launch)", "bound": "hbm", "achieved": round(gbs, 1),
+                "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                "avg_launch_us": round(us, 3), "bytes_per_launch": b,
+                "timing": "HIP events around the timed calls on the launch stream: one launch a call"}
     prof = "lin_small_kernel_config1.md"
     rp = recorded_figure(prof, "lin_small_kernel_avg_us")
     if rp:
@@ -663,18 +863,20 @@ def run_linear(args, torch, np) -> dict:
     if tr:
         roofline["traffic"] = int(tr)
         roofline["traffic_source"] = f"profiles/{prof} (rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE; copy-calibrated)"
-    cpu = None if args.no_cpu_baseline else cpu_baseline_linear(args.seed)
-    return _line(args, us, "us/linear", ms, config, roofline, cpu)
+    line = _line(args, us, "us/linear", ms, config, roofline)
+    del lins
+    torch.cuda.empty_cache()
+    return Leg("linear", line, lambda orc: linear_check(orc, chk),
+               lambda: cpu_baseline_linear(args.seed, budget_s=args.cpu_budget))
 
 
-def run_prefill(args, torch, np, R: int, steps: int | None = None, warmup: int | None = None) -> dict:
+def run_prefill(args, torch, np, R: int, planes: int = 1) -> Leg:
     """Config 4: prompt_experts.run over R rows, Zipf(1.1) routing, 4-bit experts. Its binding roof is HBM (about 68
     flops a byte at 512 rows, below the ~312 ridge); the MFMA fraction is reported beside it."""
     from ea_exl3 import device, prompt_experts, synth
     from ea_exl3.resident import DeviceRouted
 
-    steps = args.steps if steps is None else steps
-    warmup = args.warmup if warmup is None else warmup
+    steps, warmup = args.steps, args.warmup
     lay = DeviceRouted(args.seed, E, D, I, k2=8, cb=1)
 
     class _Ex:
@@ -689,30 +891,45 @@ def run_prefill(args, torch, np, R: int, steps: int | None = None, warmup: int |
     gen.manual_seed(args.seed + 3)
     x = torch.randn((R, D), device="cuda", generator=gen).to(torch.float16)
     out = torch.zeros((R, D), dtype=torch.float32, device="cuda")
-    sc = prompt_experts.Scratch(ex, R, SLOTS)
+    sc = prompt_experts.Scratch(ex, R, SLOTS, planes=bool(planes))
     s = device.stream()
 
     def step(i, stream=None):
         prompt_experts.run(s if stream is None else stream, x.data_ptr(), D, dp.data_ptr(), dw.data_ptr(), ex, sc,
                            out.data_ptr(), R, do_round=False, x_dtype=0)
 
-    ms = time_steps(step, steps, warmup, torch)
-    graph_ms = time_graph(step, steps, warmup, torch)
+    device.device_status()
+    step(0)
+    torch.cuda.synchronize()
+    rows = sorted(set(np.linspace(0, R - 1, 8).astype(int).tolist()))
+    chk = {"R": R, "rows": rows, "x": x.view(torch.int16).cpu().numpy().view(np.uint16)[rows].copy(),
+           "pick": pick[rows].copy(), "wts": wts[rows].copy(), "out": out.cpu().numpy()[rows].copy()}
+    chk["layer"] = lay.host_copy(np.unique(chk["pick"]))
+    spun = []
+
+    def spin():
+        spun.append(spin_up(step, torch, args.spin_up, 1))
+
+    ms = time_steps(step, steps, warmup, torch, spin=spin)
+    graph_ms = time_graph(step, steps, warmup, torch, spin=spin)
+    status = _status_after(device)
     distinct = sorted(set(int(e) for e in pick.reshape(-1)))
     b = sum(lay.expert_bytes(e) for e in distinct) + R * D * 2 + R * D * 4 + R * SLOTS * 8
     f = 2 * R * SLOTS * 3 * D * I
     us = ms * 1e3
     t_hbm, t_mfma = b / (HBM_PEAK_GBS * 1e9) * 1e6, f / (FP16_PEAK_TFLOPS * 1e12) * 1e6
     gbs, tfs = b / (us * 1e-6) / 1e9, f / (us * 1e-6) / 1e12
+    mode = ("planes 1: the pair plane and the slot-ordered combine (the same bits every run)" if planes else
+            "planes 0: down items add into out with fp32 atomics in arrival order (the reference's default mode 0)")
     config = {"workload": f"config 4: prefill chunk of {R} tokens x 6144 through prompt_experts.run, Zipf(1.1) top-8 "
-                          "routing over 256 4-bit experts", "distinct_experts": len(distinct), "step_bytes": b,
-              "step_flops": f, "step_roofline_us": round(max(t_hbm, t_mfma), 3),
+                          "routing over 256 4-bit experts", "mode": mode, "distinct_experts": len(distinct),
+              "step_bytes": b, "step_flops": f, "step_roofline_us": round(max(t_hbm, t_mfma), 3),
               "step_roof_frac": round(max(t_hbm, t_mfma) / us, 4), "step_gbs": round(gbs, 1),
               "step_tflops": round(tfs, 2), "mfma_frac": round(tfs / FP16_PEAK_TFLOPS, 4),
-              "timing": "launched one by one between synchronized events (the two item lists on two streams run "
-                        "side by side)", "graph_us": round(graph_ms * 1e3, 3),
+              "timing": "eager: the K layers launched one by one between synchronized events (the two item lists "
+                        "on two streams run side by side)", "graph_us": round(graph_ms * 1e3, 3),
               "graph_note": "the same layers replayed from a HIP graph: the runtime runs the side stream's branch after "
-                            "the main one, not beside it"}
+                            "the main one, not beside it", "spin_up_calls": spun, "device_status": status}
     roofline = {"kernel": "prompt_experts.run (whole call: route, rot_in, gate|up item GEMMs, epilogue, down item "
                           "GEMMs, combine)", "bound": "hbm" if t_hbm >= t_mfma else "mfma",
                 "achieved": round(gbs, 1) if t_hbm >= t_mfma else round(tfs, 2),
@@ -722,12 +939,27 @@ def run_prefill(args, torch, np, R: int, steps: int | None = None, warmup: int |
                 "mfma": {"achieved": round(tfs, 2), "peak": FP16_PEAK_TFLOPS, "unit": "TFLOP/s",
                          "frac": round(tfs / FP16_PEAK_TFLOPS, 4)}}
     prof = "prefill_config4.md"
-    tr = recorded_figure(prof, "traffic_bytes_per_layer" + ("" if R == 512 else f"_{R}"))
+    key = "traffic_bytes_per_layer" + ("" if R == 512 else f"_{R}") + ("" if planes else "_planes0")
+    tr = recorded_figure(prof, key)
     if tr is not None:  # HBM bytes of the whole layer (every kernel's FETCH_SIZE + WRITE_SIZE, copy-calibrated)
         roofline["traffic"] = int(tr)
         roofline["traffic_source"] = f"profiles/{prof} (rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE; copy-calibrated)"
-    cpu = None if args.no_cpu_baseline else cpu_baseline_prefill(args.seed, R)
-    return _line(args, us, "us/layer", ms, config, roofline, cpu) | {"steps": steps, "warmup": warmup}
+    line = _line(args, us, "us/layer", ms, config, roofline, steps, warmup)
+    del lay, sc
+    torch.cuda.empty_cache()
+    return Leg(f"prefill{R}", line, lambda orc: prefill_check(orc, chk),
+               lambda: cpu_baseline_prefill(args.seed, R, budget_s=args.cpu_budget))
+
+
+def run_leg(args, torch, np, name: str) -> Leg:
+    if name in WORKLOADS:
+        return run_decode(args, torch, np, name)
+    if name == "linear":
+        return run_linear(args, torch, np)
+    if name.startswith("prefill"):
+        return run_prefill(args, torch, np, int(name[len("prefill"):].split("_")[0]),
+                           planes=0 if name.endswith("_planes0") else args.planes)
+    raise ValueError(name)
 
 
 def main() -> int:
@@ -744,22 +976,36 @@ def main() -> int:
     device.init(0)
     if args.copy_calibration:
         copy_calibration(torch)
-    if args.config in WORKLOADS:
-        result = run_decode(args, torch, np)
-    elif args.config == "linear":
-        result = run_linear(args, torch, np)
-    else:
-        result = run_prefill(args, torch, np, 512 if args.config == "prefill512" else 2048)
-    if args.config == "decode" and not args.no_prefill:
-        # the metric's second half: the 512-token prefill chunk (config 4), timed over the line's own steps and
-        # warm-up (a layer is ~0.33 ms, so the timed region stays well under a second)
-        pf = run_prefill(args, torch, np, 512)
-        result["prefill512"] = {k: pf[k] for k in ("value", "unit", "steps", "warmup", "ms_per_step", "config",
-                                                   "roofline", "cpu_baseline")}
+    names = [args.config]
+    if args.config == "decode" and not args.no_extra:
+        names += [n for n in args.legs.split(",") if n and n != args.config]
+    # every GPU leg first, each with its own spin-up, oracle-checked launch and status word; then the CPU work
+    legs = []
+    for n in names:
+        t0 = time.perf_counter()
+        legs.append(run_leg(args, torch, np, n))
+        print(f"# {n}: {legs[-1].line['value']} {legs[-1].line['unit']} ({time.perf_counter() - t0:.1f} s)",
+              file=sys.stderr, flush=True)
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as orc  # the checker and the CPU baseline: test infrastructure, never on the timed path
+
+    ok = True
+    for leg in legs:
+        t0 = time.perf_counter()
+        leg.line["parity"] = leg.check(orc)
+        ok = ok and leg.line["parity"]["ok"] and leg.line["config"]["device_status"] == 0
+        if not args.no_cpu_baseline:
+            leg.line["cpu_baseline"] = leg.cpu()
+        print(f"# {leg.name}: oracle check {leg.line['parity']} ({time.perf_counter() - t0:.1f} s)", file=sys.stderr,
+              flush=True)
+    result = legs[0].line
+    keep = ("value", "unit", "steps", "warmup", "ms_per_step", "config", "roofline", "cpu_baseline", "parity")
+    for leg in legs[1:]:
+        result[leg.name] = {k: leg.line[k] for k in keep}
     result["library"] = library_identity()
     result["device"] = device_identity(torch)
     print(json.dumps(result))
-    return 0
+    return 0 if ok else 1
 
 
 if __name__ == "__main__":

@@ -35,12 +35,13 @@ class DeviceRouted:
         self.k2_host = k2s
         self.count, self.dims, self.width, self.cb = E, D, I, cb
         shapes = [(D, I), (D, I), (I, D)]
-        self.slabs, self.ptr, self.k2, self.bytes = [], [], [], []
+        self.slabs, self.ptr, self.k2, self.bytes, self.offs = [], [], [], [], []
         for (K, N) in shapes:
             sizes = [(K // 16) * (N // 16) * 4 * int(w) * 4 for w in k2s]
             offs = np.concatenate([[0], np.cumsum([(s + 255) & ~255 for s in sizes])]).astype(np.int64)
             slab = _words(gen, int(offs[-1]) // 4)
             self.slabs.append(slab)
+            self.offs.append(offs)
             self.ptr.append(device.upload(offs[:-1] + slab.data_ptr()))
             self.k2.append(device.upload(k2s))
             self.bytes.append(np.array(sizes, np.int64))
@@ -65,6 +66,19 @@ class DeviceRouted:
     def total_bytes(self) -> int:
         return int(sum(s.numel() * 4 for s in self.slabs))
 
+    def host_copy(self, experts) -> dict:
+        """The named experts' trellis words (per matrix: {expert: uint32 array}), the width table and every stacked
+        scale, copied to host memory (synchronous): what a host-side check of this layer reads."""
+        out = {"trellis": [{}, {}, {}], "k2": self.k2_host.copy(), "dims": self.dims, "width": self.width,
+               "cb": self.cb, "count": self.count}
+        for m in range(3):
+            for e in sorted(set(int(e) for e in experts)):
+                a, b = int(self.offs[m][e]) // 4, int(self.offs[m][e] + self.bytes[m][e]) // 4
+                out["trellis"][m][e] = self.slabs[m][a:b].cpu().numpy().view(np.uint32).copy()
+        for name in ("suh_g", "suh_u", "svh_g", "svh_u", "suh_d", "svh_d"):
+            out[name] = getattr(self, name).view(torch.int16).cpu().numpy().view(np.uint16).copy()
+        return out
+
 
 class DeviceLinear:
     """One EXL3 linear (strips layout) resident on the device, (sk, wk) from plan()."""
@@ -82,6 +96,13 @@ class DeviceLinear:
     def bytes(self) -> int:
         return self.words.numel() * 4 + 2 * (self.k + self.n)
 
+    def host_copy(self) -> dict:
+        """Words (strips layout), suh, svh and the plan, copied to host memory (synchronous)."""
+        return {"words": self.words.cpu().numpy().view(np.uint32).copy(),
+                "suh": self.suh.view(torch.int16).cpu().numpy().view(np.uint16).copy(),
+                "svh": self.svh.view(torch.int16).cpu().numpy().view(np.uint16).copy(),
+                "k": self.k, "n": self.n, "k2": self.k2, "cb": self.cb, "sk": self.sk, "wk": self.wk}
+
 
 class DeviceShared:
     """The shared expert of a TP=8 rank: gate and up (D -> I) and down (I -> D)."""
@@ -95,6 +116,9 @@ class DeviceShared:
 
     def bytes(self) -> int:
         return self.gate.bytes() + self.up.bytes() + self.down.bytes()
+
+    def host_copy(self) -> list:
+        return [self.gate.host_copy(), self.up.host_copy(), self.down.host_copy()]
 
 
 def linear_ptrs(ls):
