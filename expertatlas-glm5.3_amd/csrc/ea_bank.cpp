@@ -17,6 +17,7 @@
 #include <cstring>
 #include <map>
 #include <memory>
+#include <new>
 #include <string>
 #include <vector>
 
@@ -295,7 +296,7 @@ static int open_file(const std::string& path, std::unique_ptr<File>& out) {
             const Json& d = sh->arr[i];
             if (d.kind != Json::NUM || !d.integral) return EA_BAD_SAFETENSORS;
             e.shape[i] = d.u;
-            n *= d.u;
+            if (__builtin_mul_overflow(n, (uint64_t)d.u, &n)) return EA_BAD_SAFETENSORS;  // no such file fits
         }
         for (int i = 0; i < 2; ++i)
             if (of->arr[i].kind != Json::NUM || !of->arr[i].integral) return EA_BAD_SAFETENSORS;
@@ -317,60 +318,34 @@ static bool ends_with(const std::string& s, const std::string& t) {
     return s.size() >= t.size() && s.compare(s.size() - t.size(), t.size(), t) == 0;
 }
 
-// split.zig:18-77 for the EXL3 linears: the output-split projections cut their trellis' second axis and their svh,
-// the input-split ones their trellis' first axis and their suh; codebook markers and the other scale are whole.
+// The split rules of the tensors this library reads, the MoE block's (split.zig:18-77 holds the whole model's table,
+// attention and MTP included, with the same rule for these names). An EXL3 linear of the block -- a routed expert, a
+// shared expert, a dense MLP projection -- is cut by its projection's role: gate and up split their outputs (the
+// trellis' tile columns and svh), down its inputs (the trellis' tile rows and suh); codebook markers and the scale on
+// the uncut side stay whole. The router's weight and score-correction bias stay whole. Any other name has no rule.
 static int rule_of(const std::string& name, Rule& r) {
-    const size_t dot = name.rfind('.');
-    if (dot == std::string::npos) return EA_NO_SPLIT_RULE;
-    const std::string part = name.substr(dot + 1), stem = name.substr(0, dot);
-    const bool exl3 = part == "trellis" || part == "suh" || part == "svh" || part == "mul1" || part == "mcg";
-    const char* marks[] = {".mlp.experts.", ".mlp.shared_experts.", ".mlp.gate_proj", ".mlp.up_proj", ".mlp.down_proj",
-                           ".self_attn."};
-    bool linear = false;
-    for (const char* m : marks)
-        if (stem.find(m) != std::string::npos) linear = true;
-    if (exl3 && linear) {
-        const char* replicated[] = {".self_attn.q_a_proj", ".self_attn.kv_a_proj_with_mqa", ".self_attn.indexer.wq_b"};
-        for (const char* s : replicated)
-            if (ends_with(stem, s)) {
-                r = REP;
-                return EA_OK;
-            }
-        if (part == "mul1" || part == "mcg") {
-            r = REP;
-            return EA_OK;
-        }
-        const char* outs[] = {"gate_proj", "up_proj", ".self_attn.q_b_proj"};
-        const char* ins[] = {"down_proj", ".self_attn.o_proj"};
-        for (const char* s : outs)
-            if (ends_with(stem, s)) {
-                r = part == "trellis" ? DIM1 : part == "svh" ? ROW : REP;
-                return EA_OK;
-            }
-        for (const char* s : ins)
-            if (ends_with(stem, s)) {
-                r = (part == "trellis" || part == "suh") ? ROW : REP;
-                return EA_OK;
-            }
-    }
-    if (ends_with(name, ".self_attn.kv_b_proj.weight") || name == "lm_head.weight") {
-        r = ROW;
-        return EA_OK;
-    }
-    const char* reps[] = {"model.norm.weight", "_layernorm.weight", ".mlp.gate.weight", ".mlp.gate.e_score_correction_bias",
-                          ".self_attn.indexer.wk.weight", ".self_attn.indexer.weights_proj.weight",
-                          ".self_attn.indexer.k_norm.weight", ".self_attn.indexer.k_norm.bias", ".eh_proj.weight",
-                          ".enorm.weight", ".hnorm.weight", ".shared_head.norm.weight"};
-    if (name.compare(0, 19, "model.embed_tokens.") == 0) {
+    if (ends_with(name, ".mlp.gate.weight") || ends_with(name, ".mlp.gate.e_score_correction_bias")) {
         r = REP;
         return EA_OK;
     }
-    for (const char* s : reps)
-        if (ends_with(name, s)) {
-            r = REP;
-            return EA_OK;
-        }
-    return EA_NO_SPLIT_RULE;
+    const size_t dot = name.rfind('.');
+    if (dot == std::string::npos) return EA_NO_SPLIT_RULE;
+    const std::string part = name.substr(dot + 1), stem = name.substr(0, dot);
+    const bool in_block = stem.find(".mlp.experts.") != std::string::npos ||
+                          stem.find(".mlp.shared_experts.") != std::string::npos ||
+                          stem.find(".mlp.gate_proj") != std::string::npos ||
+                          stem.find(".mlp.up_proj") != std::string::npos || stem.find(".mlp.down_proj") != std::string::npos;
+    if (!in_block) return EA_NO_SPLIT_RULE;
+    enum { OUT, IN } role;
+    if (ends_with(stem, "gate_proj") || ends_with(stem, "up_proj")) role = OUT;
+    else if (ends_with(stem, "down_proj")) role = IN;
+    else return EA_NO_SPLIT_RULE;
+    if (part == "mcg" || part == "mul1") r = REP;
+    else if (part == "trellis") r = role == OUT ? DIM1 : ROW;
+    else if (part == "svh") r = role == OUT ? ROW : REP;
+    else if (part == "suh") r = role == IN ? ROW : REP;
+    else return EA_NO_SPLIT_RULE;
+    return EA_OK;
 }
 
 // split.zig:61-73: the cut axis divides evenly and no share straddles a Hadamard block.
@@ -406,6 +381,11 @@ static int cut(const File& f, const Entry& e, Rule r, uint64_t rank, uint64_t wo
     }
     int rc = check_cut(name, r, e, world);
     if (rc) return rc;
+    if (nbytes == 0) {  // a tensor with a zero dimension: an empty share of the cut shape
+        s.shape[r == ROW ? 0 : 1] = e.shape[r == ROW ? 0 : 1] / world;
+        s.bytes.clear();
+        return EA_OK;
+    }
     if (r == ROW) {
         const uint64_t n = e.shape[0] / world, per = nbytes / e.shape[0];
         s.shape[0] = n;
@@ -433,6 +413,12 @@ static int join(const std::vector<std::pair<const File*, const Entry*>>& parts, 
     s.rank = p0.rank;
     std::copy(p0.shape, p0.shape + MAX_RANK, s.shape);
     const uint64_t pb = p0.end - p0.begin, k = parts.size();
+    if (pb == 0 && r != REP) {  // parts with a zero dimension: an empty share of the joined shape
+        if (r == DIM1 && p0.rank < 2) return EA_STORED_SHARES_DIFFER;
+        s.shape[r == ROW ? 0 : 1] = p0.shape[r == ROW ? 0 : 1] * k;
+        s.bytes.clear();
+        return EA_OK;
+    }
     if (r == REP) {
         const uint8_t* src = parts[0].first->data + p0.begin;
         s.bytes.assign(src, src + pb);
@@ -536,7 +522,7 @@ int bank_check_world(uint32_t rank, uint32_t world, uint32_t stored_world) {
 
 extern "C" {
 
-int ea_bank_open(const char* dir, uint32_t rank, uint32_t world, uint32_t stored_world, ea_bank** out) {
+static int ea_bank_open_body(const char* dir, uint32_t rank, uint32_t world, uint32_t stored_world, ea_bank** out) {
     if (!dir || !out) return EA_BAD_ARGUMENT;
     int rc = bank_check_world(rank, world, stored_world);
     if (rc) return rc;
@@ -565,7 +551,7 @@ int ea_bank_open(const char* dir, uint32_t rank, uint32_t world, uint32_t stored
     return EA_OK;
 }
 
-int ea_bank_open_file(const char* dir, const char* fname, uint32_t rank, uint32_t world, uint32_t stored_world,
+static int ea_bank_open_file_body(const char* dir, const char* fname, uint32_t rank, uint32_t world, uint32_t stored_world,
                       ea_bank** out) {
     if (!dir || !fname || !out) return EA_BAD_ARGUMENT;
     int rc = bank_check_world(rank, world, stored_world);
@@ -584,9 +570,15 @@ int ea_bank_open_file(const char* dir, const char* fname, uint32_t rank, uint32_
 
 void ea_bank_close(ea_bank* b) { delete b; }
 
-int ea_bank_has(const ea_bank* b, const char* name) { return b && name && b->has(name) ? 1 : 0; }
+int ea_bank_has(const ea_bank* b, const char* name) {
+    try {
+        return b && name && b->has(name) ? 1 : 0;
+    } catch (...) {  // a failed host allocation: not found
+        return 0;
+    }
+}
 
-int ea_bank_share(ea_bank* b, const char* name, ea_share_info* info, void* dst, uint64_t cap) {
+static int ea_bank_share_body(ea_bank* b, const char* name, ea_share_info* info, void* dst, uint64_t cap) {
     if (!b || !name || !info) return EA_BAD_ARGUMENT;
     Share s;
     const int rc = b->get(name, s);
@@ -670,7 +662,7 @@ int read_expert(ea_bank* r, uint32_t layer, uint32_t e, ExpertRead& rd, bool swa
 
 extern "C" {
 
-int ea_layer_load(ea_bank* const* readers, uint32_t nreaders, const uint8_t* pick, uint32_t layer, uint32_t experts,
+static int ea_layer_load_body(ea_bank* const* readers, uint32_t nreaders, const uint8_t* pick, uint32_t layer, uint32_t experts,
                   ea_layer** out) {
     if (!readers || nreaders == 0 || !out || experts == 0 || experts > 4096) return EA_BAD_ARGUMENT;
     for (uint32_t i = 0; i < nreaders; ++i)
@@ -769,14 +761,17 @@ void ea_layer_free(ea_layer* l) { delete l; }
 // read and checked on the host, the three new slabs allocated, then the device written (the slabs: unchanged experts
 // copied on the device, changed ones uploaded; their scales overwritten; the ptr / k2 tables rewritten in place, where
 // captured graphs hold their addresses) and the old slabs freed. The K2 ranges only widen. Synchronous.
-int ea_layer_swap(ea_layer* l, ea_bank* const* banks, uint32_t layer, const uint8_t* target, const uint8_t* current,
+static int ea_layer_swap_body(ea_layer* l, ea_bank* const* banks, uint32_t layer, const uint8_t* target, const uint8_t* current,
                   ea_swap_stats* st) {
     if (!l || !banks || !target || !current) return EA_BAD_ARGUMENT;
     ea_routed& x = l->r;
     const uint32_t E = x.count;
     for (uint32_t j = 0; j < E; ++j) {
         if (target[j] == current[j]) continue;
-        if (target[j] < 2 || target[j] > 8) return EA_SWAP_WIDTH_UNSUPPORTED;
+        // the widths every kernel of this library decodes (K2 4..10), as the reference refuses widths its kernels do
+        // not take (expert_swap.zig:94-98: 2..4 bits, 5 with its K10 kernels): a captured graph then always replays
+        // on widths its kernels decode
+        if (target[j] < 2 || target[j] > 5) return EA_SWAP_WIDTH_UNSUPPORTED;
         if (!banks[target[j]]) return EA_SWAP_NO_BANK;
     }
     int rc = hipst(hipSetDevice(l->device));
@@ -825,50 +820,94 @@ int ea_layer_swap(ea_layer* l, ea_bank* const* banks, uint32_t layer, const uint
             return rc;
         }
     }
-    // 3. the device
+    // 3. the new slabs filled (unchanged experts copied on the device, changed ones uploaded) and the tables built on
+    // the host; nothing the layer's kernels read is written yet, so a failure here frees the new slabs and leaves the
+    // layer as it was
+    auto free_new = [&]() {
+        for (void* q : nb) (void)hipFree(q);
+    };
     uint64_t read_bytes = 0;
+    std::vector<int64_t> ptrs[3];
+    std::vector<int32_t> k2v[3];
+    uint32_t lo[3] = {99, 99, 99}, hi[3] = {0, 0, 0};
     for (int p = 0; p < 3; ++p) {
-        std::vector<int64_t> ptrs(E);
-        std::vector<int32_t> k2v(E);
-        uint32_t lo = 99, hi = 0;
+        ptrs[p].resize(E);
+        k2v[p].resize(E);
         size_t off = 0;
         for (uint32_t j = 0; j < E; ++j) {
             char* dst = static_cast<char*>(nb[p]) + off;
             if (reads[j]) {
                 const ExpertRead& rd = *reads[j];
                 rc = hipst(hipMemcpy(dst, rd.tr[p].bytes.data(), rd.tr[p].bytes.size(), hipMemcpyHostToDevice));
-                if (!rc) rc = hipst(hipMemcpy(static_cast<char*>(l->scales[2 * p]) + j * l->scale_bytes[2 * p],
-                                              rd.su[p].bytes.data(), rd.su[p].bytes.size(), hipMemcpyHostToDevice));
-                if (!rc) rc = hipst(hipMemcpy(static_cast<char*>(l->scales[2 * p + 1]) + j * l->scale_bytes[2 * p + 1],
-                                              rd.sv[p].bytes.data(), rd.sv[p].bytes.size(), hipMemcpyHostToDevice));
-                k2v[j] = (int32_t)(rd.tr[p].shape[2] / 8);
+                k2v[p][j] = (int32_t)(rd.tr[p].shape[2] / 8);
                 off += align256(rd.tr[p].bytes.size());
                 read_bytes += rd.tr[p].bytes.size() + rd.su[p].bytes.size() + rd.sv[p].bytes.size();
             } else {
                 const size_t n = per_k2 * (size_t)old_k2[p][j];
                 rc = hipst(hipMemcpy(dst, reinterpret_cast<void*>(static_cast<uintptr_t>(old_ptrs[p][j])), n,
                                      hipMemcpyDeviceToDevice));
-                k2v[j] = old_k2[p][j];
+                k2v[p][j] = old_k2[p][j];
                 off += align256(n);
             }
             if (rc) {
-                for (void* q : nb) (void)hipFree(q);
+                free_new();
                 return rc;
             }
-            ptrs[j] = (int64_t)reinterpret_cast<uintptr_t>(dst);
-            lo = std::min(lo, (uint32_t)k2v[j]);
-            hi = std::max(hi, (uint32_t)k2v[j]);
+            ptrs[p][j] = (int64_t)reinterpret_cast<uintptr_t>(dst);
+            lo[p] = std::min(lo[p], (uint32_t)k2v[p][j]);
+            hi[p] = std::max(hi[p], (uint32_t)k2v[p][j]);
         }
-        // the tables in place: the graphs hold their addresses
-        rc = hipst(hipMemcpy(l->tables[p], ptrs.data(), E * 8, hipMemcpyHostToDevice));
-        if (!rc) rc = hipst(hipMemcpy(l->tables[3 + p], k2v.data(), E * 4, hipMemcpyHostToDevice));
+    }
+    // the changed experts' present scales, kept on the host to put back if a write below fails
+    std::vector<std::vector<uint8_t>> old_scales(6);
+    for (int s = 0; s < 6; ++s) {
+        old_scales[s].resize((size_t)E * l->scale_bytes[s]);
+        for (uint32_t j = 0; j < E && !rc; ++j)
+            if (reads[j])
+                rc = hipst(hipMemcpy(old_scales[s].data() + j * l->scale_bytes[s],
+                                     static_cast<char*>(l->scales[s]) + j * l->scale_bytes[s], l->scale_bytes[s],
+                                     hipMemcpyDeviceToHost));
         if (rc) {
-            for (void* q : nb) (void)hipFree(q);
+            free_new();
             return rc;
         }
+    }
+    // 4. the layer written: the changed experts' scales, then the ptr / k2 tables in place (the graphs hold their
+    // addresses). A failed write puts back every scale and table entry written so far before the new slabs go.
+    for (uint32_t j = 0; j < E && !rc; ++j) {
+        if (!reads[j]) continue;
+        for (int p = 0; p < 3 && !rc; ++p) {
+            const ExpertRead& rd = *reads[j];
+            rc = hipst(hipMemcpy(static_cast<char*>(l->scales[2 * p]) + j * l->scale_bytes[2 * p],
+                                 rd.su[p].bytes.data(), rd.su[p].bytes.size(), hipMemcpyHostToDevice));
+            if (!rc)
+                rc = hipst(hipMemcpy(static_cast<char*>(l->scales[2 * p + 1]) + j * l->scale_bytes[2 * p + 1],
+                                     rd.sv[p].bytes.data(), rd.sv[p].bytes.size(), hipMemcpyHostToDevice));
+        }
+    }
+    for (int p = 0; p < 3 && !rc; ++p) {
+        rc = hipst(hipMemcpy(l->tables[p], ptrs[p].data(), E * 8, hipMemcpyHostToDevice));
+        if (!rc) rc = hipst(hipMemcpy(l->tables[3 + p], k2v[p].data(), E * 4, hipMemcpyHostToDevice));
+    }
+    if (rc) {
+        for (int p = 0; p < 3; ++p) {
+            (void)hipMemcpy(l->tables[p], old_ptrs[p].data(), E * 8, hipMemcpyHostToDevice);
+            (void)hipMemcpy(l->tables[3 + p], old_k2[p].data(), E * 4, hipMemcpyHostToDevice);
+        }
+        for (int s = 0; s < 6; ++s)
+            for (uint32_t j = 0; j < E; ++j)
+                if (reads[j])
+                    (void)hipMemcpy(static_cast<char*>(l->scales[s]) + j * l->scale_bytes[s],
+                                    old_scales[s].data() + j * l->scale_bytes[s], l->scale_bytes[s],
+                                    hipMemcpyHostToDevice);
+        (void)hipDeviceSynchronize();
+        free_new();
+        return rc;
+    }
+    for (int p = 0; p < 3; ++p) {
         uint32_t* rg = p == 2 ? x.k2_d : x.k2_gu;
-        rg[0] = std::min(rg[0], lo);
-        rg[1] = std::max(rg[1], hi);
+        rg[0] = std::min(rg[0], lo[p]);
+        rg[1] = std::max(rg[1], hi[p]);
     }
     for (int p = 0; p < 3; ++p) {
         (void)hipFree(l->slab[p]);
@@ -885,6 +924,48 @@ int ea_layer_swap(ea_layer* l, ea_bank* const* banks, uint32_t layer, const uint
         st->read_bytes = read_bytes;
     }
     return EA_OK;
+}
+
+}  // extern "C"
+
+// The entry points above, with every C++ exception turned into a status before it reaches a C caller: a host
+// allocation that fails (std::bad_alloc) is EA_OUT_OF_HOST_MEMORY (Zig's error.OutOfMemory), anything else
+// EA_BANK_IO. Nothing is half-done on either path that the status does not describe: the bodies build their results
+// in local objects and publish them last.
+template <class F>
+static int guarded(F&& f) {
+    try {
+        return f();
+    } catch (const std::bad_alloc&) {
+        return EA_OUT_OF_HOST_MEMORY;
+    } catch (...) {
+        return EA_BANK_IO;
+    }
+}
+
+extern "C" {
+
+int ea_bank_open(const char* dir, uint32_t rank, uint32_t world, uint32_t stored_world, ea_bank** out) {
+    return guarded([&] { return ea_bank_open_body(dir, rank, world, stored_world, out); });
+}
+
+int ea_bank_open_file(const char* dir, const char* fname, uint32_t rank, uint32_t world, uint32_t stored_world,
+                      ea_bank** out) {
+    return guarded([&] { return ea_bank_open_file_body(dir, fname, rank, world, stored_world, out); });
+}
+
+int ea_bank_share(ea_bank* b, const char* name, ea_share_info* info, void* dst, uint64_t cap) {
+    return guarded([&] { return ea_bank_share_body(b, name, info, dst, cap); });
+}
+
+int ea_layer_load(ea_bank* const* readers, uint32_t nreaders, const uint8_t* pick, uint32_t layer, uint32_t experts,
+                  ea_layer** out) {
+    return guarded([&] { return ea_layer_load_body(readers, nreaders, pick, layer, experts, out); });
+}
+
+int ea_layer_swap(ea_layer* l, ea_bank* const* banks, uint32_t layer, const uint8_t* target, const uint8_t* current,
+                  ea_swap_stats* st) {
+    return guarded([&] { return ea_layer_swap_body(l, banks, layer, target, current, st); });
 }
 
 }  // extern "C"

@@ -164,8 +164,9 @@ const char* ea_strerror(int s) {
         case EA_SWAP_CODEBOOK_DIFFERS: return "SwapCodebookDiffers: the bank's codebook differs from the layer's";
         case EA_SWAP_BAD_TRELLIS: return "SwapBadTrellis: the bank's trellis is not of the layer's shape and width";
         case EA_SWAP_BAD_SCALES: return "SwapBadScales: the bank's scales are not of the layer's shape";
-        case EA_SWAP_WIDTH_UNSUPPORTED: return "SwapWidthUnsupported: widths of 2 to 8 bits";
+        case EA_SWAP_WIDTH_UNSUPPORTED: return "SwapWidthUnsupported: the kernels take widths of 2 to 5 bits";
         case EA_SWAP_NO_BANK: return "SwapNoBank: no bank for a width the change asks for";
+        case EA_OUT_OF_HOST_MEMORY: return "a host allocation of the bank reader failed";
         default: return "unknown status";
     }
 }

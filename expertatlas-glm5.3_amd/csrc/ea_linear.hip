@@ -347,12 +347,16 @@ __global__ void __launch_bounds__(1024) lin_small_kernel(ea_jobs jobs, ea_rot_jo
                     acc2.x += __uint_as_float((uint32_t)p[q][0]);
                     acc2.y += __uint_as_float((uint32_t)p[q][1]);
                 }
-            for (int q = 0; q < SK; ++q)
-                if (!(own && q == SK - 1)) {
-                    uint64_t* at = Zt + ((size_t)q * M + m) * N + col;
-                    __hip_atomic_store(at, (uint64_t)0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    __hip_atomic_store(at + 1, (uint64_t)0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                }
+            // the slots read go back to zero for the next call. After a give-up they are left as they are: a writer
+            // that arrives late would tag a slot just cleared, and the next call's finisher would take that stale sum
+            // for its own; the status word says EA_SYNC_TIMEOUT instead, and z must be zeroed again before reuse
+            if (!timed_out)
+                for (int q = 0; q < SK; ++q)
+                    if (!(own && q == SK - 1)) {
+                        uint64_t* at = Zt + ((size_t)q * M + m) * N + col;
+                        __hip_atomic_store(at, (uint64_t)0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        __hip_atomic_store(at + 1, (uint64_t)0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    }
             if (timed_out) acc2 = float2{__builtin_nanf(""), __builtin_nanf("")};  // a writer never arrived
             finish_store_pre(acc2.x, acc2.y, lane, svw, bias != nullptr, bw, dptr<void>(J.y), J.y_dtype,
                              (size_t)m * N + col);
@@ -593,7 +597,7 @@ int ea_exl3_linear(ea_stream_t stream, const ea_jobs* jobs, uint32_t m, uint32_t
     return launch_linear(as_stream(stream), jobs, m, kdim, k2, cb, wk, loads);
 }
 
-// linear.zig:198-214
+// linear.zig:61-79 plan
 void ea_linear_plan(uint32_t k, uint32_t n, uint32_t* sk_out, uint32_t* wk_out) {
     const uint32_t kt = k / 16, nb = n / 128;
     uint32_t sk = 1, wk = nb >= 64 ? 8 : 4;
@@ -608,7 +612,7 @@ void ea_linear_plan(uint32_t k, uint32_t n, uint32_t* sk_out, uint32_t* wk_out) 
     if (wk_out) *wk_out = wk;
 }
 
-// linear.zig:270-275
+// linear.zig:133-138 groupable
 static bool groupable(const ea_linear* const* ls, uint32_t n) {
     if (!ls || n == 0 || n > EA_MAX_JOBS) return false;
     const ea_linear* a = ls[0];
@@ -618,7 +622,7 @@ static bool groupable(const ea_linear* const* ls, uint32_t n) {
     return true;
 }
 
-// the kernels' load options the engine uses: bits 1 and 2 (linear.zig:293-295; PDL has no counterpart here)
+// the kernels' load options the engine uses: bits 1 and 2 (linear.zig:156-158; PDL has no counterpart here)
 static const uint32_t LOADS = 3;
 
 // linear.call / callRotated: jobs over the layers; rot and x given for call (the rotation then happens in the

@@ -14,14 +14,14 @@ F16, BF16, F32 = 0, 1, 2
 
 
 def plan(k: int, n: int) -> tuple[int, int]:
-    """linear.zig:198-214: (K splits, warps) from the shape alone."""
+    """linear.zig:61-79 (plan): (K splits, warps) from the shape alone."""
     sk, wk = U32(), U32()
     lib().ea_linear_plan(k, n, C.byref(sk), C.byref(wk))
     return sk.value, wk.value
 
 
 def strips(T: np.ndarray, K: int, N: int, k2: int) -> np.ndarray:
-    """[K/16, N/16, TW] -> [N/128, K/16, 8, TW] (linear.zig:236-243)."""
+    """[K/16, N/16, TW] -> [N/128, K/16, 8, TW] (linear.zig:99-107)."""
     tw = 4 * k2
     return np.ascontiguousarray(T.reshape(K // 16, N // 128, 8, tw).transpose(1, 0, 2, 3)).reshape(-1)
 
@@ -66,7 +66,7 @@ def _arrays(ls, outs, dtypes):
 
 
 def call(stream: int, s: Scratch, ls, x: int, x_dtype: int, m: int, outs, out_dtypes) -> None:
-    """linear.call (linear.zig:301-311): outs[j] = x @ W_j for 1..3 groupable layers, one rot_in + one linear."""
+    """linear.call (linear.zig:164-178): outs[j] = x @ W_j for 1..3 groupable layers, one rot_in + one linear."""
     arr, o, d = _arrays(ls, outs, out_dtypes)
     check(lib().ea_linear_call(stream, C.byref(s.c), arr, len(ls), x, x_dtype, m, o, d), "linear.call")
 

@@ -39,7 +39,7 @@ typedef enum ea_status {
     EA_BAD_WIDTH = 11,                /* experts.zig:175,197 error.BadWidth */
     EA_SCRATCH_TOO_SMALL = 12,        /* moe.zig:285 error.ScratchTooSmall */
     EA_INVALID = 13,                  /* prompt_experts.zig:147,150 error.Invalid */
-    EA_NOT_GROUPABLE = 14,            /* linear.zig:302,318 error.NotGroupable */
+    EA_NOT_GROUPABLE = 14,            /* linear.zig:165,181 error.NotGroupable */
     EA_HIP_FAILED = 15,               /* driver.zig:38-47 error.CudaFailed */
     EA_OUT_OF_DEVICE_MEMORY = 16,     /* driver.zig error.OutOfDeviceMemory */
     EA_NOT_INITIALIZED = 17,          /* a call before ea_init on this device */
@@ -49,21 +49,22 @@ typedef enum ea_status {
     /* expert banks (weights.zig, split.zig, moe.zig, expert_swap.zig) */
     EA_BANK_IO = 21,                  /* a file could not be opened or mapped (std.fs errors) */
     EA_BAD_SAFETENSORS = 22,          /* core/safetensors.zig error.BadSafetensors / UnsupportedDType / RankTooHigh */
-    EA_BAD_INDEX = 23,                /* weights.zig:49 error.BadIndex */
-    EA_MISSING_TENSOR = 24,           /* weights.zig:187 error.MissingTensor */
-    EA_NO_SPLIT_RULE = 25,            /* split.zig:58 error.NoSplitRule */
+    EA_BAD_INDEX = 23,                /* weights.zig:48 error.BadIndex */
+    EA_MISSING_TENSOR = 24,           /* weights.zig:170-171 error.MissingTensor */
+    EA_NO_SPLIT_RULE = 25,            /* split.zig:59 error.NoSplitRule */
     EA_STRADDLES_HADAMARD = 26,       /* split.zig:69,71 error.StraddlesHadamard (UnevenSplit is EA_UNEVEN_SPLIT) */
-    EA_STORED_WORLD_NOT_MULTIPLE = 27,/* weights.zig:41 error.StoredWorldNotMultiple */
-    EA_TOO_MANY_STORED_RANKS = 28,    /* weights.zig:149,220 error.TooManyStoredRanks */
-    EA_STORED_SHARES_DIFFER = 29,     /* weights.zig:155 error.StoredSharesDiffer */
-    EA_BAD_TRELLIS = 30,              /* moe.zig:110 error.BadTrellis */
-    EA_PACKED_SCALES = 31,            /* moe.zig:92 error.PackedScalesUnsupported */
-    EA_MIXED_CODEBOOKS = 32,          /* moe.zig:146 error.MixedCodebooks */
+    EA_STORED_WORLD_NOT_MULTIPLE = 27,/* weights.zig:41,59 error.StoredWorldNotMultiple */
+    EA_TOO_MANY_STORED_RANKS = 28,    /* weights.zig:142,203 error.TooManyStoredRanks */
+    EA_STORED_SHARES_DIFFER = 29,     /* weights.zig:148,246 error.StoredSharesDiffer */
+    EA_BAD_TRELLIS = 30,              /* moe.zig:109,180 error.BadTrellis */
+    EA_PACKED_SCALES = 31,            /* moe.zig:88,163 error.PackedScalesUnsupported */
+    EA_MIXED_CODEBOOKS = 32,          /* moe.zig:132,212 error.MixedCodebooks */
     EA_SWAP_CODEBOOK_DIFFERS = 33,    /* expert_swap.zig:335,364 error.SwapCodebookDiffers */
-    EA_SWAP_BAD_TRELLIS = 34,         /* expert_swap.zig:383 error.SwapBadTrellis */
-    EA_SWAP_BAD_SCALES = 35,          /* expert_swap.zig:384 error.SwapBadScales */
-    EA_SWAP_WIDTH_UNSUPPORTED = 36,   /* expert_swap.zig:88 error.SwapWidthUnsupported */
-    EA_SWAP_NO_BANK = 37              /* expert_swap.zig:89 error.SwapNoBank */
+    EA_SWAP_BAD_TRELLIS = 34,         /* expert_swap.zig:382 error.SwapBadTrellis */
+    EA_SWAP_BAD_SCALES = 35,          /* expert_swap.zig:383 error.SwapBadScales */
+    EA_SWAP_WIDTH_UNSUPPORTED = 36,   /* expert_swap.zig:98 error.SwapWidthUnsupported */
+    EA_SWAP_NO_BANK = 37,             /* expert_swap.zig:99 error.SwapNoBank */
+    EA_OUT_OF_HOST_MEMORY = 38        /* a host allocation of the bank reader failed (Zig's error.OutOfMemory) */
 } ea_status;
 
 enum { EA_F16 = 0, EA_BF16 = 1, EA_F32 = 2 };
@@ -218,22 +219,23 @@ int ea_exl3_rot_in(ea_stream_t stream, const void* x, int x_dtype, const ea_rot_
 int ea_exl3_linear(ea_stream_t stream, const ea_jobs* jobs, uint32_t m, uint32_t kdim, uint32_t k2, uint32_t cb,
                    uint32_t wk, uint32_t loads);
 
-/* linear.zig:10-30 Linear (words in the strips layout [N/128][K/16][8][TW]). */
+/* linear.zig:10-33 Linear (words in the strips layout [N/128][K/16][8][TW]). */
 typedef struct ea_linear {
     uint64_t words, suh, svh, counters;  /* counters: int32 [8 * N / 128], zero; left zero by the kernel */
     uint32_t k, n, k2, cb, sk, wk;
 } ea_linear;
-/* linear.zig:140-155 Scratch: xh fp16 [M, K] and z fp32 [SK, M, N] a layer. z must not hold the small-row kernel's
+/* linear.zig:142-154 Scratch: xh fp16 [M, K] and z fp32 [SK, M, N] a layer. z must not hold the small-row kernel's
  * tag when first used (zero it once at allocation, as the counters are): calls of up to about 8 rows with an even
  * split count hand their partial sums over in z as tagged 8-byte slots and leave every slot they used zero. Two calls
- * that run at once on one z race, as in the reference. */
+ * that run at once on one z race, as in the reference. A call whose status word then reads EA_SYNC_TIMEOUT (a
+ * split's block never stored its slot) leaves its slots as they are: zero z again before the next call on it. */
 typedef struct ea_linear_scratch {
     uint64_t xh[EA_MAX_JOBS], z[EA_MAX_JOBS];
 } ea_linear_scratch;
 
-/* linear.zig:198-214 */
+/* linear.zig:61-79 plan */
 void ea_linear_plan(uint32_t k, uint32_t n, uint32_t* sk, uint32_t* wk);
-/* linear.zig:301-325: outs[j] = x @ W_j for 1..3 groupable layers, m <= 128 rows (rot_in + one linear launch). */
+/* linear.zig:164-188 call / callRotated: outs[j] = x @ W_j for 1..3 groupable layers, m <= 128 rows (rot_in + one linear launch). */
 int ea_linear_call(ea_stream_t stream, const ea_linear_scratch* s, const ea_linear* const* ls, uint32_t nls,
                    const void* x, int x_dtype, uint32_t m, const uint64_t* outs, const int* out_dtypes);
 int ea_linear_call_rotated(ea_stream_t stream, const ea_linear_scratch* s, const ea_linear* const* ls, uint32_t nls,

@@ -226,7 +226,7 @@ void or_unpack(const uint32_t* T, int K, int N, int k2, int cb, int64_t stride_k
         }
 }
 
-/* linear.zig:236-243: [K/16, N/16, TW] viewed [kt, nt/8, 8, TW] -> [nt/8, kt, 8, TW]. */
+/* linear.zig:99-107 (load): [K/16, N/16, TW] viewed [kt, nt/8, 8, TW] -> [nt/8, kt, 8, TW]. */
 void or_expert_to_strips(const uint32_t* T, int K, int N, int k2, uint32_t* S) {
     const int TW = 4 * k2, KT = K / 16, NT = N / 16;
     for (int b = 0; b < NT / 8; ++b)
@@ -514,7 +514,7 @@ void or_prompt_experts(const void* x, int x_dtype, int x_stride, const int* pick
 /* EXL3 linear                                                                                      */
 /* ------------------------------------------------------------------------------------------------ */
 
-/* linear.zig:198-214 */
+/* linear.zig:61-79 plan */
 void or_linear_plan(int k, int n, int* sk_out, int* wk_out) {
     const int kt = k / 16, nb = n / 128;
     int sk = 1, wk = nb >= 64 ? 8 : 4;

@@ -47,7 +47,7 @@ void or_dequant_expert(const uint32_t* T, int K, int N, int k2, int cb, uint16_t
 /* strided layout: tile (kt, nt) at kt*stride_k + (nt/8)*stride_nb + (nt%8)*TW (exl3_linear.cu:489-503) */
 void or_unpack(const uint32_t* T, int K, int N, int k2, int cb, int64_t stride_k, int64_t stride_nb,
                uint16_t* W);
-/* expert layout -> "strips" [N/128][K/16][8][TW] (linear.zig:236-243) */
+/* expert layout -> "strips" [N/128][K/16][8][TW] (linear.zig:99-107) */
 void or_expert_to_strips(const uint32_t* T, int K, int N, int k2, uint32_t* S);
 
 /* ---- Hadamard (decode.cuh:146-163) ---- */

@@ -46,7 +46,7 @@ def test_status_strings_name_the_reference_errors():
 
 
 @pytest.mark.parametrize("k,n,sk,wk", [
-    # linear.zig:327-341, the reference's own plan() test on GLM-5.3 TP=4 shapes
+    # linear.zig:190-204, the reference's own plan() test on GLM-5.3 TP=4 shapes
     (2048, 4096, 4, 4), (4096, 6144, 4, None), (6144, 2048, 8, None), (6144, 640, 8, None), (512, 6144, 1, None),
     # the TP=8 shared expert of this path: gate/up (6144 -> 256) and down (256 -> 6144)
     (6144, 256, 8, 4), (256, 6144, 1, 4),

@@ -148,3 +148,27 @@ def test_header_json_forms(tmp_path):
     with pytest.raises(EaError) as e:  # no split rule for a name outside the model's
         r.get("abc")
     assert e.value.code == 25  # NoSplitRule
+
+
+def test_zero_size_and_overflowing_shapes(tmp_path):
+    """A legal zero-size tensor is an empty share of the cut shape on every rank (no division by its zero axis); a
+    header whose shape product overflows 64 bits is refused as BadSafetensors, not wrapped around."""
+    d = tmp_path / "z"
+    d.mkdir()
+    name = bank.expert_name(LAYER, 0, "down", "suh")  # down's suh: cut on its rows
+    hdr = json.dumps({name: {"dtype": "F16", "shape": [0], "data_offsets": [0, 0]}}).encode()
+    (d / "z.safetensors").write_bytes(len(hdr).to_bytes(8, "little") + hdr)
+    for rank in (0, 3):
+        got = bank.Reader(str(d), rank, 4, 4, fname="z.safetensors").get(name)
+        assert got.shape == (0,) and got.nbytes == 0
+    tname = bank.expert_name(LAYER, 0, "gate", "trellis")  # gate's trellis: cut on its tile columns
+    hdr = json.dumps({tname: {"dtype": "I16", "shape": [4, 0, 64], "data_offsets": [0, 0]}}).encode()
+    (d / "t.safetensors").write_bytes(len(hdr).to_bytes(8, "little") + hdr)
+    got = bank.Reader(str(d), 1, 2, 2, fname="t.safetensors").get(tname)
+    assert got.shape == (4, 0, 64)
+    big = 1 << 40
+    hdr = json.dumps({name: {"dtype": "F16", "shape": [big, big], "data_offsets": [0, 0]}}).encode()
+    (d / "o.safetensors").write_bytes(len(hdr).to_bytes(8, "little") + hdr)
+    with pytest.raises(EaError) as e:
+        bank.Reader(str(d), 0, 1, 1, fname="o.safetensors")
+    assert e.value.code == 22  # BadSafetensors

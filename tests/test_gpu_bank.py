@@ -133,6 +133,11 @@ def test_load_rank_shard_and_swap_under_graph(ea, tmp_path):
         lay.swap({3: b3}, np.full(E, 2, np.uint8), cur)
     assert e.value.code == 37  # SwapNoBank
     np.testing.assert_array_equal(replay(), first)
+    # so is a width the kernels do not decode (6 bits), even with a bank for it
+    with pytest.raises(EaError) as e:
+        lay.swap({6: b3}, np.full(E, 6, np.uint8), cur)
+    assert e.value.code == 36  # SwapWidthUnsupported
+    np.testing.assert_array_equal(replay(), first)
     del g
     lay.free()
 

@@ -131,7 +131,7 @@ def test_linear_errors(ea):
     sc = linear.Scratch(1, 512, 4096)
     y = device.zeros((1, 128), torch.float32)
     dx = device.upload(x)
-    with pytest.raises(EaError) as e:  # different K: not groupable (linear.zig:270-275)
+    with pytest.raises(EaError) as e:  # different K: not groupable (linear.zig:133-138)
         linear.call(device.stream(), sc, [a, b], dx.data_ptr(), 1, 1, [y.data_ptr()] * 2, [2, 2])
     assert e.value.code == 14
     with pytest.raises(EaError) as e:  # 129 rows
