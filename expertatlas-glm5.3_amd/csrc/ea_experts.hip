@@ -98,14 +98,37 @@ __global__ void __launch_bounds__(GROUP_THREADS) group_kernel(const int* __restr
 // activations are read once and rotated for each of its slots in turn. out[p] = fp16((x[row] * suh[e]) @ H *
 // HAD_SCALE) for each pair p of the row with an expert (exl3_experts.cu:116-134). The butterflies run over value-index
 // bits 0..6 in that order (three inside a lane, four across lanes), as in a one-lane-pair-a-value layout, so each
-// output is the same fp32 sum rounded the same way.
+// output is the same fp32 sum rounded the same way. With `zero`, the matrix-0 blocks also clear the row's values
+// k .. k + 7 of zero [rows, K] (fp32, or fp16 with zero_half): the output that a prefill pass without a pair plane
+// adds its slots into.
 __global__ void __launch_bounds__(256) rot_in_kernel(const void* __restrict__ x, int x_dtype, int x_stride,
                                                      const int* __restrict__ pick, const uint16_t* __restrict__ suh0,
                                                      const uint16_t* __restrict__ suh1, uint16_t* __restrict__ out0,
-                                                     uint16_t* __restrict__ out1, int K, int slots, int E, int vec) {
+                                                     uint16_t* __restrict__ out1, int K, int slots, int E, int vec,
+                                                     void* __restrict__ zero, int zero_half) {
     const int row = blockIdx.x, mat = blockIdx.y, lane = threadIdx.x & 63;
     const int k = blockIdx.z * 2048 + 8 * (int)threadIdx.x;
     if (k >= K) return;  // whole 16-lane groups (K % 128 == 0)
+    if (zero && mat == 0) {
+        const bool al = (reinterpret_cast<uintptr_t>(zero) & 15) == 0;  // uniform; K % 128 == 0 keeps rows aligned
+        if (zero_half) {
+            uint16_t* z = static_cast<uint16_t*>(zero) + (size_t)row * K + k;
+            if (al)
+                *reinterpret_cast<u4v*>(z) = u4v{0u, 0u, 0u, 0u};
+            else
+#pragma unroll
+                for (int j = 0; j < 8; ++j) z[j] = 0;
+        } else {
+            float* z = static_cast<float*>(zero) + (size_t)row * K + k;
+            if (al) {
+                *reinterpret_cast<f4v*>(z) = f4v{0.f, 0.f, 0.f, 0.f};
+                *reinterpret_cast<f4v*>(z + 4) = f4v{0.f, 0.f, 0.f, 0.f};
+            } else {
+#pragma unroll
+                for (int j = 0; j < 8; ++j) z[j] = 0.f;
+            }
+        }
+    }
     const uint16_t* suh = mat ? suh1 : suh0;
     uint16_t* out = mat ? out1 : out0;
     const size_t xr = (size_t)row * x_stride;
@@ -384,7 +407,7 @@ int launch_group(hipStream_t s, const int* pick, int* uids, int* ucount, int* me
 
 int launch_rot_in(hipStream_t s, const void* x, int x_dtype, uint32_t x_stride, const int* pick, const uint16_t* suh0,
                   const uint16_t* suh1, uint16_t* out0, uint16_t* out1, uint32_t rows, uint32_t kdim, uint32_t slots,
-                  uint32_t experts) {
+                  uint32_t experts, void* zero, int zero_half) {
     EA_REQUIRE_CTX(c);
     if (kdim % 128 != 0) return EA_BAD_ROT_IN;
     if (x_dtype < 0 || x_dtype > 2 || !x || !pick) return EA_BAD_ARGUMENT;
@@ -393,7 +416,7 @@ int launch_rot_in(hipStream_t s, const void* x, int x_dtype, uint32_t x_stride, 
     const int vec = (reinterpret_cast<uintptr_t>(x) & 15) == 0 && ((size_t)x_stride * eb) % 16 == 0;
     dim3 grid(rows, 2, (kdim + 2047) / 2048);
     rot_in_kernel<<<grid, 256, 0, s>>>(x, x_dtype, (int)x_stride, pick, suh0, suh1, out0, out1, (int)kdim,
-                                       (int)slots, (int)experts, vec);
+                                       (int)slots, (int)experts, vec, zero, zero_half);
     return launched();
 }
 

@@ -12,7 +12,7 @@ int launch_group(hipStream_t s, const int* pick, int* uids, int* ucount, int* me
                  uint32_t experts, uint32_t maxm);
 int launch_rot_in(hipStream_t s, const void* x, int x_dtype, uint32_t x_stride, const int* pick, const uint16_t* suh0,
                   const uint16_t* suh1, uint16_t* out0, uint16_t* out1, uint32_t rows, uint32_t kdim, uint32_t slots,
-                  uint32_t experts);
+                  uint32_t experts, void* zero = nullptr, int zero_half = 0);
 int launch_grouped(hipStream_t s, const ea_grouped_args& a);
 // With pclass: a pair with pclass[pair] != 0 sums z's split 0 and then zp's planes 1 .. skp - 1 ([skp - 1][2][p][n])
 // instead of z's sk splits; only >= 0 (with pclass) takes just the pairs of that class (0 or 1).

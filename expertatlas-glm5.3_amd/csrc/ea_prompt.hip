@@ -3,9 +3,11 @@
 // (prompt_experts.cu / prompt_experts.zig of the reference give the interface and the item scheme).
 //
 // A pass over <= 4096 rows: route -> per-pair input rotation -> item GEMM gate|up -> gate/up epilogue -> item GEMM
-// down -> down epilogue + slot-ordered combine [-> bf16 rounding]. Every row's arithmetic is independent of which
-// item or M-tile it lands in (MFMA rows do not mix), and the combine adds the slots in order, so the output is the
-// same on every run (the reference's deterministic mode; its atomic mode is not reproduced).
+// down -> [down epilogue + slot-ordered combine] [-> bf16 rounding]. Every row's arithmetic is independent of which
+// item or M-tile it lands in (MFMA rows do not mix). With a pair plane (the reference's deterministic mode 2) the
+// down GEMM writes each pair's row and the combine adds the slots in order, so the output is the same on every run.
+// Without one (modes 0 and 1, the reference's default) the down GEMM's epilogue adds each pair into its row of out
+// with fp32 (or packed fp16) atomics in arrival order; the rotation launch clears out first.
 #include <hip/hip_runtime.h>
 
 #include "ea_device.hpp"
@@ -157,14 +159,115 @@ __global__ void __launch_bounds__(ROUTE_THREADS) route_kernel(const int* __restr
     for (int i = ROUTE_HELD * ROUTE_THREADS + threadIdx.x; i < n; i += ROUTE_THREADS) place(i, pick[i]);
 }
 
+// ---- the down epilogue without a pair plane ---------------------------------------------------------------------
+
+constexpr int ES = 128 + 4;  // LDS row stride of a row tile's epilogue buffer, floats (rows 4 apart on other banks)
+
+// Where the atomic down epilogue adds: out [rows, D] fp32 (fp16 with half), the expert's svh_d row, the item's pairs
+// and routing weights (LDS), and a double buffer of one row tile x 128 columns in LDS.
+struct DnAtomic {
+    void* out;
+    const uint16_t* svh;  // svh_d + e * D
+    const int* pair_sh;   // the item's pairs, -1 past its count
+    const float* wts_sh;  // their routing weights
+    float* ebuf;          // [2][16][ES]
+    int D, slots, half;
+};
+
+// The down items' epilogue without a pair plane (prompt_experts.cu:719-797, modes 0 and 1): for each occupied row
+// tile, the block's four waves hand their 16 rows x 32 columns (two column tiles each, MFMA accumulator layout) to LDS,
+// then thread (row r, lane l16) takes the row's columns l16 + 16 j of the 128-column block cb: the FWHT over the
+// block (column bits 4, 5, 6 inside the thread, bits 0..3 across the row's 16 lanes), the output scale svh_d *
+// HAD_SCALE (sv, loaded by the caller) and the pair's routing weight, then an atomic add into its row of out: fp32, 16
+// lanes a row covering 64 contiguous bytes an instruction; or, with half, packed fp16 pairs once the lanes of a column
+// pair have traded values. The slots of a row meet in out in arrival order, so the sums' bits may differ run to run.
+// The buffer halves alternate (eb), so one barrier a row tile suffices: a half is written again only after the
+// barrier that follows every thread's reads of it.
+template <int MT>
+__device__ __forceinline__ void dn_atomic(const f4v (&acc)[MT][2], int mts, int wave, int lane, int cb,
+                                          const uint32_t (&sv)[4], const DnAtomic& a, int& eb) {
+    const int r = (int)threadIdx.x >> 4, l16 = lane & 15;
+    const float s1 = l16 & 1 ? -1.f : 1.f, s2 = l16 & 2 ? -1.f : 1.f, s4 = l16 & 4 ? -1.f : 1.f,
+                s8 = l16 & 8 ? -1.f : 1.f;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+        if (mt >= mts) break;  // uniform
+        float* E = a.ebuf + eb * 16 * ES;
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) E[(4 * (lane >> 4) + i) * ES + 32 * wave + 16 * j + l16] = acc[mt][j][i];
+        __syncthreads();
+        float v[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = E[r * ES + 16 * j + l16];
+        eb ^= 1;
+#pragma unroll
+        for (int b = 1; b < 8; b <<= 1)
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+                if (!(j & b)) {
+                    const float lo = v[j], hi = v[j | b];
+                    v[j] = lo + hi;
+                    v[j | b] = lo - hi;
+                }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = __builtin_fmaf(s1, v[j], lane_xor<1>(v[j]));
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = __builtin_fmaf(s2, v[j], lane_xor<2>(v[j]));
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = __builtin_fmaf(s4, v[j], lane_xor<4>(v[j]));
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = __builtin_fmaf(s8, v[j], lane_xor<8>(v[j]));
+        const int idx = mt * 16 + r, p = a.pair_sh[idx];
+        const float w = p >= 0 ? a.wts_sh[idx] : 0.f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = v[j] * (h2f((uint16_t)(sv[j >> 1] >> (16 * (j & 1)))) * HAD_SCALE) * w;
+        const size_t ro = (size_t)(p >= 0 ? p / a.slots : 0) * a.D + (size_t)cb * 128;
+        if (!a.half) {
+            if (p >= 0) {
+                float* o = static_cast<float*>(a.out) + ro + l16;
+#pragma unroll
+                for (int j = 0; j < 8; ++j)
+                    __builtin_amdgcn_global_atomic_fadd_f32((__attribute__((address_space(1))) float*)(o + 16 * j),
+                                                            v[j]);
+            }
+        } else {
+            // lane pair (l16, l16 ^ 1) holds columns (16 j + even, 16 j + odd): the even lane adds j = 0..3, the odd
+            // lane j = 4..7, each as one packed pair at the even column (static indices only: both lanes' pairs are
+            // formed and one is chosen)
+            const bool odd = l16 & 1;
+            uint16_t* base = static_cast<uint16_t*>(a.out) + ro + (l16 & ~1);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const float oe = lane_xor<1>(v[q]), oo = lane_xor<1>(v[q + 4]);  // the partner's values
+                const float lo = odd ? oo : v[q], hi = odd ? v[q + 4] : oe;
+                const h2v hv = __builtin_bit_cast(h2v, (uint32_t)f2h(lo) | ((uint32_t)f2h(hi) << 16));
+                if (p >= 0)
+                    __builtin_amdgcn_global_atomic_fadd_v2f16(
+                        (__attribute__((address_space(1))) h2v*)(base + 16 * (odd ? q + 4 : q)), hv);
+            }
+        }
+    }
+}
+
+// svh_d of thread (r, l16)'s eight columns l16 + 16 j of column block cb, two fp16 a word (j even low).
+__device__ __forceinline__ void dn_atomic_scales(const uint16_t* svh, int cb, int lane, uint32_t (&sv)[4]) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+        sv[q] = (uint32_t)svh[cb * 128 + 32 * q + (lane & 15)] | ((uint32_t)svh[cb * 128 + 32 * q + 16 + (lane & 15)] << 16);
+}
+
 // Block (item, n block of NW * NTW tiles, matrix): wave w covers NTW n tiles over the whole K range for all of the
 // item's rows (IPM_WIDE_TILES groups of 16), so each trellis tile is decoded once per item. Z[mat][pair][n] fp32.
-template <int CB, int LO, int HI, int NTW, int NW>
+template <int CB, int LO, int HI, int NTW, int NW, bool ATOM>
 __global__ void __launch_bounds__(NW * 64) item_gemm_kernel(
     const uint16_t* __restrict__ X0, const uint16_t* __restrict__ X1, const int64_t* __restrict__ TP0,
     const int64_t* __restrict__ TP1, const int* __restrict__ K2_0, const int* __restrict__ K2_1,
     const int* __restrict__ sorted, const int* __restrict__ items, const int* __restrict__ item_count,
-    float* __restrict__ Z, int K, int N, int P, int big, int max_items, int* __restrict__ status) {
+    float* __restrict__ Z, int K, int N, int P, int big, int max_items, int* __restrict__ status,
+    const float* __restrict__ wts, const uint16_t* __restrict__ svh_d, void* __restrict__ out, int slots, int half) {
+    static_assert(!ATOM || NTW * NW == 8, "the atomic epilogue takes 128-column blocks of four waves");
     int e, first, cnt;
     if (!item_at(items, item_count, big, max_items, blockIdx.x, e, first, cnt)) return;
     const int mat = blockIdx.z;
@@ -173,10 +276,16 @@ __global__ void __launch_bounds__(NW * 64) item_gemm_kernel(
     const int k2 = mat ? K2_1[e] : K2_0[e];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     __shared__ int pair_sh[IPM_WIDE];
+    constexpr int EWORDS = ATOM ? 2 * 16 * ES : 1;
+    constexpr int WWORDS = ATOM ? IPM_WIDE : 1;
+    __shared__ float ebuf[EWORDS];
+    __shared__ float wts_sh[WWORDS];
     if (threadIdx.x < IPM_WIDE) pair_sh[threadIdx.x] = (int)threadIdx.x < cnt ? sorted[first + threadIdx.x] : -1;
+    if constexpr (ATOM)
+        if (threadIdx.x < IPM_WIDE) wts_sh[threadIdx.x] = (int)threadIdx.x < cnt ? wts[sorted[first + threadIdx.x]] : 0.f;
     __syncthreads();
     const int nt0 = (blockIdx.y * NW + wave) * NTW;
-    if (nt0 * 16 >= N) return;
+    if (!ATOM && nt0 * 16 >= N) return;  // ATOM: N % 128 == 0 (host-checked), every wave in range
     const uint16_t* xrow[IPM_WIDE_TILES];
 #pragma unroll
     for (int m = 0; m < IPM_WIDE_TILES; ++m) {
@@ -199,6 +308,14 @@ __global__ void __launch_bounds__(NW * 64) item_gemm_kernel(
         for (int m = 0; m < IPM_WIDE_TILES; ++m)
 #pragma unroll
             for (int j = 0; j < NTW; ++j) acc[m][j] = nan4();
+    }
+    if constexpr (ATOM) {
+        uint32_t sv[4];
+        dn_atomic_scales(svh_d + (size_t)e * N, (int)blockIdx.y, lane, sv);
+        int eb = 0;
+        const DnAtomic at{out, svh_d + (size_t)e * N, pair_sh, wts_sh, ebuf, N, slots, half};
+        dn_atomic<IPM_WIDE_TILES>(acc, (cnt + 15) >> 4, wave, lane, (int)blockIdx.y, sv, at, eb);
+        return;
     }
     float* Zm = Z + (size_t)mat * P * N;
 #pragma unroll
@@ -611,9 +728,10 @@ item_ring_kernel(const uint16_t* __restrict__ X0, const uint16_t* __restrict__ X
 
 // The column blocks of a down block for one width: step s is column block s / nch, chunk s % nch; the trellis two
 // steps ahead; each column block's rows are stored when its last chunk is done.
-template <int CB, int K2, int MT, int NG>
+template <int CB, int K2, int MT, int NG, bool ATOM>
 __device__ __forceinline__ void dn_loop(const TileSpan& sp, const uint16_t* xa, uint32_t* st, int lane, int wave,
-                                        int mts, int nch, int nb0, const int* pair_sh, float* __restrict__ Z, int N) {
+                                        int mts, int nch, int nb0, const int* pair_sh, float* __restrict__ Z, int N,
+                                        const DnAtomic& at) {
     constexpr int NL = stage_loads_k<PK, K2>();
     constexpr int TWB = 16 * K2;
     const LaneQuad lq = lane_quad_k<K2>(lane);
@@ -621,6 +739,8 @@ __device__ __forceinline__ void dn_loop(const TileSpan& sp, const uint16_t* xa, 
     static_assert(NG % 2 == 0, "two steps an iteration");
     u4v ta[NL], tb[NL];
     f4v acc[MT][2];
+    uint32_t sv[4];  // ATOM: svh_d of this thread's epilogue columns, loaded at a column block's first chunk
+    int eb = 0;
     auto issue_t = [&](int s2, u4v (&tv)[NL]) __attribute__((always_inline)) {
         s2 = s2 < steps ? s2 : steps - 1;
         TileSpan sc = sp;
@@ -632,11 +752,14 @@ __device__ __forceinline__ void dn_loop(const TileSpan& sp, const uint16_t* xa, 
         if (c == 0) {
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt) acc[mt][0] = acc[mt][1] = f4v{0.f, 0.f, 0.f, 0.f};
+            if constexpr (ATOM) dn_atomic_scales(at.svh, nb0 + s2 / nch, lane, sv);
         }
         stage_store_k<PK, K2>(st, lane, tv);  // only this wave reads its region, in order
         issue_t(s2 + 2, tv);
         item_chunk<CB, K2, MT>(st, lq, xa + c * PK * 16, mts, lane, acc, DXS);
-        if (c == nch - 1) {
+        if (c == nch - 1 && ATOM) {
+            if constexpr (ATOM) dn_atomic<MT>(acc, mts, wave, lane, nb0 + s2 / nch, sv, at, eb);
+        } else if (c == nch - 1) {
             const int nt0 = (nb0 + s2 / nch) * 8 + 2 * wave;
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt)
@@ -659,11 +782,13 @@ __device__ __forceinline__ void dn_loop(const TileSpan& sp, const uint16_t* xa, 
 
 // The down matrix (K = I of 128 or 256: one or two chunks): a block (item of list MT > 2, NG column blocks of 128)
 // loads the item's activations for all of K into LDS once, then its waves run the column blocks independently.
-template <int CB, int MT, int NG>
+template <int CB, int MT, int NG, bool ATOM>
 __global__ void __launch_bounds__(PW * 64) __attribute__((amdgpu_waves_per_eu(MT > 2 ? 2 : 4)))
 item_dn_kernel(const uint16_t* __restrict__ X, const int64_t* __restrict__ TP, const int* __restrict__ K2T,
                const int* __restrict__ sorted, const int* __restrict__ items, const int* __restrict__ item_count,
-               float* __restrict__ Z, int K, int N, int P, int max_items, int* __restrict__ status) {
+               float* __restrict__ Z, int K, int N, int P, int max_items, int* __restrict__ status,
+               const float* __restrict__ wts, const uint16_t* __restrict__ svh_d, void* __restrict__ out, int slots,
+               int half) {
     int e, first, cnt;
     // the larger items' blocks in XCD order (a column group's slice of an expert on the same XCDs for all of the
     // expert's items); the small items' (one item an expert) item by item
@@ -680,10 +805,18 @@ item_dn_kernel(const uint16_t* __restrict__ X, const int64_t* __restrict__ TP, c
     __shared__ int pair_sh[MT * 16];
     __shared__ __attribute__((aligned(16))) uint16_t xa[MT * 16 * DXS];
     __shared__ __attribute__((aligned(16))) uint32_t st[PW][PSTAGE];
+    constexpr int EWORDS = ATOM ? 2 * 16 * ES : 1;
+    constexpr int WWORDS = ATOM ? MT * 16 : 1;
+    __shared__ float ebuf[EWORDS];
+    __shared__ float wts_sh[WWORDS];
     if (tid < MT * 16) pair_sh[tid] = tid < cnt ? sorted[first + tid] : -1;
+    if constexpr (ATOM)
+        if (tid < MT * 16) wts_sh[tid] = tid < cnt ? wts[sorted[first + tid]] : 0.f;
     __syncthreads();
     const int mts = (cnt + 15) >> 4;
     const int nch = K / (PK * 16);  // 1 or 2
+    DnAtomic at{};
+    if constexpr (ATOM) at = DnAtomic{out, svh_d + (size_t)e * N, pair_sh, wts_sh, ebuf, N, slots, half};
     {
         const __amdgpu_buffer_rsrc_t xrs = buffer_rsrc(X, (uint32_t)((size_t)P * K * 2));
         u4v av[2][MT];
@@ -711,14 +844,18 @@ item_dn_kernel(const uint16_t* __restrict__ X, const int64_t* __restrict__ TP, c
     sp.off = (nb0 * 8 + 2 * wave) * TWB;
     sp.kstride = ns * TWB;
     __syncthreads();  // the activations are in LDS
-    const bool ok =
-        EA_K2_SWITCH(k2, 2, 10, (dn_loop<CB, K2V, MT, NG>(sp, xa, st[wave], lane, wave, mts, nch, nb0, pair_sh, Z, N)));
+    const bool ok = EA_K2_SWITCH(
+        k2, 2, 10, (dn_loop<CB, K2V, MT, NG, ATOM>(sp, xa, st[wave], lane, wave, mts, nch, nb0, pair_sh, Z, N, at)));
     if (!ok) {  // no product ran: the item's outputs of the block's column blocks are NaN
         if (lane == 0) record_error(status, DEV_UNSUPPORTED_WIDTH);
         for (int g = 0; g < NG; ++g)
             for (int i = 0; i < MT * 16; ++i) {
                 const int p = pair_sh[i];
-                if (p >= 0) Z[(size_t)p * N + (nb0 + g) * 128 + wave * 32 + (lane & 31)] = __builtin_nanf("");
+                if (p < 0) continue;
+                const size_t o = (size_t)(nb0 + g) * 128 + wave * 32 + (lane & 31);
+                if (!ATOM) Z[(size_t)p * N + o] = __builtin_nanf("");
+                else if (!half) static_cast<float*>(out)[(size_t)(p / slots) * N + o] = __builtin_nanf("");
+                else static_cast<uint16_t*>(out)[(size_t)(p / slots) * N + o] = 0x7E00;
             }
     }
 }
@@ -785,14 +922,10 @@ __global__ void __launch_bounds__(256) prompt_combine_kernel(const float* __rest
     *reinterpret_cast<f4v*>(out + (size_t)r * D + k + 4) = f4v{a[4], a[5], a[6], a[7]};
 }
 
-// out fp32 -> bf16 -> fp32 in place (prompt_experts.zig:246), or fp32 -> fp16 into a half output.
+// out fp32 -> bf16 -> fp32 in place (prompt_experts.zig:246).
 __global__ void round_kernel(float* __restrict__ out, size_t n) {
     for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
         out[i] = bf16r(out[i]);
-}
-__global__ void to_half_kernel(const float* __restrict__ in, uint16_t* __restrict__ out, size_t n) {
-    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
-        out[i] = f2h(in[i]);
 }
 
 static size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
@@ -800,10 +933,16 @@ static size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
 struct PromptLayout {
     size_t sorted, items, count, xd, plane, xg, xu, z, zp, pclass, total;
     uint32_t rows, max_items;
+    bool has_plane;
 };
 
-static PromptLayout prompt_layout(const ea_routed* ex, uint32_t rows, uint32_t slots) {
+// Whether a pass without a pair plane covers the layer's shape: the atomic epilogue of the staged down GEMM takes
+// K = I of at most 256 and whole pairs of 128-column blocks (D % 256 == 0). Other shapes keep the plane.
+static bool atomic_down_fits(const ea_routed* ex) { return ex->width <= 2 * PK * 16 && ex->dims % 256 == 0; }
+
+static PromptLayout prompt_layout(const ea_routed* ex, uint32_t rows, uint32_t slots, int planes) {
     PromptLayout l{};
+    l.has_plane = planes || !atomic_down_fits(ex);
     const uint32_t r = rows < CHUNK_ROWS ? rows : CHUNK_ROWS;
     const size_t n = (size_t)r * slots, D = ex->dims, I = ex->width;
     l.rows = r;
@@ -818,7 +957,7 @@ static PromptLayout prompt_layout(const ea_routed* ex, uint32_t rows, uint32_t s
     l.items = take(3 * (size_t)l.max_items * 4);
     l.count = take(16);
     l.xd = take(n * I * 2);
-    l.plane = take(n * D * 4);   // per-pair down outputs (the reference's pair plane)
+    l.plane = l.has_plane ? take(n * D * 4) : 0;  // per-pair down outputs (the reference's pair plane)
     l.xg = take(n * D * 2);
     l.xu = take(n * D * 2);
     l.z = take(2 * n * I * 4);
@@ -828,15 +967,30 @@ static PromptLayout prompt_layout(const ea_routed* ex, uint32_t rows, uint32_t s
     return l;
 }
 
+// The atomic epilogue's arguments for a down launch (out null: the pair plane Z instead).
+struct DownOut {
+    const float* wts = nullptr;
+    const uint16_t* svh_d = nullptr;
+    void* out = nullptr;
+    int slots = 0, half = 0;
+};
+
 template <int CB, int LO, int HI>
 static void item_gemm(hipStream_t s, const uint16_t* X0, const uint16_t* X1, const int64_t* TP0, const int64_t* TP1,
                       const int* B0, const int* B1, const int* sorted, const int* items, const int* count, float* Z,
-                      int K, int N, int P, int mats, uint32_t max_items, int* status) {
+                      int K, int N, int P, int mats, uint32_t max_items, int* status, const DownOut& d = DownOut{}) {
     constexpr int NTW = 2, NW = 4;
     dim3 grid(max_items, (N / 16 + NTW * NW - 1) / (NTW * NW), mats);
-    for (int big = 1; big >= 0; --big)
-        item_gemm_kernel<CB, LO, HI, NTW, NW><<<grid, NW * 64, 0, s>>>(X0, X1, TP0, TP1, B0, B1, sorted, items, count,
-                                                                       Z, K, N, P, big, (int)max_items, status);
+    for (int big = 1; big >= 0; --big) {
+        if (d.out)
+            item_gemm_kernel<CB, LO, HI, NTW, NW, true><<<grid, NW * 64, 0, s>>>(
+                X0, X1, TP0, TP1, B0, B1, sorted, items, count, Z, K, N, P, big, (int)max_items, status, d.wts,
+                d.svh_d, d.out, d.slots, d.half);
+        else
+            item_gemm_kernel<CB, LO, HI, NTW, NW, false><<<grid, NW * 64, 0, s>>>(
+                X0, X1, TP0, TP1, B0, B1, sorted, items, count, Z, K, N, P, big, (int)max_items, status, nullptr,
+                nullptr, nullptr, 0, 0);
+    }
 }
 
 // What one item list's pass reads and writes: the rotated activations, the three matrices' trellis tables and
@@ -852,6 +1006,7 @@ struct ListPass {
     uint16_t* xd;
     int D, I, P, rows, slots, E, mi;
     int* status;
+    DownOut down;  // out set: no pair plane, the down items add into out (fp32, or fp16 with half)
 };
 
 // One item list from its gate|up product to its down product, in order on q: big = 1 takes the larger items (the
@@ -877,16 +1032,38 @@ static int list_pass(hipStream_t q, const ListPass& a, int big) {
                                (uint32_t)a.I, 1, (uint32_t)a.slots, (uint32_t)a.E, __builtin_inff(), 1, a.pclass, a.zp,
                                (uint32_t)ns, big);
     if (r) return r;
-    if (a.I <= 2 * PK * 16 && (a.D / 128) % DNG == 0) {
-        if (big && a.rows > LONG_ROWS && (a.D / 128) % DNG_BIG_LONG == 0)
-            item_dn_kernel<CB, IPM_TILES, DNG_BIG_LONG><<<xcd_blocks(a.mi, 1, a.D / 128 / DNG_BIG_LONG), PW * 64, 0, q>>>(
-                a.xd, a.tp[2], a.k2[2], a.sorted, a.items, a.count, a.plane, a.I, a.D, a.P, a.mi, a.status);
+    if (a.down.out) {  // no pair plane: the atomic epilogue (atomic_down_fits holds)
+        const DownOut& d = a.down;
+        const int nb = a.D / 128;
+        if (big && a.rows > LONG_ROWS && nb % DNG_BIG_LONG == 0)
+            item_dn_kernel<CB, IPM_TILES, DNG_BIG_LONG, true><<<xcd_blocks(a.mi, 1, nb / DNG_BIG_LONG), PW * 64, 0, q>>>(
+                a.xd, a.tp[2], a.k2[2], a.sorted, a.items, a.count, nullptr, a.I, a.D, a.P, a.mi, a.status, d.wts,
+                d.svh_d, d.out, d.slots, d.half);
         else if (big)
-            item_dn_kernel<CB, IPM_TILES, DNG_BIG><<<xcd_blocks(a.mi, 1, a.D / 128 / DNG_BIG), PW * 64, 0, q>>>(
-                a.xd, a.tp[2], a.k2[2], a.sorted, a.items, a.count, a.plane, a.I, a.D, a.P, a.mi, a.status);
+            item_dn_kernel<CB, IPM_TILES, DNG_BIG, true><<<xcd_blocks(a.mi, 1, nb / DNG_BIG), PW * 64, 0, q>>>(
+                a.xd, a.tp[2], a.k2[2], a.sorted, a.items, a.count, nullptr, a.I, a.D, a.P, a.mi, a.status, d.wts,
+                d.svh_d, d.out, d.slots, d.half);
+        else if (nb % DNG == 0)
+            item_dn_kernel<CB, SMALL_ROWS / 16, DNG, true><<<dim3(a.mi, nb / DNG, 1), PW * 64, 0, q>>>(
+                a.xd, a.tp[2], a.k2[2], a.sorted, a.items, a.count, nullptr, a.I, a.D, a.P, a.mi, a.status, d.wts,
+                d.svh_d, d.out, d.slots, d.half);
         else
-            item_dn_kernel<CB, SMALL_ROWS / 16, DNG><<<dim3(a.mi, a.D / 128 / DNG, 1), PW * 64, 0, q>>>(
-                a.xd, a.tp[2], a.k2[2], a.sorted, a.items, a.count, a.plane, a.I, a.D, a.P, a.mi, a.status);
+            item_dn_kernel<CB, SMALL_ROWS / 16, 2, true><<<dim3(a.mi, nb / 2, 1), PW * 64, 0, q>>>(
+                a.xd, a.tp[2], a.k2[2], a.sorted, a.items, a.count, nullptr, a.I, a.D, a.P, a.mi, a.status, d.wts,
+                d.svh_d, d.out, d.slots, d.half);
+    } else if (a.I <= 2 * PK * 16 && (a.D / 128) % DNG == 0) {
+        if (big && a.rows > LONG_ROWS && (a.D / 128) % DNG_BIG_LONG == 0)
+            item_dn_kernel<CB, IPM_TILES, DNG_BIG_LONG, false><<<xcd_blocks(a.mi, 1, a.D / 128 / DNG_BIG_LONG), PW * 64, 0, q>>>(
+                a.xd, a.tp[2], a.k2[2], a.sorted, a.items, a.count, a.plane, a.I, a.D, a.P, a.mi, a.status, nullptr,
+                nullptr, nullptr, 0, 0);
+        else if (big)
+            item_dn_kernel<CB, IPM_TILES, DNG_BIG, false><<<xcd_blocks(a.mi, 1, a.D / 128 / DNG_BIG), PW * 64, 0, q>>>(
+                a.xd, a.tp[2], a.k2[2], a.sorted, a.items, a.count, a.plane, a.I, a.D, a.P, a.mi, a.status, nullptr,
+                nullptr, nullptr, 0, 0);
+        else
+            item_dn_kernel<CB, SMALL_ROWS / 16, DNG, false><<<dim3(a.mi, a.D / 128 / DNG, 1), PW * 64, 0, q>>>(
+                a.xd, a.tp[2], a.k2[2], a.sorted, a.items, a.count, a.plane, a.I, a.D, a.P, a.mi, a.status, nullptr,
+                nullptr, nullptr, 0, 0);
     } else if (big) {
         item_gu_kernel<CB><<<xcd_blocks(a.mi, a.D / (16 * 2 * PW), 1), PW * 64, 0, q>>>(
             a.xd, a.xd, a.tp[2], a.tp[2], a.k2[2], a.k2[2], a.sorted, a.items, a.count, a.plane, nullptr, a.I, a.D,
@@ -923,13 +1100,14 @@ static int list_passes(hipStream_t s, uint32_t cb, const ListPass& a) {
 // Widths above 10 (three trellis words a lane): the register-streaming GEMM, both lists in turn on s.
 static void wide_gemm(hipStream_t s, uint32_t cb, const uint16_t* X0, const uint16_t* X1, const int64_t* TP0,
                       const int64_t* TP1, const int* B0, const int* B1, const int* sorted, const int* items,
-                      const int* count, float* Z, int K, int N, int P, int mats, uint32_t max_items, int* status) {
+                      const int* count, float* Z, int K, int N, int P, int mats, uint32_t max_items, int* status,
+                      const DownOut& d = DownOut{}) {
     if (cb == 1) {
-        item_gemm<1, 2, 16>(s, X0, X1, TP0, TP1, B0, B1, sorted, items, count, Z, K, N, P, mats, max_items, status);
+        item_gemm<1, 2, 16>(s, X0, X1, TP0, TP1, B0, B1, sorted, items, count, Z, K, N, P, mats, max_items, status, d);
     } else if (cb == 2) {
-        item_gemm<2, 2, 16>(s, X0, X1, TP0, TP1, B0, B1, sorted, items, count, Z, K, N, P, mats, max_items, status);
+        item_gemm<2, 2, 16>(s, X0, X1, TP0, TP1, B0, B1, sorted, items, count, Z, K, N, P, mats, max_items, status, d);
     } else {
-        item_gemm<0, 2, 16>(s, X0, X1, TP0, TP1, B0, B1, sorted, items, count, Z, K, N, P, mats, max_items, status);
+        item_gemm<0, 2, 16>(s, X0, X1, TP0, TP1, B0, B1, sorted, items, count, Z, K, N, P, mats, max_items, status, d);
     }
 }
 
@@ -958,25 +1136,23 @@ int ea_prompt_experts_supported(const ea_routed* ex, int* ok) {
 }
 
 size_t ea_prompt_scratch_bytes(const ea_routed* ex, uint32_t rows, uint32_t slots, int planes) {
-    (void)planes;
     if (!ex || rows == 0 || slots == 0) return 0;
-    return prompt_layout(ex, rows, slots).total;
+    return prompt_layout(ex, rows, slots, planes).total;
 }
 
 int ea_prompt_scratch_init(ea_stream_t stream, ea_prompt_scratch* s, void* base, size_t bytes, const ea_routed* ex,
                            uint32_t rows, uint32_t slots, int planes) {
-    (void)planes;  // the pair plane is always there: the slots are always added in order
     EA_REQUIRE_CTX(c);
     if (!s || !base || !ex || rows == 0 || slots == 0 || slots > 32) return EA_BAD_ARGUMENT;
     if (reinterpret_cast<uintptr_t>(base) & 255) return EA_BAD_ARGUMENT;
-    const PromptLayout l = prompt_layout(ex, rows, slots);
+    const PromptLayout l = prompt_layout(ex, rows, slots, planes);
     if (bytes < l.total) return EA_SCRATCH_TOO_SMALL;
     const uint64_t b = reinterpret_cast<uintptr_t>(base);
     s->sorted = b + l.sorted;
     s->items = b + l.items;
     s->count = b + l.count;
     s->xd = b + l.xd;
-    s->plane = b + l.plane;
+    s->plane = l.has_plane ? b + l.plane : 0;
     s->xg = b + l.xg;
     s->xu = b + l.xu;
     s->z = b + l.z;
@@ -994,12 +1170,18 @@ int ea_prompt_experts_run(ea_stream_t stream, const void* x, int x_dtype, uint32
                           int do_round, int half_sums) {
     EA_REQUIRE_CTX(c);
     if (half_sums && do_round) return EA_INVALID;  // prompt_experts.zig:147
+    if (half_sums && sc && sc->plane) return EA_INVALID;  // prompt_experts.zig:155: the pair plane takes fp32 rows only
     if (!x || !pick || !wts || !ex || !sc || !out) return EA_BAD_ARGUMENT;
     if (x_dtype < 0 || x_dtype > 2 || sc->slots == 0) return EA_BAD_ARGUMENT;
     if (ex->width % 128 || ex->dims % 128) return EA_BAD_WIDTH;
+    // no pair plane: the down items add each slot into out with atomics (packed fp16 pairs with half_sums), which a
+    // scratch made for this layer's shape allows (atomic_down_fits) and which needs out 4-byte aligned
+    const bool atom = sc->plane == 0;
+    if (atom && (!atomic_down_fits(ex) || (reinterpret_cast<uintptr_t>(out) & 3))) return EA_BAD_ARGUMENT;
     hipStream_t s = as_stream(stream);
     const uint32_t D = ex->dims, I = ex->width, E = ex->count, S = sc->slots;
     const size_t xb = x_dtype == 2 ? 4 : 2;
+    const size_t ob = half_sums ? 2 : 4;
     const bool wide = ex->k2_gu[1] > 10 || ex->k2_d[1] > 10;
     for (uint32_t r0 = 0; r0 < R; r0 += sc->rows) {
         const uint32_t n = R - r0 < sc->rows ? R - r0 : sc->rows;
@@ -1015,9 +1197,20 @@ int ea_prompt_experts_run(ea_stream_t stream, const void* x, int x_dtype, uint32
                                                                   dptr<int>(sc->pclass), (int)max_items, ipm);
         int r = launched();
         if (r) return r;
+        // without a plane the pass's rows of out are cleared by the rotation launch, before any down item adds
+        char* opass = static_cast<char*>(out) + (size_t)r0 * D * ob;
         r = launch_rot_in(s, xs, x_dtype, xstride, pk, dptr<const uint16_t>(ex->suh_g), dptr<const uint16_t>(ex->suh_u),
-                          dptr<uint16_t>(sc->xg), dptr<uint16_t>(sc->xu), n, D, S, E);
+                          dptr<uint16_t>(sc->xg), dptr<uint16_t>(sc->xu), n, D, S, E, atom ? opass : nullptr,
+                          half_sums);
         if (r) return r;
+        DownOut down;
+        if (atom) {
+            down.wts = wt;
+            down.svh_d = dptr<const uint16_t>(ex->svh_d);
+            down.out = opass;
+            down.slots = (int)S;
+            down.half = half_sums;
+        }
         if (!wide) {
             ListPass a{};
             a.xg = dptr<const uint16_t>(sc->xg);
@@ -1046,6 +1239,7 @@ int ea_prompt_experts_run(ea_stream_t stream, const void* x, int x_dtype, uint32
             a.E = (int)E;
             a.mi = (int)max_items;
             a.status = c->status;
+            a.down = down;
             r = list_passes(s, ex->cb, a);
         } else {
             wide_gemm(s, ex->cb, dptr<const uint16_t>(sc->xg), dptr<const uint16_t>(sc->xu),
@@ -1063,13 +1257,21 @@ int ea_prompt_experts_run(ea_stream_t stream, const void* x, int x_dtype, uint32
                       dptr<const int64_t>(ex->ptr[2]), dptr<const int64_t>(ex->ptr[2]), dptr<const int>(ex->k2[2]),
                       dptr<const int>(ex->k2[2]), dptr<const int>(sc->sorted), dptr<const int>(sc->items),
                       dptr<const int>(sc->count), dptr<float>(sc->plane), (int)I, (int)D, (int)pairs, 1, max_items,
-                      c->status);
+                      c->status, down);
             r = launched();
         }
         if (r) return r;
-        // slots without an expert add nothing (the reference's route skips them); fp16 sums go through an fp32
-        // staging buffer (xg, free by now)
-        float* o32 = half_sums ? dptr<float>(sc->xg) : static_cast<float*>(out) + (size_t)r0 * D;
+        if (atom) {  // every slot is in out already
+            if (do_round) {
+                round_kernel<<<1024, 256, 0, s>>>(reinterpret_cast<float*>(opass), (size_t)n * D);
+                r = launched();
+                if (r) return r;
+            }
+            continue;
+        }
+        // the pair plane summed in slot order (fp32 rows only: half sums were refused above); slots without an
+        // expert add nothing (the reference's route skips them)
+        float* o32 = reinterpret_cast<float*>(opass);
         if ((reinterpret_cast<uintptr_t>(o32) & 15) == 0) {  // 16-byte stores
             prompt_combine_kernel<<<dim3(n, (D + 2047) / 2048), 256, 0, s>>>(dptr<const float>(sc->plane), pk,
                                                                              dptr<const uint16_t>(ex->svh_d), wt, o32,
@@ -1080,12 +1282,8 @@ int ea_prompt_experts_run(ea_stream_t stream, const void* x, int x_dtype, uint32
                                     dptr<float>(sc->plane), wt, o32, n, pairs, D, 1, S, E, true);
         }
         if (r) return r;
-        const size_t cnt = (size_t)n * D;
-        if (half_sums) {
-            to_half_kernel<<<1024, 256, 0, s>>>(o32, static_cast<uint16_t*>(out) + (size_t)r0 * D, cnt);
-            r = launched();
-        } else if (do_round) {
-            round_kernel<<<1024, 256, 0, s>>>(o32, cnt);
+        if (do_round) {
+            round_kernel<<<1024, 256, 0, s>>>(o32, (size_t)n * D);
             r = launched();
         }
         if (r) return r;

@@ -180,12 +180,19 @@ typedef struct ea_prompt_scratch {
 
 /* Whether the prefill kernels cover `ex` (prompt_experts.zig:46-61); reads the width tables (synchronous). */
 int ea_prompt_experts_supported(const ea_routed* ex, int* ok);
+/* prompt_experts.zig:105-122 Scratch.planeBytes / init. planes 0 (the reference's default): no pair plane, the down
+ * items add the slots into out with atomics in arrival order (modes 0 and 1); planes 1: the fp32 pair plane [min(rows,
+ * 4096) * slots, D] and a slot-ordered combine, the same bits every run (mode 2). A shard the atomic down epilogue does
+ * not take (I above 256, or D % 256 != 0) keeps the plane whatever planes says; the byte count follows. */
 size_t ea_prompt_scratch_bytes(const ea_routed* ex, uint32_t rows, uint32_t slots, int planes);
 int ea_prompt_scratch_init(ea_stream_t stream, ea_prompt_scratch* s, void* base, size_t bytes, const ea_routed* ex,
                            uint32_t rows, uint32_t slots, int planes);
 
 /* out [R, D] fp32 (fp16 with half_sums) = sum over slots of wts * expert(x), rounded through bf16 when do_round.
- * Replaces prompt_experts.run (prompt_experts.zig:146-248). The two item lists run side by side: the call forks one
+ * Replaces prompt_experts.run (prompt_experts.zig:146-248). Without a pair plane (s->plane 0) the pass clears its rows
+ * of out and its down items add each slot with fp32 atomics (half_sums: packed fp16 atomics; out 4-byte aligned);
+ * half_sums with a plane is EA_INVALID (prompt_experts.zig:155), as is half_sums with do_round (:147). The two item
+ * lists run side by side: the call forks one
  * per-device side stream off `stream` with events and joins it back before returning, so the call stays capturable;
  * calls on one device therefore must not run or be captured concurrently from several host threads (the side stream
  * and its events are shared; a mutex orders the forks, not the streams' work). */

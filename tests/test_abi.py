@@ -60,3 +60,19 @@ def test_linear_plan_matches_reference(k, n, sk, wk):
     if wk is not None:
         assert got[1] == wk
     assert orc.linear_plan(k, n) == got
+
+
+@pytest.mark.parametrize("rows", [512, 2048, 4096, 6000])
+def test_prompt_scratch_sized_by_planes(rows):
+    """ea_prompt_scratch_bytes honours `planes` (prompt_experts.zig:105-122): planes 1 holds the pair plane, fp32
+    [min(rows, 4096) * slots, D], planes 0 does not; a shard the atomic down epilogue does not take (I above 256)
+    keeps the plane either way. Host-only arithmetic, no device memory touched."""
+    L = _lib.lib()
+    r = _lib.Routed()
+    r.count, r.dims, r.width, r.cb = 256, 6144, 256, 1
+    with_plane = L.ea_prompt_scratch_bytes(C.byref(r), rows, 8, 1)
+    without = L.ea_prompt_scratch_bytes(C.byref(r), rows, 8, 0)
+    n = min(rows, 4096) * 8
+    assert with_plane - without == n * 6144 * 4
+    r.width = 512
+    assert L.ea_prompt_scratch_bytes(C.byref(r), rows, 8, 0) == L.ea_prompt_scratch_bytes(C.byref(r), rows, 8, 1)

@@ -141,7 +141,7 @@ def test_linear_errors(ea):
 
 # ---- prefill -------------------------------------------------------------------------------------------------------
 
-def _prompt_case(ea, R, E, D, I, k2, seed, x_dtype=1, zipf=True, cb=1):
+def _prompt_case(ea, R, E, D, I, k2, seed, x_dtype=1, zipf=True, cb=1, planes=True):
     device, _, moe, pe, synth = ea
     slots = 8
     pick = synth.picks_zipf(seed, R, 1.1, E, slots) if zipf else synth.picks_uniform(seed, R, E, slots)
@@ -150,7 +150,7 @@ def _prompt_case(ea, R, E, D, I, k2, seed, x_dtype=1, zipf=True, cb=1):
     x = synth.activations(seed + 3, R, D, ["f16", "bf16", "f32"][x_dtype])
     ex = moe.Routed(host)
     assert pe.supported(ex)
-    sc = pe.Scratch(ex, R, slots)
+    sc = pe.Scratch(ex, R, slots, planes=planes)
     dx, dp, dw = device.upload(x), device.upload(pick), device.upload(wts)
     return host, ex, sc, x, pick, wts, dx, dp, dw
 
@@ -183,11 +183,13 @@ def test_prompt_experts_run(ea, R, E, D, I, k2):
     assert device.device_status() == 0
 
 
-def test_prompt_experts_full_shape_512(ea):
-    """BASELINE config 4 at its real shape: 512 rows, D 6144, I 256, 256 experts, Zipf(1.1), 4 bits, fp16 x."""
+@pytest.mark.parametrize("planes", [True, False])
+def test_prompt_experts_full_shape_512(ea, planes):
+    """BASELINE config 4 at its real shape: 512 rows, D 6144, I 256, 256 experts, Zipf(1.1), 4 bits, fp16 x; with the
+    pair plane and without it."""
     device, _, _, pe, synth = ea
     R, D = 512, 6144
-    host, ex, sc, x, pick, wts, dx, dp, dw = _prompt_case(ea, R, 256, D, 256, 8, 200, x_dtype=0)
+    host, ex, sc, x, pick, wts, dx, dp, dw = _prompt_case(ea, R, 256, D, 256, 8, 200, x_dtype=0, planes=planes)
     want = orc.prompt_experts(x, pick, wts, oracle_routed(host), R, 8)
     out = device.zeros((R, D), torch.float32)
     pe.run(device.stream(), dx.data_ptr(), D, dp.data_ptr(), dw.data_ptr(), ex, sc, out.data_ptr(), R,
@@ -224,22 +226,70 @@ def test_prompt_unaligned_output_same_bits(ea):
 
 
 def test_prompt_half_sums_and_invalid(ea):
+    """half_sums is the reference's mode 1: no pair plane, each slot added into the fp16 out as packed fp16 atomics
+    (prompt_experts.zig:150-155, prompt_experts.cu:785-797). Refused with rounding (prompt_experts.zig:147) and with a
+    pair plane (:155). fp16 sums of 8 slots: each slot's value is rounded to fp16 and every add rounds, so the bar is
+    1e-2 * RMS here (2e-3 for the fp32 modes)."""
     device, _, _, pe, synth = ea
     from ea_exl3._lib import EaError
 
     R, D = 20, 256
-    host, ex, sc, x, pick, wts, dx, dp, dw = _prompt_case(ea, R, 16, D, 128, 8, 300)
+    host, ex, sc, x, pick, wts, dx, dp, dw = _prompt_case(ea, R, 16, D, 128, 8, 300, planes=False)
     out = device.zeros((R, D), torch.float32)
     with pytest.raises(EaError) as e:  # prompt_experts.zig:147: half sums and rounding together
         pe.run(device.stream(), dx.data_ptr(), D, dp.data_ptr(), dw.data_ptr(), ex, sc, out.data_ptr(), R,
                do_round=True, half_sums=True)
     assert e.value.code == 13
+    sc_plane = pe.Scratch(ex, R, 8, planes=True)
+    with pytest.raises(EaError) as e:  # prompt_experts.zig:155: the pair plane takes fp32 rows only
+        pe.run(device.stream(), dx.data_ptr(), D, dp.data_ptr(), dw.data_ptr(), ex, sc_plane, out.data_ptr(), R,
+               do_round=False, half_sums=True)
+    assert e.value.code == 13
     pick2 = pick.copy()
     pick2[0, 3] = -1  # a slot that is not an expert adds nothing
     want = orc.prompt_experts(x, pick2, wts, oracle_routed(host), R, 8, bf16=True)
     h = device.zeros((R, D), torch.float16)
+    h.fill_(7.0)  # the pass clears its rows of out before the slots are added
     dp2 = device.upload(pick2)
     pe.run(device.stream(), dx.data_ptr(), D, dp2.data_ptr(), dw.data_ptr(), ex, sc, h.data_ptr(), R,
            do_round=False, half_sums=True)
     got = device.download(h).view(np.float16).astype(np.float32)
-    assert_close_rms(got, want, 2e-3, "half sums")
+    assert_close_rms(got, want, 1e-2, "half sums (fp16 atomics)")
+    assert device.device_status() == 0
+
+
+@pytest.mark.parametrize("R,E,D,I,k2", [(130, 64, 512, 256, 8), (300, 256, 1024, 256, "mixed"), (40, 32, 256, 128, 6),
+                                        (300, 32, 256, 128, 12), (260, 32, 512, 256, "wide-mixed")])
+def test_prompt_experts_no_plane(ea, R, E, D, I, k2):
+    """planes = 0, the reference's default mode 0: no pair plane and no combine; the down items add each pair's slot
+    into out with fp32 atomics in arrival order (bits may differ run to run). Both item lists, the staged and the
+    register-streaming (widths above 10) down GEMMs; out starts dirty and is cleared by the pass; do_round rounds the
+    sums through bf16. Every run meets the oracle's bar and the planes-1 output's."""
+    device, _, _, pe, synth = ea
+    if k2 == "wide-mixed":
+        k2v = np.array([(12, 8, 6, 16, 10, 11, 4, 14)[e % 8] for e in range(E)], np.int32)
+    else:
+        k2v = synth.mixed_widths(5, E) if k2 == "mixed" else k2
+    host, ex, sc, x, pick, wts, dx, dp, dw = _prompt_case(ea, R, E, D, I, k2v, 700 + R, planes=False)
+    assert sc.c.plane == 0
+    want = orc.prompt_experts(x, pick, wts, oracle_routed(host), R, 8, bf16=True)
+    sc_plane = pe.Scratch(ex, R, 8, planes=True)
+    ref = device.zeros((R, D), torch.float32)
+    pe.run(device.stream(), dx.data_ptr(), D, dp.data_ptr(), dw.data_ptr(), ex, sc_plane, ref.data_ptr(), R,
+           do_round=False)
+    for rep in range(2):
+        out = device.zeros((R, D), torch.float32)
+        out.fill_(float("nan") if rep else 3.0)
+        pe.run(device.stream(), dx.data_ptr(), D, dp.data_ptr(), dw.data_ptr(), ex, sc, out.data_ptr(), R,
+               do_round=False)
+        got = device.download(out)
+        assert_close_rms(got, want, 2e-3, f"prompt experts, no plane, run {rep}")
+        assert_close_rms(got, device.download(ref), 2e-3, f"no plane against the plane, run {rep}")
+    pe.run(device.stream(), dx.data_ptr(), D, dp.data_ptr(), dw.data_ptr(), ex, sc, out.data_ptr(), R, do_round=True)
+    r = device.download(out)
+    np.testing.assert_array_equal(r, synth.bf16_to_f32(synth.bf16_bits(r)))  # every value a bf16
+    # within the fp32 bar plus bf16's half ulp (2^-9 relative) of each value
+    w64 = want.astype(np.float64)
+    bound = 2e-3 * np.sqrt(np.mean(w64 ** 2)) + np.abs(w64) * 2.0 ** -8
+    assert np.all(np.abs(r.astype(np.float64) - w64) <= bound), "no plane, rounded through bf16"
+    assert device.device_status() == 0
