@@ -60,8 +60,8 @@ def parse():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--config", default="decode",
-                    choices=["decode", "multi", "stack", "linear", "prefill512", "prefill2048", "prefill512_planes0",
-                             "prefill2048_planes0"])
+                    choices=["decode", "multi", "stack", "window64", "window128", "linear", "prefill512",
+                             "prefill2048", "prefill512_planes0", "prefill2048_planes0"])
     ap.add_argument("--legs", default=",".join(EXTRA_LEGS_DEFAULT),
                     help="decode: the further workloads timed into the same line, each as an object of its own")
     ap.add_argument("--no-extra", "--no-prefill", dest="no_extra", action="store_true",
@@ -155,6 +155,9 @@ class DecodeBench:
         if self.path != "fused":
             self.sequence(j)
             return
+        if self.R > 16:  # a window the decode layer does not take: ops.topk, moe.routed, the shared expert, add
+            self.window(j, stream)
+            return
         l, R = self.layer_of(j), self.R
         if self.router:
             r = self.fn_router(stream or self.s, self._x, 0, D, self.router_w[l].data_ptr(),
@@ -178,12 +181,37 @@ class DecodeBench:
         for q in range(self.per_step):
             self.launch(i * self.per_step + q, stream)
 
+    def window(self, j: int, stream: int | None = None, ev: list | None = None) -> None:
+        """A window of more than 16 rows as forward.ffnMain issues it (forward.zig:2361-2403): ops.topk, moe.routed
+        (ea_moe_routed: the prefill path's item GEMMs in the scratch's prompt region), the shared expert's mlp and the
+        add; with ev, torch events on the launch stream around moe.routed."""
+        torch = self.torch
+        l, R = self.layer_of(j), self.R
+        s = stream or self.s
+        pick, wts = self._pick0 + j * R * SLOTS * 4, self._wts0 + j * R * SLOTS * 4
+        self.ops.topk(s, self._logits0 + j * R * E * 4, self._bias, pick, wts, R)
+        if ev is not None:
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+        self.moe.routed(s, self._x, D, pick, wts, self.ex[l], self.scratch, self._out, R, x_dtype=0)
+        if ev is not None:
+            e1.record()
+            ev.append((j, e0, e1, "routed"))
+        sh = self.shared[l]
+        self.linear.call(s, self.lscratch, [sh.gate, sh.up], self._x, 0, R, [self.g.data_ptr(), self.u.data_ptr()],
+                         [1, 1])
+        self.ops.swiglu2(s, self.g.data_ptr(), self.u.data_ptr(), self.act.data_ptr(), R, I)
+        self.linear.call(s, self.lscratch, [sh.down], self.act.data_ptr(), 1, R, [self.sy.data_ptr()], [2])
+        self.ops.add_f32(s, self._out, self.sy.data_ptr(), R * D)
+
     def step_events(self, i: int, ev: list) -> None:
         """Step i again, timing its launches: the fused path's launches from the library's stage events
         (recorded on the launch stream), the sequence path's grouped launches from torch events on the same stream."""
         for q in range(self.per_step):
             j = i * self.per_step + q
-            if self.path == "fused":
+            if self.path == "fused" and self.R > 16:
+                self.window(j, ev=ev)
+            elif self.path == "fused":
                 self.launch(j)
                 ms = (C.c_float * 4)()
                 from ea_exl3._lib import check, lib
@@ -203,6 +231,9 @@ class DecodeBench:
         P = R * SLOTS
         maxu = min(P, E)
         self.ops.topk(s, self.logits[j].data_ptr(), self._bias, pick, wts, R)
+        if ev is not None:
+            e_in = torch.cuda.Event(enable_timing=True)
+            e_in.record()
         k = self.k
         k.group(s, pick, sc.ids, sc.count, sc.members, R, SLOTS, E, R)
         k.rot_in(s, self._x, D, pick, ex.suh_g, ex.suh_u, sc.xg, sc.xu, R, D, SLOTS, E, x_dtype=0)
@@ -226,7 +257,11 @@ class DecodeBench:
         if ev is not None:
             ev.append((j, e0, e1, "gateup"))
             ev.append((j, e2, e3, "down"))
+            e4 = torch.cuda.Event(enable_timing=True)
+            ev.append((j, e_in, e4, "routed"))  # the sequence's moe.routed: group to down_combine
         k.down_combine(s, sc.z, pick, ex.svh_d, sc.y, wts, self._out, R, P, D, 1, SLOTS, E)
+        if ev is not None:
+            ev[-1][2].record()
         sh = self.shared[l]
         self.linear.call(s, self.lscratch, [sh.gate, sh.up], self._x, 0, R, [self.g.data_ptr(), self.u.data_ptr()],
                          [1, 1])
@@ -663,6 +698,11 @@ WORKLOADS = {  # name -> (workload, rows, mixed widths, layers a step, unit)
               "the routed experts at 3 bits", 16, True, 1, "us/layer"),
     "stack": ("config 5: 75 resident MoE layers of one TP=8 rank (3-bit for 70 % of the routed experts, 4-bit "
               "shared experts), one token through all of them", 1, True, 75, "us/token"),
+    "window64": ("a 64-row decode window (the reference's moe.routed takes up to 128, forward.zig:21) of the config-3 "
+                 "layer: uniform top-8, 70 % of the routed experts at 3 bits; ops.topk, moe.routed, the shared expert, "
+                 "add", 64, True, 1, "us/layer"),
+    "window128": ("a 128-row decode window of the config-3 layer: uniform top-8, 70 % of the routed experts at 3 "
+                  "bits; ops.topk, moe.routed, the shared expert, add", 128, True, 1, "us/layer"),
 }
 
 def _line(args, value, unit, ms, config, roofline, steps=None, warmup=None) -> dict:
@@ -700,7 +740,7 @@ def run_decode(args, torch, np, name: str) -> Leg:
     n_layers = 75 if name == "stack" else args.layers
     total = args.warmup + args.steps
     bench = DecodeBench(R, n_layers, per_step, mixed, args.seed, 3 * total + 2, args.path,
-                        uniform=name == "multi", router=args.router)
+                        uniform=name == "multi" or name.startswith("window"), router=args.router)
     device.device_status()  # clear the status word before this leg
     # the layer whose output the oracle checks: launch 3 total (none of the timed ones), rows 0 and R - 1 (and two
     # between at 16 rows)
@@ -733,13 +773,21 @@ def run_decode(args, torch, np, name: str) -> Leg:
     picks = bench.pick.cpu().numpy()
     stages = None
     one_launch = args.path == "fused" and R == 1
-    if one_launch:
+    if R > 16 or args.path != "fused":
+        routed = [(j, a_, b_) for j, a_, b_, w in ev if w == "routed"]
+        durs = [a_.elapsed_time(b_) for _, a_, b_ in routed]
+        nbytes = [bench.launch_bytes(j, picks)[0] - bench.shared[bench.layer_of(j)].bytes() for j, _, _ in routed]
+        kernel = ("moe.routed (ea_moe_routed: " + ("route, rot_in, the two item lists' gate|up, epilogue and down "
+                  "GEMMs, the slot-ordered combine; the prefill path in the scratch's prompt region"
+                  if args.path == "fused" else "the reference's six-launch sequence: group, rot_in, grouped gate|up, "
+                  "epilogue, grouped down, down_combine") + "), timed with HIP events on its stream")
+    elif one_launch:
         # one row routed from logits: the layer is one launch, so the dominant kernel is the whole layer
         durs = [ms_[0] for _, ms_ in ev]
         nbytes = [bench.launch_bytes(j, picks)[0] for j, _ in ev]
         kernel = ("layer1_kernel (ea_ffn_moe_decode at one row routed from logits, the whole layer in one launch: "
                   "top-8, gate|up of the 8 picks and the shared expert, SwiGLU, down, slot-ordered combine)")
-    elif args.path == "fused":
+    else:
         durs = [ms_[0] for _, ms_ in ev]
         nbytes = [bench.gateup_bytes(j, picks) for j, _ in ev]
         kernel = ("route_kernel + gateup_wide_kernel (ea_ffn_moe_decode's first two launches, timed together: the "
@@ -747,10 +795,6 @@ def run_decode(args, torch, np, name: str) -> Leg:
                   "of the shared expert)")
         stages = {nm: round(sum(ms_[k] for _, ms_ in ev) / len(ev) * 1e3, 3)
                   for k, nm in enumerate(("gateup_us", "epilogue_us", "down_us", "combine_us"))}
-    else:
-        durs = [a.elapsed_time(b) for _, a, b, _ in ev]
-        nbytes = [bench.grouped_bytes(j, picks, w) for j, _, _, w in ev]
-        kernel = "grouped_kernel (the routed experts' EXL3 grouped GEMV: gate|up and down launches)"
     avg_ms = sum(durs) / len(durs)
     avg_b = sum(nbytes) / len(nbytes)
     timing = "HIP events recorded on the launch stream around each launch (dispatch included)"

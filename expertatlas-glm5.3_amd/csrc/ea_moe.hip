@@ -13,6 +13,11 @@ constexpr uint32_t DOWN_CFG[4] = {8, 4, 1, 1};
 
 static size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
 
+// Windows the decode layer does not hold (more than 16 rows) up to the reference's widest decode window
+// (forward.zig:21 MAX_LIN_ROWS = 128) take the prefill path's item GEMMs instead of the six-launch sequence; the
+// scratch holds a prompt scratch for them after the sequence's buffers (which the experts.* calls may still use).
+constexpr uint32_t WINDOW_ROWS = 128;
+
 struct MoeLayout {
     size_t xg, xu, xd, z, y, ids, count, members, sync, fused, fused_bytes, total;
 };
@@ -38,6 +43,8 @@ static MoeLayout moe_layout(const ea_routed* ex, uint32_t rows, uint32_t slots) 
     l.members = take(maxu * rows * 4);
     l.sync = take(4096);
     l.fused_bytes = dl_region_bytes(rows, slots, (uint32_t)D, (uint32_t)I, ex->count);
+    if (l.fused_bytes == 0 && rows > DL_REGION_ROWS && rows <= WINDOW_ROWS && D % 128 == 0 && I % 128 == 0)
+        l.fused_bytes = prompt_region_bytes(ex, rows, slots);
     l.fused = take(l.fused_bytes);
     l.total = off;
     return l;
@@ -106,6 +113,17 @@ int ea_moe_routed(ea_stream_t stream, const void* x, int x_dtype, uint32_t x_str
     const int f = decode_layer(s, x, x_dtype, x_stride, nullptr, nullptr, 0.f, const_cast<int32_t*>(pick),
                                const_cast<float*>(wts), ex, nullptr, sc, out, R);
     if (f != EA_UNPORTED_GROUPED_VARIANT) return f;
+    // more than 16 rows: the prefill path in the scratch's prompt region, when the scratch was made for this shape
+    // (its region sits where this layer's layout puts it) and the widths are ones the item GEMMs decode
+    if (sc->rows > DL_REGION_ROWS && sc->fused && ex->k2_gu[0] >= 2 && ex->k2_gu[1] <= 16 && ex->k2_d[0] >= 2 &&
+        ex->k2_d[1] <= 16 && ex->cb <= 2) {
+        const MoeLayout l = moe_layout(ex, sc->rows, sc->slots);
+        if (l.fused_bytes && sc->fused == sc->xg + l.fused) {
+            ea_prompt_scratch ps{};
+            prompt_region_carve(ex, sc->rows, sc->slots, sc->fused, &ps);
+            return ea_prompt_experts_run(stream, x, x_dtype, x_stride, pick, wts, ex, &ps, out, R, 0, 0);
+        }
+    }
     const uint32_t D = ex->dims, I = ex->width, E = ex->count, slots = sc->slots, P = R * slots;
     const uint32_t maxu = P < E ? P : E;
     int r = launch_group(s, pick, dptr<int>(sc->ids), dptr<int>(sc->count), dptr<int>(sc->members), R, slots, E, R);

@@ -1111,6 +1111,31 @@ static void wide_gemm(hipStream_t s, uint32_t cb, const uint16_t* X0, const uint
     }
 }
 
+// A decode window of more than 16 rows through the prefill path (ea_moe_routed): the moe scratch holds a prompt
+// scratch with the pair plane (the slots added in order, so a window's rows get the same bits on every run) in its
+// region; both follow from the layer's shape.
+size_t prompt_region_bytes(const ea_routed* ex, uint32_t rows, uint32_t slots) {
+    return prompt_layout(ex, rows, slots, 1).total;
+}
+
+int prompt_region_carve(const ea_routed* ex, uint32_t rows, uint32_t slots, uint64_t base, ea_prompt_scratch* s) {
+    const PromptLayout l = prompt_layout(ex, rows, slots, 1);
+    s->sorted = base + l.sorted;
+    s->items = base + l.items;
+    s->count = base + l.count;
+    s->xd = base + l.xd;
+    s->plane = base + l.plane;
+    s->xg = base + l.xg;
+    s->xu = base + l.xu;
+    s->z = base + l.z;
+    s->zp = base + l.zp;
+    s->pclass = base + l.pclass;
+    s->rows = l.rows;
+    s->slots = slots;
+    s->max_items = l.max_items;
+    return EA_OK;
+}
+
 }  // namespace ea
 
 using namespace ea;

@@ -149,7 +149,8 @@ typedef struct ea_routed {
 typedef struct ea_moe_scratch {
     uint64_t xg, xu, xd, z, y, ids, count, members;
     uint64_t sync;         /* reserved counters (zeroed by ea_moe_scratch_init) */
-    uint64_t fused;        /* the decode layer's region (rows <= 16), else 0; zeroed by init */
+    uint64_t fused;        /* the decode layer's region (rows <= 16), the prefill path's (17..128 rows), else 0;
+                              zeroed by init */
     uint32_t rows, slots;
 } ea_moe_scratch;
 
@@ -161,10 +162,12 @@ int ea_moe_scratch_init(ea_stream_t stream, ea_moe_scratch* s, void* base, size_
 
 /* out fp32 [R, D] = the R rows' routed experts weighted by wts. Replaces moe.routed (moe.zig:279-293).
  * x: [R, D] rows x_stride apart; pick int32 / wts fp32 [R, slots]. With a scratch of at most 16 rows, widths
- * 2..10, mcg or mul1 and I of 128 or 256, the decode layer's launches (three at one row, five above); otherwise the
- * six-launch sequence of moe.zig:279-293. As the reference groups pairs (maxm = R), an expert computes its first R
- * pairs in pair order; a slot past them (picks naming one expert more than R times) reads y as it is, as a slot
- * without an expert does. */
+ * 2..10, mcg or mul1 and I of 128 or 256, the decode layer's launches (three at one row, five above); with a scratch
+ * of 17..128 rows (the reference's decode windows, forward.zig:21), the prefill path's item GEMMs in the scratch's
+ * prompt region, the slots added in order (the same bits every run; every pair of a window computed); otherwise the
+ * six-launch sequence of moe.zig:279-293. On the decode layer and the sequence, as the reference groups pairs
+ * (maxm = R), an expert computes its first R pairs in pair order; a slot past them (picks naming one expert more than
+ * R times) reads y as it is, as a slot without an expert does. */
 int ea_moe_routed(ea_stream_t stream, const void* x, int x_dtype, uint32_t x_stride, const int32_t* pick,
                   const float* wts, const ea_routed* ex, const ea_moe_scratch* s, float* out, uint32_t R);
 

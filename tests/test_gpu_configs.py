@@ -142,3 +142,37 @@ def test_config5_mixed_width_layers_from_logits(ea):
         want = orc.moe_routed(x, pick_w, wts_w, oracle_routed(host), 1, 8) + shared.oracle(x, 1, False)
         assert_close_rms(device.download(out), want, 2e-3, f"config 5 layer {call % 3} call {call}")
     assert device.device_status() == 0
+
+
+@pytest.mark.parametrize("R", [64, 128])
+def test_decode_window_rows_through_prefill(ea, R):
+    """moe.routed on decode windows of 17..128 rows (forward.zig:21, moe.zig:279-293) at the full shard shape, config
+    3's routing (uniform top-8) and widths (70 % of the experts at 3 bits): the scratch's prompt region runs the prefill
+    path's item GEMMs. Every eighth row and the last against the oracle's moe.routed, and the same bits on a second
+    run (the slots are added in order)."""
+    device, _, moe, _, synth = ea
+    E, D, I, slots = 256, 6144, 256, 8
+    pick = synth.picks_uniform(1300 + R, R, E, slots)
+    wts = synth.routing_weights(1301 + R, R, slots)
+    host = synth.HostLayer(1302 + R, experts=E, dims=D, width=I, k2=synth.mixed_widths(1303, E), only=np.unique(pick))
+    x = synth.activations(1304 + R, R, D, "f16")
+    ex = moe.Routed(host)
+    sc = moe.Scratch(ex, R, slots)
+    assert sc.c.fused != 0  # the prompt region
+    dx, dp, dw = device.upload(x), device.upload(pick), device.upload(wts)
+    outs = []
+    for _ in range(2):
+        out = device.zeros((R, D), torch.float32)
+        moe.routed(device.stream(), dx.data_ptr(), D, dp.data_ptr(), dw.data_ptr(), ex, sc, out.data_ptr(), R,
+                   x_dtype=0)
+        outs.append(device.download(out))
+    rows = np.unique(np.concatenate([np.arange(0, R, 8), [R - 1]]))
+    want = orc.moe_routed(np.ascontiguousarray(x[rows]), np.ascontiguousarray(pick[rows]),
+                          np.ascontiguousarray(wts[rows]), oracle_routed(host), len(rows), slots)
+    assert_close_rms(outs[0][rows], want, 2e-3, f"moe.routed, {R}-row window")
+    np.testing.assert_array_equal(outs[1], outs[0])
+    # a window smaller than the scratch: the first 40 rows alone give the same rows' bits
+    out = device.zeros((40, D), torch.float32)
+    moe.routed(device.stream(), dx.data_ptr(), D, dp.data_ptr(), dw.data_ptr(), ex, sc, out.data_ptr(), 40, x_dtype=0)
+    np.testing.assert_array_equal(device.download(out), outs[0][:40])
+    assert device.device_status() == 0

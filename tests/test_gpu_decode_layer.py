@@ -120,8 +120,9 @@ def test_ffn_decode_routed_only_i128(ea):
 
 
 def test_moe_routed_fused_matches_sequence(ea):
-    """ea_moe_routed takes the one-launch path for a scratch of <= 16 rows and the six-launch sequence above that;
-    both must meet the bar against the oracle on the same inputs (and agree with each other to the same bar)."""
+    """ea_moe_routed takes the decode layer for a scratch of <= 16 rows, the prefill path's item GEMMs in the scratch's
+    prompt region for 17..128 rows, and the six-launch sequence above that; all three meet the bar against the oracle on
+    the same inputs (and agree with each other to the same bar)."""
     device, linear, moe, synth = ea
     R, E, D, I = 12, 256, 2048, 256
     pick = synth.picks_uniform(500, R, E, 8)
@@ -134,15 +135,16 @@ def test_moe_routed_fused_matches_sequence(ea):
     ex = moe.Routed(host)
     dx, dp, dw = device.upload(x), device.upload(pick), device.upload(wts)
     outs = []
-    for cap in (16, 32):
+    for cap in (16, 32, 200):
         sc = moe.Scratch(ex, cap, 8)
-        assert (sc.c.fused != 0) == (cap <= 16)
+        assert (sc.c.fused != 0) == (cap <= 128)
         out = device.zeros((R, D), torch.float32)
         moe.routed(device.stream(), dx.data_ptr(), D, dp.data_ptr(), dw.data_ptr(), ex, sc, out.data_ptr(), R, x_dtype=0)
         outs.append(device.download(out))
         assert device.device_status() == 0
         assert_close_rms(outs[-1], want, 2e-3, f"moe.routed cap={cap}")
-    assert_close_rms(outs[0], outs[1], 2e-3, "fused vs sequence")
+    assert_close_rms(outs[0], outs[1], 2e-3, "decode layer vs prefill path")
+    assert_close_rms(outs[0], outs[2], 2e-3, "decode layer vs sequence")
 
 
 def test_ffn_decode_one_row_routed_only_i128(ea):
