@@ -58,9 +58,11 @@ __device__ __forceinline__ float load_coherent(const float* p) {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Block (job, column block nb of 128, split): WK waves each take per_warp consecutive k tiles of the split; rows in
-// passes of 16. SK == 1: the block finishes its columns. SK > 1: partial sums to Z[split], and the block that
-// arrives last on the (pass, nb) counter sums the splits in order, finishes, and resets the counter to zero.
+// Block (job, column block nb of 128, split; pass of 16 rows = blockIdx.y): WK waves each take per_warp consecutive k
+// tiles of the split for the pass's rows. Every pass is its own block (the passes decode the same tiles side by side,
+// not one after another: 128 rows of a 6144 x 256 linear are 256 blocks, not 32 blocks of eight passes). SK == 1: the
+// block finishes its columns. SK > 1: partial sums to Z[split], and the block that arrives last on the (pass, nb)
+// counter sums the splits in order, finishes, and resets the counter to zero.
 template <int CB, int K2, int WK>
 __global__ void __launch_bounds__(WK * 64) linear_kernel(ea_jobs jobs, int M, int K) {
     int ji = 0;
@@ -85,7 +87,8 @@ __global__ void __launch_bounds__(WK * 64) linear_kernel(ea_jobs jobs, int M, in
 
     __shared__ float red[WK][16][128];
     __shared__ int last;
-    for (int m0 = 0, pass = 0; m0 < M; m0 += 16, ++pass) {
+    {
+        const int pass = (int)blockIdx.y, m0 = 16 * pass;
         const int R = min(16, M - m0);
         const int r = m0 + (lane & 15);
         const uint16_t* const xrow[1] = {r < M ? xh + (size_t)r * K : nullptr};
@@ -517,9 +520,10 @@ static bool launch_small(const ea_jobs& jobs, const ea_rot_jobs* rj, hipStream_t
 // the (K2, codebook) pairs this build instantiates: the reference's four (exl3.zig:40) and 3 / 4 bits mcg
 template <int CB, int K2>
 static void launch_wk(const ea_jobs& jobs, int blocks, hipStream_t s, int M, int K, int wk) {
-    if (wk == 2) linear_kernel<CB, K2, 2><<<blocks, 2 * 64, 0, s>>>(jobs, M, K);
-    else if (wk == 4) linear_kernel<CB, K2, 4><<<blocks, 4 * 64, 0, s>>>(jobs, M, K);
-    else linear_kernel<CB, K2, 8><<<blocks, 8 * 64, 0, s>>>(jobs, M, K);
+    const dim3 grid((unsigned)blocks, (unsigned)((M + 15) / 16));  // passes of 16 rows side by side
+    if (wk == 2) linear_kernel<CB, K2, 2><<<grid, 2 * 64, 0, s>>>(jobs, M, K);
+    else if (wk == 4) linear_kernel<CB, K2, 4><<<grid, 4 * 64, 0, s>>>(jobs, M, K);
+    else linear_kernel<CB, K2, 8><<<grid, 8 * 64, 0, s>>>(jobs, M, K);
 }
 
 static bool launch_variant(const ea_jobs& jobs, int blocks, hipStream_t s, int M, int K, uint32_t k2, uint32_t cb,

@@ -46,6 +46,8 @@ def test_unpack_bit_exact(ea, k2, cb):
     (16, 6144, 256, 10, 2, 2),   # 5-bit mul1 (the real checkpoints' shared expert), 16 rows
     (40, 1024, 640, 8, 2, 0),    # three row passes, fp16 out
     (128, 512, 384, 6, 1, 2),    # the most rows a call takes
+    (128, 6144, 256, 8, 1, 1),   # the shared expert's gate / up on a 128-row window: 8 row passes x 8 K splits at once
+    (96, 256, 6144, 8, 1, 2),    # its down on a 96-row window
     (4, 6144, 2048, 8, 1, 2),    # config 1's shape at four rows (the small-row kernel: 32-column groups x 8 splits)
     (7, 2048, 512, 6, 1, 0),     # 3 bits, fp16 out, a ragged row count
     (2, 1024, 384, 4, 1, 2),     # 2 bits
