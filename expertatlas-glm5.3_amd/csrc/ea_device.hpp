@@ -133,13 +133,21 @@ __device__ __forceinline__ uint32_t cb_pair(uint32_t s0, uint32_t s1) {
         // add of a word's two halves a value (SDWA selects the halves and the destination half)
         const uint32_t a = __builtin_amdgcn_bitop3_b32(x0, 0x8FFF8FFFu, 0x3B603B60u, 0x6A);
         const uint32_t b = __builtin_amdgcn_bitop3_b32(x1, 0x8FFF8FFFu, 0x3B603B60u, 0x6A);
+        // Both adds write half a register (SDWA dst_sel WORD_0 / WORD_1), and on gfx950 a half-register write needs
+        // wait states before anything reads that register: the second add reads the first's (it keeps the low half),
+        // and the MFMA or VALU that takes the pair reads the second's. The compiler inserts such wait states for code
+        // it generates but cannot see them inside an asm string, so they are part of the sequence itself: two after
+        // each add. Without them the result depended on how far the scheduler happened to place the readers: the
+        // register-streaming item GEMM built for 3 row tiles summed wrong at widths 12-16 while the 7-tile build
+        // passed. (The compiler's own form of these adds writes both halves padded and merges them with a v_or:
+        // one VALU more a pair, measured 1-3.5 % slower on the decode-bound kernels.)
         uint32_t r;
-        asm("v_add_f16_sdwa %0, %1, %1 dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:WORD_0 src1_sel:WORD_1"
-            : "=v"(r)
-            : "v"(a));
-        asm("v_add_f16_sdwa %0, %1, %1 dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:WORD_0 src1_sel:WORD_1"
-            : "+v"(r)
-            : "v"(b));
+        asm("v_add_f16_sdwa %0, %1, %1 dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:WORD_0 src1_sel:WORD_1\n\t"
+            "s_nop 1\n\t"
+            "v_add_f16_sdwa %0, %2, %2 dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:WORD_0 src1_sel:WORD_1\n\t"
+            "s_nop 1"
+            : "=&v"(r)
+            : "v"(a), "v"(b));
         return r;
     }
 }

@@ -21,15 +21,13 @@ namespace ea {
 // this library's for the register-streaming GEMM of widths above 10 (IPM_WIDE); the staged GEMMs (widths 2..10) take
 // items of up to 80 (five row tiles): against 48 the same at 512 rows and 3-4 % faster at 2048 (a heavy expert
 // decoded in fewer items), against 112 (seven row tiles, more accumulators) faster at both; 64 and 96 measured between.
-// A pair's sums do not depend on its item. The register-streaming GEMM is built for 7 row tiles only: routing into items of
-// at most 48 pairs is right with it (checked with that kernel at widths above 10), but the same kernel built for 3
-// row tiles gave wrong sums at width 12 (no register spills, the same index arithmetic, extra wait states after the
-// decoder's fp16 adds changed nothing); that instantiation is not built.
+// A pair's sums do not depend on its item. The register-streaming GEMM keeps the reference's 112 (7 row tiles); its
+// index arithmetic is the same for any number of row tiles (a 3-tile build once summed wrong at widths 12-16: the
+// decoder's half-register fp16 adds lacked the wait states their readers need, which cb_pair now carries).
 constexpr int IPM = 80;
 constexpr int IPM_TILES = IPM / 16;
 constexpr int IPM_WIDE = 112;
 constexpr int IPM_WIDE_TILES = IPM_WIDE / 16;
-static_assert(IPM_WIDE_TILES == 7, "the register-streaming item GEMM is verified for 7 row tiles only");
 constexpr uint32_t CHUNK_ROWS = 4096;  // rows a pass at most (prompt_experts.zig:17)
 constexpr int ROUTE_THREADS = 1024;
 constexpr int ROUTE_HELD = 16;  // picks a route thread holds in registers: 16,384 pairs (2,048 rows of 8 slots)
