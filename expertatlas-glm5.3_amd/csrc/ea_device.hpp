@@ -271,6 +271,54 @@ __device__ __forceinline__ void fwht128_w64(float& v0, float& v1, int lane) {
     fwht_level<32>(v0, v1, lane);
 }
 
+// ---- Walsh-Hadamard over 128 values held eight a lane by 16 lanes ---------------------------------------------
+// Lane l of a 16-lane group holds values 8 h8_group(l) .. + 7. The butterflies run over value-index bits 0..6 in that
+// order: bits 0..2 inside the lane, bits 3..6 across lanes at distances 1, 2, 7 and 8 (h8_group places the groups so
+// that each of those distances is one DPP pattern: the two quad permutes, the half-row mirror, the row rotation by 8).
+// A cross-lane step is one v_fmac_f32 with the partner's value as its DPP operand: v + s * partner, s = -1 in the lane
+// holding the butterfly's upper element, whose result is then (lower - upper) negated, exactly (s = +-1, one
+// rounding); the partner of every later step holds a value of the same sign, so after the four steps each lane's true
+// values are its values times the returned sign, (-1)^popcount(group). Nonzero results are the plain butterflies'
+// bits; a caller that scales by the sign with an fma adding +0 also returns every zero as +0.
+__device__ __forceinline__ int h8_group(int lane) {
+    const int l = lane & 15;
+    return l ^ (((l >> 2) & 1) * 3);
+}
+
+// The four cross-lane steps of eight values in one statement, so their order is fixed: every DPP read comes eight
+// instructions after the write of its register, the leading s_nop covers the first read, and the trailing one a DPP
+// read of the last results by the code that follows (a VALU write followed by a DPP read of the same register needs
+// two wait states, which the compiler's hazard pass does not see across an asm statement).
+#define EA_FMAC_DPP8(ctl, s)                                                                                      \
+    "v_fmac_f32_dpp %0, %0, " s " " ctl " row_mask:0xf bank_mask:0xf\n\t"                                           \
+    "v_fmac_f32_dpp %1, %1, " s " " ctl " row_mask:0xf bank_mask:0xf\n\t"                                           \
+    "v_fmac_f32_dpp %2, %2, " s " " ctl " row_mask:0xf bank_mask:0xf\n\t"                                           \
+    "v_fmac_f32_dpp %3, %3, " s " " ctl " row_mask:0xf bank_mask:0xf\n\t"                                           \
+    "v_fmac_f32_dpp %4, %4, " s " " ctl " row_mask:0xf bank_mask:0xf\n\t"                                           \
+    "v_fmac_f32_dpp %5, %5, " s " " ctl " row_mask:0xf bank_mask:0xf\n\t"                                           \
+    "v_fmac_f32_dpp %6, %6, " s " " ctl " row_mask:0xf bank_mask:0xf\n\t"                                           \
+    "v_fmac_f32_dpp %7, %7, " s " " ctl " row_mask:0xf bank_mask:0xf\n\t"
+
+__device__ __forceinline__ float fwht128_x8(float (&v)[8], int lane) {
+#pragma unroll
+    for (int b = 1; b < 8; b <<= 1)
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            if (!(j & b)) {
+                const float lo = v[j], hi = v[j | b];
+                v[j] = lo + hi;
+                v[j | b] = lo - hi;
+            }
+    const int g = h8_group(lane);
+    const float s3 = g & 1 ? -1.f : 1.f, s4 = g & 2 ? -1.f : 1.f, s5 = g & 4 ? -1.f : 1.f, s6 = g & 8 ? -1.f : 1.f;
+    asm volatile("s_nop 1\n\t" EA_FMAC_DPP8("quad_perm:[1,0,3,2]", "%8") EA_FMAC_DPP8("quad_perm:[2,3,0,1]", "%9")
+                     EA_FMAC_DPP8("row_half_mirror", "%10") EA_FMAC_DPP8("row_ror:8", "%11") "s_nop 1"
+                 : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]), "+v"(v[4]), "+v"(v[5]), "+v"(v[6]), "+v"(v[7])
+                 : "v"(s3), "v"(s4), "v"(s5), "v"(s6));
+    return __builtin_popcount((unsigned)g) & 1 ? -1.f : 1.f;
+}
+#undef EA_FMAC_DPP8
+
 // 32-lane half-wave variant: lane j (0..31 within its half) holds values 4j .. 4j + 3.
 __device__ __forceinline__ void fwht128_h32(float (&v)[4], int lane) {
     const float a = v[0] + v[1], b = v[0] - v[1], c = v[2] + v[3], d = v[2] - v[3];

@@ -94,11 +94,11 @@ __global__ void __launch_bounds__(GROUP_THREADS) group_kernel(const int* __restr
 }
 
 // ---- per-pair input rotation ------------------------------------------------------------------------------------
-// Block (row, matrix, 2048 columns of K): 16 lanes a 128-block, lane l holding its values 8 (l & 15) .. +7; the row's
-// activations are read once and rotated for each of its slots in turn. out[p] = fp16((x[row] * suh[e]) @ H *
+// Block (row, matrix, 2048 columns of K): 16 lanes a 128-block, lane l holding its values 8 h8_group(l) .. +7; the
+// row's activations are read once and rotated for each of its slots in turn. out[p] = fp16((x[row] * suh[e]) @ H *
 // HAD_SCALE) for each pair p of the row with an expert (exl3_experts.cu:116-134). The butterflies run over value-index
-// bits 0..6 in that order (three inside a lane, four across lanes), as in a one-lane-pair-a-value layout, so each
-// output is the same fp32 sum rounded the same way. With `zero`, the matrix-0 blocks also clear the row's values
+// bits 0..6 in that order (three inside a lane, four across lanes: fwht128_x8), as in a one-lane-pair-a-value layout,
+// so each output is the same fp32 sum rounded the same way. With `zero`, the matrix-0 blocks also clear the row's values
 // k .. k + 7 of zero [rows, K] (fp32, or fp16 with zero_half): the output that a prefill pass without a pair plane
 // adds its slots into.
 __global__ void __launch_bounds__(256) rot_in_kernel(const void* __restrict__ x, int x_dtype, int x_stride,
@@ -107,7 +107,7 @@ __global__ void __launch_bounds__(256) rot_in_kernel(const void* __restrict__ x,
                                                      uint16_t* __restrict__ out1, int K, int slots, int E, int vec,
                                                      void* __restrict__ zero, int zero_half) {
     const int row = blockIdx.x, mat = blockIdx.y, lane = threadIdx.x & 63;
-    const int k = blockIdx.z * 2048 + 8 * (int)threadIdx.x;
+    const int k = blockIdx.z * 2048 + 128 * ((int)threadIdx.x >> 4) + 8 * h8_group(lane);
     if (k >= K) return;  // whole 16-lane groups (K % 128 == 0)
     if (zero && mat == 0) {
         const bool al = (reinterpret_cast<uintptr_t>(zero) & 15) == 0;  // uniform; K % 128 == 0 keeps rows aligned
@@ -132,9 +132,6 @@ __global__ void __launch_bounds__(256) rot_in_kernel(const void* __restrict__ x,
     const uint16_t* suh = mat ? suh1 : suh0;
     uint16_t* out = mat ? out1 : out0;
     const size_t xr = (size_t)row * x_stride;
-    // v' = s * v + o: o - v for the lane holding the upper element of a butterfly, v + o otherwise (exact: s = +-1)
-    const float s1 = lane & 1 ? -1.f : 1.f, s2 = lane & 2 ? -1.f : 1.f, s4 = lane & 4 ? -1.f : 1.f,
-                s8 = lane & 8 ? -1.f : 1.f;
     float xv[8];
     if (vec) {  // 16-byte aligned rows
         if (x_dtype == F32) {
@@ -164,27 +161,12 @@ __global__ void __launch_bounds__(256) rot_in_kernel(const void* __restrict__ x,
         float v[8];
 #pragma unroll
         for (int j = 0; j < 8; ++j) v[j] = xv[j] * h2f((uint16_t)(sw[j >> 1] >> (16 * (j & 1))));
-#pragma unroll
-        for (int b = 1; b < 8; b <<= 1)
-#pragma unroll
-            for (int j = 0; j < 8; ++j)
-                if (!(j & b)) {
-                    const float lo = v[j], hi = v[j | b];
-                    v[j] = lo + hi;
-                    v[j | b] = lo - hi;
-                }
-#pragma unroll
-        for (int j = 0; j < 8; ++j) v[j] = __builtin_fmaf(s1, v[j], lane_xor<1>(v[j]));
-#pragma unroll
-        for (int j = 0; j < 8; ++j) v[j] = __builtin_fmaf(s2, v[j], lane_xor<2>(v[j]));
-#pragma unroll
-        for (int j = 0; j < 8; ++j) v[j] = __builtin_fmaf(s4, v[j], lane_xor<4>(v[j]));
-#pragma unroll
-        for (int j = 0; j < 8; ++j) v[j] = __builtin_fmaf(s8, v[j], lane_xor<8>(v[j]));
+        const float sc = fwht128_x8(v, lane) * HAD_SCALE;  // the values' sign folded into the scale (exact)
         u4v w;
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-            w[j] = (uint32_t)f2h(v[2 * j] * HAD_SCALE) | ((uint32_t)f2h(v[2 * j + 1] * HAD_SCALE) << 16);
+            w[j] = (uint32_t)f2h(__builtin_fmaf(v[2 * j], sc, 0.f)) |
+                   ((uint32_t)f2h(__builtin_fmaf(v[2 * j + 1], sc, 0.f)) << 16);
         *reinterpret_cast<u4v*>(out + (size_t)p * K + k) = w;
     }
 }

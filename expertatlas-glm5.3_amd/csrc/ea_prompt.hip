@@ -174,19 +174,17 @@ struct DnAtomic {
 
 // The down items' epilogue without a pair plane (prompt_experts.cu:719-797, modes 0 and 1): for each occupied row
 // tile, the block's four waves hand their 16 rows x 32 columns (two column tiles each, MFMA accumulator layout) to LDS,
-// then thread (row r, lane l16) takes the row's columns l16 + 16 j of the 128-column block cb: the FWHT over the
-// block (column bits 4, 5, 6 inside the thread, bits 0..3 across the row's 16 lanes), the output scale svh_d *
-// HAD_SCALE (sv, loaded by the caller) and the pair's routing weight, then an atomic add into its row of out: fp32, 16
-// lanes a row covering 64 contiguous bytes an instruction; or, with half, packed fp16 pairs once the lanes of a column
-// pair have traded values. The slots of a row meet in out in arrival order, so the sums' bits may differ run to run.
+// then thread (row r, lane l16) takes the row's columns g + 16 j (g = h8_group(l16)) of the 128-column block cb: the
+// FWHT over the block (fwht128_x8: column bits 4, 5, 6 inside the thread, bits 0..3 across the row's 16 lanes), the
+// output scale svh_d * HAD_SCALE (sv, loaded by the caller) and the pair's routing weight, then an atomic add into
+// its row of out: fp32, 16 lanes a row covering 64 contiguous bytes an instruction; or, with half, packed fp16 pairs
+// once the lanes of a column pair have traded values. The slots of a row meet in out in arrival order, so the sums' bits may differ run to run.
 // The buffer halves alternate (eb), so one barrier a row tile suffices: a half is written again only after the
 // barrier that follows every thread's reads of it.
 template <int MT>
 __device__ __forceinline__ void dn_atomic(const f4v (&acc)[MT][2], int mts, int wave, int lane, int cb,
                                           const uint32_t (&sv)[4], const DnAtomic& a, int& eb) {
-    const int r = (int)threadIdx.x >> 4, l16 = lane & 15;
-    const float s1 = l16 & 1 ? -1.f : 1.f, s2 = l16 & 2 ? -1.f : 1.f, s4 = l16 & 4 ? -1.f : 1.f,
-                s8 = l16 & 8 ? -1.f : 1.f;
+    const int r = (int)threadIdx.x >> 4, l16 = lane & 15, g = h8_group(lane);
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
         if (mt >= mts) break;  // uniform
@@ -198,44 +196,28 @@ __device__ __forceinline__ void dn_atomic(const f4v (&acc)[MT][2], int mts, int 
         __syncthreads();
         float v[8];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) v[j] = E[r * ES + 16 * j + l16];
+        for (int j = 0; j < 8; ++j) v[j] = E[r * ES + 16 * j + g];
         eb ^= 1;
-#pragma unroll
-        for (int b = 1; b < 8; b <<= 1)
-#pragma unroll
-            for (int j = 0; j < 8; ++j)
-                if (!(j & b)) {
-                    const float lo = v[j], hi = v[j | b];
-                    v[j] = lo + hi;
-                    v[j | b] = lo - hi;
-                }
-#pragma unroll
-        for (int j = 0; j < 8; ++j) v[j] = __builtin_fmaf(s1, v[j], lane_xor<1>(v[j]));
-#pragma unroll
-        for (int j = 0; j < 8; ++j) v[j] = __builtin_fmaf(s2, v[j], lane_xor<2>(v[j]));
-#pragma unroll
-        for (int j = 0; j < 8; ++j) v[j] = __builtin_fmaf(s4, v[j], lane_xor<4>(v[j]));
-#pragma unroll
-        for (int j = 0; j < 8; ++j) v[j] = __builtin_fmaf(s8, v[j], lane_xor<8>(v[j]));
+        const float sg = fwht128_x8(v, lane);  // the values' sign, folded into the scale (exact)
         const int idx = mt * 16 + r, p = a.pair_sh[idx];
         const float w = p >= 0 ? a.wts_sh[idx] : 0.f;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) v[j] = v[j] * (h2f((uint16_t)(sv[j >> 1] >> (16 * (j & 1)))) * HAD_SCALE) * w;
+        for (int j = 0; j < 8; ++j) v[j] = v[j] * (sg * (h2f((uint16_t)(sv[j >> 1] >> (16 * (j & 1)))) * HAD_SCALE)) * w;
         const size_t ro = (size_t)(p >= 0 ? p / a.slots : 0) * a.D + (size_t)cb * 128;
         if (!a.half) {
             if (p >= 0) {
-                float* o = static_cast<float*>(a.out) + ro + l16;
+                float* o = static_cast<float*>(a.out) + ro + g;
 #pragma unroll
                 for (int j = 0; j < 8; ++j)
                     __builtin_amdgcn_global_atomic_fadd_f32((__attribute__((address_space(1))) float*)(o + 16 * j),
                                                             v[j]);
             }
         } else {
-            // lane pair (l16, l16 ^ 1) holds columns (16 j + even, 16 j + odd): the even lane adds j = 0..3, the odd
-            // lane j = 4..7, each as one packed pair at the even column (static indices only: both lanes' pairs are
-            // formed and one is chosen)
-            const bool odd = l16 & 1;
-            uint16_t* base = static_cast<uint16_t*>(a.out) + ro + (l16 & ~1);
+            // lane pair (l16, l16 ^ 1) holds columns (16 j + even, 16 j + odd) (its groups differ in bit 0 only): the
+            // even column's lane adds j = 0..3, the odd one's j = 4..7, each as one packed pair at the even column
+            // (static indices only: both lanes' pairs are formed and one is chosen)
+            const bool odd = g & 1;
+            uint16_t* base = static_cast<uint16_t*>(a.out) + ro + (g & ~1);
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 const float oe = lane_xor<1>(v[q]), oo = lane_xor<1>(v[q + 4]);  // the partner's values
@@ -249,11 +231,13 @@ __device__ __forceinline__ void dn_atomic(const f4v (&acc)[MT][2], int mts, int 
     }
 }
 
-// svh_d of thread (r, l16)'s eight columns l16 + 16 j of column block cb, two fp16 a word (j even low).
+// svh_d of thread (r, l16)'s eight columns g + 16 j (g = h8_group(l16)) of column block cb, two fp16 a word (j even
+// low).
 __device__ __forceinline__ void dn_atomic_scales(const uint16_t* svh, int cb, int lane, uint32_t (&sv)[4]) {
 #pragma unroll
     for (int q = 0; q < 4; ++q)
-        sv[q] = (uint32_t)svh[cb * 128 + 32 * q + (lane & 15)] | ((uint32_t)svh[cb * 128 + 32 * q + 16 + (lane & 15)] << 16);
+        sv[q] = (uint32_t)svh[cb * 128 + 32 * q + h8_group(lane)] |
+                ((uint32_t)svh[cb * 128 + 32 * q + 16 + h8_group(lane)] << 16);
 }
 
 // Block (item, n block of NW * NTW tiles, matrix): wave w covers NTW n tiles over the whole K range for all of the
@@ -859,20 +843,19 @@ item_dn_kernel(const uint16_t* __restrict__ X, const int64_t* __restrict__ TP, c
 }
 
 // The down epilogue and slot combine of a prompt pass. Block (row r, 2048 columns): a thread holds 8 consecutive
-// columns of one 128-block (16 lanes a block); for each slot in order y = FWHT(plane[pair]) * HAD_SCALE * svh_d[e],
-// then out = fma(w, y, out) from zero, a slot without an expert adding w * 0. These are the operations and the order of
-// down_combine_kernel with one split (the butterflies over value-index bits 0..6, three inside a lane and four
-// across lanes), so the same bits; the rotated plane is not written back (nothing reads it after the combine).
+// columns of one 128-block (16 lanes a block, lane l the columns 8 h8_group(l) .. + 7); for each slot in order
+// y = FWHT(plane[pair]) * HAD_SCALE * svh_d[e], then out = fma(w, y, out) from zero, a slot without an expert adding
+// w * 0. These are the operations and the order of down_combine_kernel with one split (the butterflies over
+// value-index bits 0..6, three inside a lane and four across lanes: fwht128_x8), so the same bits (a zero y's sign
+// does not reach out, which starts at +0); the rotated plane is not written back (nothing reads it after the combine).
 // (prompt_experts.cu's deterministic combine; exl3_experts.cu:186-214 for the epilogue.)
 __global__ void __launch_bounds__(256) prompt_combine_kernel(const float* __restrict__ Z, const int* __restrict__ pick,
                                                              const uint16_t* __restrict__ svh_d,
                                                              const float* __restrict__ wts, float* __restrict__ out,
                                                              int D, int E, int slots) {
     const int r = blockIdx.x, lane = threadIdx.x & 63;
-    const int k = blockIdx.y * 2048 + 8 * (int)threadIdx.x;
+    const int k = blockIdx.y * 2048 + 128 * ((int)threadIdx.x >> 4) + 8 * h8_group(lane);
     if (k >= D) return;  // whole 16-lane groups (D % 128 == 0)
-    const float s1 = lane & 1 ? -1.f : 1.f, s2 = lane & 2 ? -1.f : 1.f, s4 = lane & 4 ? -1.f : 1.f,
-                s8 = lane & 8 ? -1.f : 1.f;
     float a[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) a[j] = 0.f;
@@ -890,25 +873,9 @@ __global__ void __launch_bounds__(256) prompt_combine_kernel(const float* __rest
                 v[j] = 0.f + z0[j];  // the split sum from zero
                 v[4 + j] = 0.f + z1[j];
             }
+            const float sc = fwht128_x8(v, lane) * HAD_SCALE;  // the values' sign folded into the scale (exact)
 #pragma unroll
-            for (int b = 1; b < 8; b <<= 1)
-#pragma unroll
-                for (int j = 0; j < 8; ++j)
-                    if (!(j & b)) {
-                        const float lo = v[j], hi = v[j | b];
-                        v[j] = lo + hi;
-                        v[j | b] = lo - hi;
-                    }
-#pragma unroll
-            for (int j = 0; j < 8; ++j) v[j] = __builtin_fmaf(s1, v[j], lane_xor<1>(v[j]));
-#pragma unroll
-            for (int j = 0; j < 8; ++j) v[j] = __builtin_fmaf(s2, v[j], lane_xor<2>(v[j]));
-#pragma unroll
-            for (int j = 0; j < 8; ++j) v[j] = __builtin_fmaf(s4, v[j], lane_xor<4>(v[j]));
-#pragma unroll
-            for (int j = 0; j < 8; ++j) v[j] = __builtin_fmaf(s8, v[j], lane_xor<8>(v[j]));
-#pragma unroll
-            for (int j = 0; j < 8; ++j) o[j] = v[j] * HAD_SCALE * h2f((uint16_t)(sv[j >> 1] >> (16 * (j & 1))));
+            for (int j = 0; j < 8; ++j) o[j] = v[j] * sc * h2f((uint16_t)(sv[j >> 1] >> (16 * (j & 1))));
         } else {
 #pragma unroll
             for (int j = 0; j < 8; ++j) o[j] = 0.f;
