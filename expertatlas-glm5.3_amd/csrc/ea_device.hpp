@@ -34,6 +34,12 @@ __device__ __forceinline__ float materialise(float x) {
 __device__ __forceinline__ float h2f(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
 // fp32 -> fp16, round to nearest even, from the fp32 value itself.
 __device__ __forceinline__ uint16_t f2h(float f) { return __builtin_bit_cast(uint16_t, (_Float16)materialise(f)); }
+// Two fp32 values -> a packed fp16 pair (the first in the low half), each rounded to nearest even from the fp32 value
+// itself: one v_cvt_pk_f16_f32.
+__device__ __forceinline__ uint32_t f2h2(float a, float b) {
+    typedef float f2v __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f2v){materialise(a), materialise(b)}, h2v));
+}
 __device__ __forceinline__ float bf2f(uint16_t b) { return __builtin_bit_cast(float, (uint32_t)b << 16); }
 __device__ __forceinline__ uint16_t f2bf(float f) {
     uint32_t u = __builtin_bit_cast(uint32_t, f);

@@ -154,20 +154,35 @@ __global__ void __launch_bounds__(256) rot_in_kernel(const void* __restrict__ x,
 #pragma unroll
         for (int j = 0; j < 8; ++j) xv[j] = load_act(x, x_dtype, xr + k + j);
     }
-    for (int q = 0; q < slots; ++q) {
-        const int p = row * slots + q, e = pick[p];
-        if (e < 0 || e >= E) continue;  // uniform over the block
-        const u4v sw = *reinterpret_cast<const u4v*>(suh + (size_t)e * K + k);
-        float v[8];
+    // eight slots at a time: their picks, then all their suh loads in flight before the first rotation (a slot
+    // without an expert loads expert 0's and is skipped)
+    constexpr int QB = 8;
+    for (int q0 = 0; q0 < slots; q0 += QB) {
+        int ev[QB];
+        u4v sw[QB];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) v[j] = xv[j] * h2f((uint16_t)(sw[j >> 1] >> (16 * (j & 1))));
-        const float sc = fwht128_x8(v, lane) * HAD_SCALE;  // the values' sign folded into the scale (exact)
-        u4v w;
+        for (int j = 0; j < QB; ++j) {
+            const int q = q0 + j < slots ? q0 + j : q0;
+            const int e = pick[row * slots + q];
+            ev[j] = q0 + j < slots && e >= 0 && e < E ? e : -1;
+        }
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-            w[j] = (uint32_t)f2h(__builtin_fmaf(v[2 * j], sc, 0.f)) |
-                   ((uint32_t)f2h(__builtin_fmaf(v[2 * j + 1], sc, 0.f)) << 16);
-        *reinterpret_cast<u4v*>(out + (size_t)p * K + k) = w;
+        for (int j = 0; j < QB; ++j)
+            sw[j] = *reinterpret_cast<const u4v*>(suh + (size_t)(ev[j] >= 0 ? ev[j] : 0) * K + k);
+        issued();
+#pragma unroll
+        for (int j = 0; j < QB; ++j) {
+            if (ev[j] < 0) continue;  // uniform over the block
+            float v[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) v[i] = xv[i] * h2f((uint16_t)(sw[j][i >> 1] >> (16 * (i & 1))));
+            const float sc = fwht128_x8(v, lane) * HAD_SCALE;  // the values' sign folded into the scale (exact)
+            u4v w;
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                w[i] = f2h2(__builtin_fmaf(v[2 * i], sc, 0.f), __builtin_fmaf(v[2 * i + 1], sc, 0.f));
+            *reinterpret_cast<u4v*>(out + (size_t)(row * slots + q0 + j) * K + k) = w;
+        }
     }
 }
 

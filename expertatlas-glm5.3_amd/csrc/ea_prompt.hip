@@ -859,29 +859,46 @@ __global__ void __launch_bounds__(256) prompt_combine_kernel(const float* __rest
     float a[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) a[j] = 0.f;
-    for (int q = 0; q < slots; ++q) {
-        const int p = r * slots + q, e = pick[p];
-        const float w = wts[p];
-        float o[8];
-        if (e >= 0 && e < E) {  // uniform over the block
-            const f4v z0 = *reinterpret_cast<const f4v*>(Z + (size_t)p * D + k);
-            const f4v z1 = *reinterpret_cast<const f4v*>(Z + (size_t)p * D + k + 4);
-            const u4v sv = *reinterpret_cast<const u4v*>(svh_d + (size_t)e * D + k);
-            float v[8];
+    // four slots at a time: their picks and weights, then all their plane and svh loads in flight before the first
+    // slot's rotation (a slot without an expert loads pair 0's row and expert 0's scales, and adds w * 0)
+    constexpr int QB = 4;
+    for (int q0 = 0; q0 < slots; q0 += QB) {
+        int ev[QB];
+        float wv[QB];
+        f4v z0[QB], z1[QB];
+        u4v sv[QB];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                v[j] = 0.f + z0[j];  // the split sum from zero
-                v[4 + j] = 0.f + z1[j];
-            }
-            const float sc = fwht128_x8(v, lane) * HAD_SCALE;  // the values' sign folded into the scale (exact)
-#pragma unroll
-            for (int j = 0; j < 8; ++j) o[j] = v[j] * sc * h2f((uint16_t)(sv[j >> 1] >> (16 * (j & 1))));
-        } else {
-#pragma unroll
-            for (int j = 0; j < 8; ++j) o[j] = 0.f;
+        for (int j = 0; j < QB; ++j) {
+            const int p = r * slots + (q0 + j < slots ? q0 + j : q0), e = pick[p];
+            wv[j] = wts[p];
+            ev[j] = e >= 0 && e < E ? p : -1;
+            const size_t zo = (size_t)(ev[j] >= 0 ? p : r * slots) * D + k;
+            z0[j] = *reinterpret_cast<const f4v*>(Z + zo);
+            z1[j] = *reinterpret_cast<const f4v*>(Z + zo + 4);
+            sv[j] = *reinterpret_cast<const u4v*>(svh_d + (size_t)(ev[j] >= 0 ? e : 0) * D + k);
         }
+        issued();
 #pragma unroll
-        for (int j = 0; j < 8; ++j) a[j] = __builtin_fmaf(w, o[j], a[j]);
+        for (int j = 0; j < QB; ++j) {
+            if (q0 + j >= slots) break;  // uniform
+            float o[8];
+            if (ev[j] >= 0) {  // uniform over the block
+                float v[8];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    v[i] = 0.f + z0[j][i];  // the split sum from zero
+                    v[4 + i] = 0.f + z1[j][i];
+                }
+                const float sc = fwht128_x8(v, lane) * HAD_SCALE;  // the values' sign folded into the scale (exact)
+#pragma unroll
+                for (int i = 0; i < 8; ++i) o[i] = v[i] * sc * h2f((uint16_t)(sv[j][i >> 1] >> (16 * (i & 1))));
+            } else {
+#pragma unroll
+                for (int i = 0; i < 8; ++i) o[i] = 0.f;
+            }
+#pragma unroll
+            for (int i = 0; i < 8; ++i) a[i] = __builtin_fmaf(wv[j], o[i], a[i]);
+        }
     }
     *reinterpret_cast<f4v*>(out + (size_t)r * D + k) = f4v{a[0], a[1], a[2], a[3]};
     *reinterpret_cast<f4v*>(out + (size_t)r * D + k + 4) = f4v{a[4], a[5], a[6], a[7]};
