@@ -127,14 +127,38 @@ __global__ void __launch_bounds__(WK * 64) linear_kernel(ea_jobs jobs, int M, in
             __syncthreads();
             if (last) {
                 __threadfence();
-                for (int rr = wave; rr < R; rr += WK) {
+                // the wave's rows wave, wave + WK, ..: QB splits of all of them loaded at once (64 values a lane),
+                // then added in split order (one round trip a batch of splits instead of one a split and row)
+                constexpr int RW = 16 / WK, QB = 32 / RW;
+                float v[RW][2];
+                for (int q0 = 0; q0 < SK; q0 += QB) {
+                    float z[QB][RW][2];
+#pragma unroll
+                    for (int q = 0; q < QB; ++q)
+#pragma unroll
+                        for (int i = 0; i < RW; ++i) {
+                            const int rr = wave + WK * i < R ? wave + WK * i : wave;  // rows past R re-read a row
+                            const size_t at = (size_t)(q0 + q < SK ? q0 + q : q0) * M * N +
+                                              ((size_t)m0 + rr) * N + col0 + 2 * lane;
+                            z[q][i][0] = load_coherent(Z + at);
+                            z[q][i][1] = load_coherent(Z + at + 1);
+                        }
+#pragma unroll
+                    for (int q = 0; q < QB; ++q)
+                        if (q0 + q < SK) {  // uniform
+#pragma unroll
+                            for (int i = 0; i < RW; ++i) {
+                                v[i][0] = q0 + q == 0 ? z[q][i][0] : v[i][0] + z[q][i][0];
+                                v[i][1] = q0 + q == 0 ? z[q][i][1] : v[i][1] + z[q][i][1];
+                            }
+                        }
+                }
+#pragma unroll
+                for (int i = 0; i < RW; ++i) {
+                    const int rr = wave + WK * i;
+                    if (rr >= R) break;  // uniform
                     const size_t at = ((size_t)m0 + rr) * N + col0 + 2 * lane;
-                    float v0 = load_coherent(Z + at), v1 = load_coherent(Z + at + 1);
-                    for (int q = 1; q < SK; ++q) {
-                        v0 += load_coherent(Z + (size_t)q * M * N + at);
-                        v1 += load_coherent(Z + (size_t)q * M * N + at + 1);
-                    }
-                    finish_store(v0, v1, lane, svh, bias, y, J.y_dtype, at, col0 + 2 * lane);
+                    finish_store(v[i][0], v[i][1], lane, svh, bias, y, J.y_dtype, at, col0 + 2 * lane);
                 }
                 if (threadIdx.x == 0) counters[pass * NB + nb] = 0;  // every split of the column block arrived
             }
