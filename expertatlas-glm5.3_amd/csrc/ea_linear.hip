@@ -435,13 +435,19 @@ __global__ void __launch_bounds__(1024) lin_small_kernel(ea_jobs jobs, ea_rot_jo
         __syncthreads();
         if (!last) return;
     }
-    // the last block of the 128-column block: the splits in order, then finish
+    // the last block of the 128-column block: the splits in order (eight loaded at once), then finish
     for (int m = wave; m < M; m += WK) {
-        float2 acc2 = ld_coh2(Z + (size_t)m * N + col);
-        for (int q = 1; q < SK; ++q) {
-            const float2 z = ld_coh2(Z + ((size_t)q * M + m) * N + col);
-            acc2.x += z.x;
-            acc2.y += z.y;
+        float2 acc2;
+        for (int q0 = 0; q0 < SK; q0 += 8) {
+            float2 z[8];
+#pragma unroll
+            for (int q = 0; q < 8; ++q) z[q] = ld_coh2(Z + ((size_t)(q0 + q < SK ? q0 + q : q0) * M + m) * N + col);
+#pragma unroll
+            for (int q = 0; q < 8; ++q)
+                if (q0 + q < SK) {
+                    acc2.x = q0 + q == 0 ? z[q].x : acc2.x + z[q].x;
+                    acc2.y = q0 + q == 0 ? z[q].y : acc2.y + z[q].y;
+                }
         }
         if (last == 2) acc2 = float2{__builtin_nanf(""), __builtin_nanf("")};  // a writer never arrived
         finish_store_pre(acc2.x, acc2.y, lane, svw, bias != nullptr, bw, dptr<void>(J.y), J.y_dtype,
