@@ -15,8 +15,9 @@ A step is one pass of the hot path over one batch of synthetic input, with every
 The default run times config 2 and then, into the same line as objects of their own, the workloads named by --legs
 (the other BASELINE configs). Every GPU leg runs before any CPU work: a leg spins up on its own work (--spin-up
 seconds of untimed calls), runs one layer outside the timed region whose output it keeps, does its W warm-up steps,
-times exactly K steps launched one by one between synchronized events (a HIP graph replay of the same steps is
-reported beside it), and reads the library's device status word afterwards. Then, on the host, the oracle recomputes
+times exactly K steps launched one by one between synchronized events (the start event queued behind a GPU sleep
+kernel that lasts while the host enqueues the K steps, so they run back to back from the first; a HIP graph replay of
+the same steps is reported beside it), and reads the library's device status word afterwards. Then, on the host, the oracle recomputes
 each kept layer (the check: max|diff| <= 2e-3 RMS(out), picks bit-exact; "parity" in the line) and the tuned CPU
 layer is timed on a bounded sample ("cpu_baseline"). The run exits 1 when a check fails or a status word is set.
 
@@ -302,15 +303,45 @@ class DecodeBench:
         return sum(int(lay.bytes[2][e]) for e in distinct) + P * I * 2 + P * D * 4
 
 
+_HOLD = {}
+HOLD_NOTE = ("; the start event is queued behind a GPU sleep kernel that covers the host's enqueueing of the K steps, "
+             "so they run back to back from the first (the first launch's host latency is not timed)")
+
+
+def hold_gpu(torch, us: float) -> float:
+    """Queue a sleep kernel of about `us` microseconds on the current stream (torch's spin kernel, calibrated once
+    against events), so that the GPU is busy while the host enqueues the launches that follow it: a timed region's
+    start event recorded after the hold then does not include the first launch's host latency (about 20 us from
+    Python, one extra microsecond a layer at 20 layers). Nothing of the measured work runs in it. Returns the hold's
+    length in microseconds (0 where torch has no spin kernel)."""
+    if not hasattr(torch.cuda, "_sleep") or us <= 0:
+        return 0.0
+    if "cyc_per_us" not in _HOLD:
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        torch.cuda._sleep(2_000_000)
+        e1.record()
+        torch.cuda.synchronize()
+        _HOLD["cyc_per_us"] = 2_000_000 / max(e0.elapsed_time(e1) * 1e3, 1.0)
+    torch.cuda._sleep(int(_HOLD["cyc_per_us"] * us))
+    return us
+
+
 def time_steps(fn, steps: int, warmup: int, torch, first: int = 0, spin=None) -> float:
     """Milliseconds a step over `steps` steps after `warmup` untimed ones, between two synchronised events; `spin()`
-    (untimed calls of the leg's own work) runs right before the warm-up, with no idle gap after it."""
+    (untimed calls of the leg's own work) runs right before the warm-up, with no idle gap after it. The start event is
+    queued behind a GPU hold as long as 1.5 times the host's enqueue time of the timed steps (measured on the warm-up
+    steps), so the steps run back to back from the first, as in a model whose host runs ahead of the GPU."""
     if spin is not None:
         spin()
+    t0 = time.perf_counter()
     for i in range(warmup):
         fn(first + i)
+    host_us = (time.perf_counter() - t0) * 1e6 / max(warmup, 1)
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    hold_gpu(torch, min(1.5 * host_us * steps + 50.0, 300000.0))
     e0.record()
     for i in range(steps):
         fn(first + warmup + i)
@@ -370,6 +401,7 @@ def time_graph(step, steps: int, warmup: int, torch, first: int = 0, spin=None) 
     graphs[0].replay()
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    hold_gpu(torch, 500.0)  # the replay's host submission behind the hold, as in time_steps
     e0.record()
     graphs[1].replay()
     e1.record()
@@ -819,10 +851,11 @@ def run_decode(args, torch, np, name: str) -> Leg:
     if args.router:
         workload += "; logits computed from x by a bf16 router weight [256, 6144] (ea_ffn_moe_decode_router)"
     config = {"workload": workload, "path": args.path,
-              "timing": "eager: the K steps launched one by one between synchronized events on the launch stream",
+              "timing": "eager: the K steps launched one by one between synchronized events on the launch stream"
+                        + HOLD_NOTE,
               "graph_us": None if graph_ms is None else round(graph_ms * 1e3, 3),
-              "graph_note": "the same K steps replayed from one HIP graph between synchronized events: the replay "
-                            "carries a fixed start-up cost (about 25 us) that 200 steps amortize and 20 do not",
+              "graph_note": "the same K steps replayed from one HIP graph between synchronized events, the replay "
+                            "behind the same kind of hold",
               "spin_up_calls": spun, "layers_resident": n_layers, "distinct_experts_per_layer": round(distinct, 2),
               "step_bytes": int(step_b), "step_flops": int(step_f), "step_roofline_us": round(t_roof_us, 3),
               "step_hbm_frac": round(t_roof_us / us, 4), "step_gbs": round(step_b / (us * 1e-6) / 1e9, 1),
@@ -903,7 +936,8 @@ def run_linear(args, torch, np) -> Leg:
     config = {"workload": "config 1: one EXL3 4-bit linear K 6144 x N 2048 at one fp16 row, fp32 out (linear.call: "
                           "one launch of the small-row kernel, rotation in the kernel)", "linears_resident": args.layers,
               "step_bytes": b, "step_roofline_us": round(t_roof, 3), "step_hbm_frac": round(t_roof / us, 4),
-              "timing": "eager: the K calls launched one by one between synchronized events on the launch stream",
+              "timing": "eager: the K calls launched one by one between synchronized events on the launch stream"
+                        + HOLD_NOTE,
               "graph_us": round(graph_ms * 1e3, 3), "spin_up_calls": spun, "device_status": status}
     roofline = {"kernel": "lin_small_kernel (the whole call: one launch)", "bound": "hbm", "achieved": round(gbs, 1),
                 "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
@@ -983,7 +1017,7 @@ def run_prefill(args, torch, np, R: int, planes: int = 1) -> Leg:
               "step_roof_frac": round(max(t_hbm, t_mfma) / us, 4), "step_gbs": round(gbs, 1),
               "step_tflops": round(tfs, 2), "mfma_frac": round(tfs / FP16_PEAK_TFLOPS, 4),
               "timing": "eager: the K layers launched one by one between synchronized events (the two item lists "
-                        "on two streams run side by side)", "graph_us": round(graph_ms * 1e3, 3),
+                        "on two streams run side by side)" + HOLD_NOTE, "graph_us": round(graph_ms * 1e3, 3),
               "graph_note": "the same layers replayed from a HIP graph: the runtime runs the side stream's branch after "
                             "the main one, not beside it", "spin_up_calls": spun, "device_status": status}
     roofline = {"kernel": "prompt_experts.run (whole call: route, rot_in, gate|up item GEMMs, epilogue, down item "
