@@ -22,6 +22,7 @@
 #include "ea_experts.hpp"
 #include "ea_gemm.hpp"
 #include "ea_host.hpp"
+#include "ea_stamps.hpp"
 
 namespace ea {
 
@@ -1405,7 +1406,9 @@ __device__ __forceinline__ bool l1_down_product(const DLArgs& a, L1Sh& sh, int u
     for (int tp = 0; tp < PRE; ++tp)
 #pragma unroll
         for (int j = 0; j < 2; ++j) hold(pb[tp][j]);  // decoded before the wait, not after it
+    EA_STAMP(2, threadIdx.x == 0);  // wave 0's pre-decode done
     const bool r = l1_down_wait(a, sh, u, tag, lane);
+    EA_STAMP(3, threadIdx.x == 0);  // the down inputs seen
     __builtin_amdgcn_s_setprio(2);  // the pre-decode ran at the lowest priority, beside the gate|up decode
     const bool row0 = (lane & 15) == 0;
     const uint16_t* xr = sh.xs + 2 * ((lane >> 4) & 3);
@@ -1489,8 +1492,10 @@ __device__ __forceinline__ void l1_gateup(const DLArgs& a, L1Sh& sh, int u, int 
     const uint32_t tag = (uint32_t)uniform((int)sh.tag);
     uint32_t* st = sh.stage[wave];
     stage_store<DL_KT>(st, k2, lane, v);
+    EA_STAMP(5, threadIdx.x == 0);  // the activations rotated, wave 0's trellis landed
     f4v acc[2] = {f4v{0.f, 0.f, 0.f, 0.f}, f4v{0.f, 0.f, 0.f, 0.f}};
     const bool ok = l1_mfma_k2<CB, DL_KT>(k2, st, lq, sh.xs, lane, acc);
+    EA_STAMP(6, threadIdx.x == 0);  // wave 0's tiles decoded and multiplied
     if (!ok) {
         if (lane == 0) record_error(a.status, DEV_UNSUPPORTED_WIDTH);
         acc[0] = acc[1] = nan4();
@@ -1551,6 +1556,7 @@ __device__ __forceinline__ void l1_epilogue(const DLArgs& a, L1Sh& sh, const Uni
         *reinterpret_cast<float2*>(&sh.ep.half[mat][2 * lane]) = float2{s0, s1};
     }
     __syncthreads();
+    EA_STAMP(3, threadIdx.x == 0);  // every wave's polls done
     if (h == 1) {
         const float2 f = *reinterpret_cast<const float2*>(&sh.ep.half[mat][2 * lane]);
         s0 = f.x;
@@ -1569,6 +1575,7 @@ __device__ __forceinline__ void l1_epilogue(const DLArgs& a, L1Sh& sh, const Uni
         const float2 g = *reinterpret_cast<const float2*>(&sh.ep.gus[0][2 * lane]);
         const float2 up = *reinterpret_cast<const float2*>(&sh.ep.gus[1][2 * lane]);
         st_tag(a.lay.txd + (size_t)u * (a.I / 2) + nh * 64 + lane, act_pair(uv, g, up, sd, lane), tag);
+        EA_STAMP(4, lane == 0);  // the down inputs stored
     }
 }
 
@@ -1617,6 +1624,7 @@ __device__ __forceinline__ void l1_down(const DLArgs& a, L1Sh& sh, const UnitVie
         acc[0] = acc[1] = nan4();
     }
     __syncthreads();  // every wave is done with its staging: the column sums take its place
+    EA_STAMP(4, threadIdx.x == 0);  // every wave's MFMAs done
     if (lane < 16) {
 #pragma unroll
         for (int j = 0; j < 2; ++j) sh.ys[(2 * wave + j) * 16 + lane] = acc[j][0];
@@ -1632,6 +1640,7 @@ __device__ __forceinline__ void l1_down(const DLArgs& a, L1Sh& sh, const UnitVie
         uint64_t* y = a.lay.ty + (size_t)u * a.D + n;
         st_tag(y, __float_as_uint(v0), tag);
         st_tag(y + 1, __float_as_uint(v1), tag);
+        EA_STAMP(5, lane == 0);  // the outputs stored
         return;
     }
     // the combine of the column block (the last unit is the last slot's): the other units' outputs, then the slots
@@ -1656,6 +1665,7 @@ __device__ __forceinline__ void l1_down(const DLArgs& a, L1Sh& sh, const UnitVie
         }
         __builtin_amdgcn_s_sleep(1);
     }
+    EA_STAMP(5, lane == 0);  // the other units' outputs seen
     // slot k is unit hs + k (U = hs + 8): slots 0..6 from the tagged slots, slot 7 this block's own
     const bool hs = a.hs;
     float a0 = 0.f, a1 = 0.f;
@@ -1672,6 +1682,7 @@ __device__ __forceinline__ void l1_down(const DLArgs& a, L1Sh& sh, const UnitVie
     }
     if (timed_out2) a0 = a1 = __builtin_nanf("");
     *reinterpret_cast<float2*>(a.out + n) = float2{a0, a1};
+    EA_STAMP(6, lane == 0);  // the column block combined
 }
 
 // Five waves a SIMD: the down items hold their whole pre-decoded product (64 VGPRs) through their wait.
@@ -1680,9 +1691,12 @@ __global__ void __launch_bounds__(DL_THREADS) __attribute__((amdgpu_waves_per_eu
     __shared__ L1Sh sh;
     const int NH = a.I / 128, KC = a.D / 256, DB = a.D / 128;
     const int GU = NH * 2 * KC;  // gate|up items a unit
+    EA_STAMP(0, threadIdx.x == 0);  // the block's start
     const uint32_t e0 = l1_epoch_load(a);
     if (blockIdx.x == 0) {
         l1_router(a, sh, e0);
+        EA_STAMP(1, threadIdx.x == 0);  // the picks published
+        EA_STAMP_VALUE(STAMP_POINTS - 1, 1, threadIdx.x == 0);
         return;
     }
     const int b = blockIdx.x - 1, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -1692,26 +1706,35 @@ __global__ void __launch_bounds__(DL_THREADS) __attribute__((amdgpu_waves_per_eu
     if (b < a.U * GU) {
         const int u = b / GU, rem = b % GU, nh = rem / (2 * KC), mat = (rem / KC) & 1, c = rem % KC;
         uv.shared = a.hs && u == 0;
+        // descriptor: 2 shared / 3 routed gate|up item, unit, column block, matrix, chunk
+        EA_STAMP_VALUE(STAMP_POINTS - 1, (uint64_t)(uv.shared ? 2 : 3) | (uint64_t)u << 8 | (uint64_t)nh << 16 |
+                                          (uint64_t)mat << 20 | (uint64_t)c << 24, threadIdx.x == 0);
         if (uv.shared) {
             uv.e = -1;
             __builtin_amdgcn_s_setprio(2);
             l1_gateup<SCB, true>(a, sh, u, nh, mat, c, e0);
         } else {
             l1_route_self(a, sh, mat, u - a.hs);
+            EA_STAMP(1, threadIdx.x == 0);  // routed up to its pick
             uv.e = uniform(sh.e);
             __builtin_amdgcn_s_setprio(2);  // the gate|up decode is on the layer's critical path
             l1_gateup<CB, false>(a, sh, u, nh, mat, c, e0);
         }
+        EA_STAMP(2, threadIdx.x == 0);  // its partial sums stored
         if (mat == 1 && c == KC - 1) l1_epilogue(a, sh, uv, u, nh);
         return;
     }
     const int d = b - a.U * GU, u = d / DB, cb = d % DB;
     uv.shared = a.hs && u == 0;
+    // descriptor: 4 down item, 5 the combining one (the last unit's), unit, output column block
+    EA_STAMP_VALUE(STAMP_POINTS - 1, (uint64_t)(u == a.U - 1 ? 5 : 4) | (uint64_t)u << 8 | (uint64_t)cb << 16,
+                threadIdx.x == 0);
     if (threadIdx.x == 0) sh.tag = l1_next(e0);
     // the last unit's block combines the column block: it takes every weight
     if (!uv.shared && wave == 0)
         l1_route_wait(a, sh, u - a.hs, 2, l1_next((uint32_t)uniform((int)e0)), u == a.U - 1, lane);  // lane 0 is thread 0
     __syncthreads();
+    EA_STAMP(1, threadIdx.x == 0);  // the router's slots seen
     uv.e = uv.shared ? -1 : uniform(sh.e);
     if (a.I == 256)
         l1_down<CB, SCB, 16>(a, sh, uv, u, cb);
@@ -1980,6 +2003,11 @@ int dl_static_setup(DevCtx& c) {
 using namespace ea;
 
 extern "C" {
+
+#ifdef EA_STAMPS
+// The timeline build only: the stamp region of the decode layer kernels (ea_stamps.hpp).
+int ea_stamps_attach_layer(void* region) { return stamp_attach(region); }
+#endif
 
 int ea_ffn_moe_decode_static(ea_stream_t stream, const void* x, int x_dtype, uint32_t x_stride, const float* logits,
                              const float* bias, float scale, int32_t* pick, float* wts, const ea_routed* ex,

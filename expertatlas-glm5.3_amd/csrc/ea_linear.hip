@@ -7,6 +7,7 @@
 #include "ea_device.hpp"
 #include "ea_gemm.hpp"
 #include "ea_host.hpp"
+#include "ea_stamps.hpp"
 
 namespace ea {
 
@@ -196,6 +197,7 @@ __global__ void __launch_bounds__(1024) lin_small_kernel(ea_jobs jobs, ea_rot_jo
                                                         int x_bf16, int* status) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     constexpr int TW = 4 * K2;
+    EA_STAMP(0, threadIdx.x == 0);  // the block's start
     int ji = 0;
 #pragma unroll
     for (int q = 1; q < EA_MAX_JOBS; ++q)
@@ -245,6 +247,9 @@ __global__ void __launch_bounds__(1024) lin_small_kernel(ea_jobs jobs, ea_rot_jo
     // the svh and bias of the lane's two columns of the 128-column block, for whichever block finishes it (loaded by
     // every block, unconditionally: a load in a branch would make the compiler wait for all loads before the first use)
     const bool finisher = (g & 3) == 3 && split == SK - 1;  // the highest-index block of the 4 SK
+    // descriptor: 1 a block that hands its sums on, 2 the finisher; column group, split
+    EA_STAMP_VALUE(STAMP_POINTS - 1, (uint64_t)(finisher ? 2 : 1) | (uint64_t)g << 8 | (uint64_t)split << 20,
+                   threadIdx.x == 0);
     const int col = (g >> 2) * 128 + 2 * lane;
     const uint16_t* svh = dptr<const uint16_t>(J.svh);
     const uint16_t* bias = dptr<const uint16_t>(J.bias);
@@ -257,6 +262,7 @@ __global__ void __launch_bounds__(1024) lin_small_kernel(ea_jobs jobs, ea_rot_jo
     // the trellis into the wave's LDS region (it waits only for the trellis loads), then every tile decoded into its
     // MFMA operand
     stage_store_k<NKT, K2>(st, lane, v);
+    EA_STAMP(1, threadIdx.x == 0);  // wave 0's trellis landed
     const LaneQuad lq = lane_quad_k<K2>(lane);
     u4v bq[NKT / 2][2];
     {
@@ -276,6 +282,7 @@ __global__ void __launch_bounds__(1024) lin_small_kernel(ea_jobs jobs, ea_rot_jo
     for (int t = 0; t < NKT / 2; ++t)
 #pragma unroll
         for (int j = 0; j < 2; ++j) hold(bq[t][j]);  // decoded before the activations are waited for
+    EA_STAMP(2, threadIdx.x == 0);  // wave 0's tiles decoded
 #pragma unroll
     for (int i = 0; i < XL; ++i) {
         const int c = i * NT + (int)threadIdx.x;
@@ -286,6 +293,7 @@ __global__ void __launch_bounds__(1024) lin_small_kernel(ea_jobs jobs, ea_rot_jo
     }
     if (ROT && (int)threadIdx.x < cpr) *reinterpret_cast<u4v*>(suh_s + 8 * threadIdx.x) = sv;
     __syncthreads();
+    EA_STAMP(3, threadIdx.x == 0);  // the activations in LDS, every wave's tiles decoded
     if constexpr (ROT) {
         // rotate in place: a wave a (row, Hadamard block), two values a lane (exl3_linear.cu:152-173)
         uint16_t* xh = dptr<uint16_t>(rj.xh[ji]);
@@ -303,6 +311,7 @@ __global__ void __launch_bounds__(1024) lin_small_kernel(ea_jobs jobs, ea_rot_jo
             if (g == 0 && xh) *reinterpret_cast<uint32_t*>(xh + (size_t)m * K + (hb0 + hb) * 128 + 2 * lane) = h;
         }
         __syncthreads();
+        EA_STAMP(4, threadIdx.x == 0);  // rotated
     }
 
     // the product: A rows are the activation rows (zero past M), B the decoded tiles
@@ -317,6 +326,7 @@ __global__ void __launch_bounds__(1024) lin_small_kernel(ea_jobs jobs, ea_rot_jo
             acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, __builtin_bit_cast(h8v, bq[t >> 1][j]), acc[j], 0, 0, 0);
     }
     __syncthreads();  // every wave is done with the staged trellis: the wave sums take its place
+    EA_STAMP(5, threadIdx.x == 0);  // every wave's MFMAs done
 #pragma unroll
     for (int j = 0; j < 2; ++j)
 #pragma unroll
@@ -336,6 +346,7 @@ __global__ void __launch_bounds__(1024) lin_small_kernel(ea_jobs jobs, ea_rot_jo
                                    ((uint64_t)LS_TAG << 32) | __float_as_uint(sum), __ATOMIC_RELAXED,
                                    __HIP_MEMORY_SCOPE_AGENT);
         }
+        EA_STAMP(6, threadIdx.x == 0);  // thread 0's sums stored (the finisher: kept)
         if (!finisher) return;
         __syncthreads();
         // the finisher: a wave a row, two columns a lane; its own split's slots of its own 32 columns (lanes 48..63)
@@ -362,6 +373,7 @@ __global__ void __launch_bounds__(1024) lin_small_kernel(ea_jobs jobs, ea_rot_jo
                 }
                 __builtin_amdgcn_s_sleep(1);
             }
+            EA_STAMP(7, threadIdx.x == 0);  // wave 0's polls done
             if (own) {
                 const int c = 2 * lane - 96;
                 p[SK - 1][0] = __float_as_uint(red[m * 32 + c]);
@@ -388,6 +400,7 @@ __global__ void __launch_bounds__(1024) lin_small_kernel(ea_jobs jobs, ea_rot_jo
             finish_store_pre(acc2.x, acc2.y, lane, svw, bias != nullptr, bw, dptr<void>(J.y), J.y_dtype,
                              (size_t)m * N + col);
         }
+        EA_STAMP(8, threadIdx.x == 0);  // wave 0's rows finished
         return;
     }
     float* Z = dptr<float>(J.Z);
@@ -620,6 +633,11 @@ int launch_linear(hipStream_t s, const ea_jobs* jobs_in, uint32_t m, uint32_t kd
 using namespace ea;
 
 extern "C" {
+
+#ifdef EA_STAMPS
+// The timeline build only: the stamp region of the linear kernels (ea_stamps.hpp).
+int ea_stamps_attach_linear(void* region) { return stamp_attach(region); }
+#endif
 
 int ea_exl3_rot_in(ea_stream_t stream, const void* x, int x_dtype, const ea_rot_jobs* jobs, uint32_t njobs,
                    uint32_t m, uint32_t kdim) {
