@@ -209,7 +209,8 @@ def _routed_case(ea, R, E, D, I, k2, x_dtype, seed):
     return got, want
 
 
-@pytest.mark.parametrize("R,x_dtype", [(1, 0), (4, 1), (16, 0)])
+# fp32 activations (x_dtype 2) take the six-launch sequence (the decode layer reads 16-bit rows only)
+@pytest.mark.parametrize("R,x_dtype", [(1, 0), (4, 1), (16, 0), (4, 2), (16, 2)])
 def test_moe_routed_reduced_width(ea, R, x_dtype):
     got, want = _routed_case(ea, R, 64, 1024, 256, 8, x_dtype, 30 + R)
     assert_close_rms(got, want, 2e-3, "moe.routed")

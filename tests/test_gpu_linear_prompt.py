@@ -199,6 +199,23 @@ def test_prompt_experts_full_shape_512(ea, planes):
     assert_close_rms(device.download(out), want, 2e-3, "prompt experts R=512")
 
 
+@pytest.mark.parametrize("planes", [True, False])
+def test_prompt_experts_f32_activations(ea, planes):
+    """fp32 activations (x_dtype 2: the rotation launch reads them and rounds the rotated rows to fp16 as for 16-bit
+    ones), with the pair plane and without it, against the oracle on the same fp32 rows."""
+    device, _, _, pe, synth = ea
+    R, E, D, I = 96, 32, 512, 256
+    host, ex, sc, x, pick, wts, dx, dp, dw = _prompt_case(ea, R, E, D, I, 8, 700 + int(planes), x_dtype=2,
+                                                          planes=planes)
+    assert x.dtype == np.float32
+    want = orc.prompt_experts(x, pick, wts, oracle_routed(host), R, 8)
+    out = device.zeros((R, D), torch.float32)
+    pe.run(device.stream(), dx.data_ptr(), D, dp.data_ptr(), dw.data_ptr(), ex, sc, out.data_ptr(), R,
+           do_round=False, x_dtype=2)
+    assert_close_rms(device.download(out), want, 2e-3, f"prompt experts, fp32 x, planes={planes}")
+    assert device.device_status() == 0
+
+
 @pytest.mark.parametrize("cb,I", [(0, 256), (2, 256), (2, 128), (0, 128)])
 def test_prompt_experts_codebooks(ea, cb, I):
     """3inst and mul1 through both item lists (the small items' ring kernel and the larger items' kernel), both
