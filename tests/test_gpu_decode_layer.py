@@ -114,6 +114,13 @@ def test_ffn_decode_mixed_widths(ea):
     _case(ea, [16], 6144, 256, synth.mixed_widths(301, 256), 1, 8, 1, 0, 300)
 
 
+@pytest.mark.parametrize("k2", [2, 3, 4, 5, 7, 9])
+def test_ffn_decode_every_width(ea, k2):
+    """The widths the tests above leave out (K2 6, 8 and 10 are theirs), for the routed experts and the shared expert
+    alike: one row (the one-launch layer), then four (the multi-row launches), mcg codebook, D 1024."""
+    _case(ea, [1, 4], 1024, 256, k2, 1, k2, 1, 0, 700 + k2)
+
+
 def test_ffn_decode_routed_only_i128(ea):
     """No shared expert, I = 128 (a TP=16 shard), mul1 routed experts."""
     _case(ea, [5, 2], 2048, 128, 10, 2, None, None, 0, 400)

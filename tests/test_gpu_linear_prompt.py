@@ -199,6 +199,20 @@ def test_prompt_experts_full_shape_512(ea, planes):
     assert_close_rms(device.download(out), want, 2e-3, "prompt experts R=512")
 
 
+@pytest.mark.parametrize("k2", [2, 3, 4, 5, 7, 9, 10])
+def test_prompt_experts_every_staged_width(ea, k2):
+    """The staged item GEMMs' widths the tests above leave out (K2 6 and 8 are theirs), through both item lists (Zipf
+    over 32 experts at 160 rows gives items of both sizes), with the pair plane."""
+    device, _, _, pe, synth = ea
+    R, E, D, I = 160, 32, 512, 256
+    host, ex, sc, x, pick, wts, dx, dp, dw = _prompt_case(ea, R, E, D, I, k2, 900 + k2)
+    want = orc.prompt_experts(x, pick, wts, oracle_routed(host), R, 8, bf16=True)
+    out = device.zeros((R, D), torch.float32)
+    pe.run(device.stream(), dx.data_ptr(), D, dp.data_ptr(), dw.data_ptr(), ex, sc, out.data_ptr(), R, do_round=False)
+    assert_close_rms(device.download(out), want, 2e-3, f"prompt experts, K2 {k2}")
+    assert device.device_status() == 0
+
+
 @pytest.mark.parametrize("planes", [True, False])
 def test_prompt_experts_f32_activations(ea, planes):
     """fp32 activations (x_dtype 2: the rotation launch reads them and rounds the rotated rows to fp16 as for 16-bit
