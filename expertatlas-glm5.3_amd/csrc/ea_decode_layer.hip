@@ -1914,7 +1914,7 @@ int decode_layer(hipStream_t s, const void* x, int x_dtype, uint32_t x_stride, c
         if (x_stride < D || x_stride % 4 != 0) return EA_BAD_ROW_STRIDE;
         if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(router_w)) & 7) return EA_BAD_ARGUMENT;
     }
-    int scb = (int)ex->cb;
+    int scb = ex->cb == 0 ? 1 : (int)ex->cb;  // without a shared expert any built pairing (its codebook is unused)
     DLArgs a{};
     if (shared) {
         const ea_linear *g = shared[0], *u = shared[1], *d = shared[2];
@@ -1965,6 +1965,10 @@ int decode_layer(hipStream_t s, const void* x, int x_dtype, uint32_t x_stride, c
     if (rcb == 1 && scb == 2) return dl_launch<1, 2>(s, a, c->cus, c->device);
     if (rcb == 2 && scb == 2) return dl_launch<2, 2>(s, a, c->cus, c->device);
     if (rcb == 2 && scb == 1) return dl_launch<2, 1>(s, a, c->cus, c->device);
+    // routed 3inst experts (the reference's grouped kernel takes every codebook, exl3_experts.cu:306-309) beside a
+    // shared expert in one of the codebooks its linear takes (mcg, mul1)
+    if (rcb == 0 && scb == 1) return dl_launch<0, 1>(s, a, c->cus, c->device);
+    if (rcb == 0 && scb == 2) return dl_launch<0, 2>(s, a, c->cus, c->device);
     return EA_UNPORTED_GROUPED_VARIANT;
 }
 

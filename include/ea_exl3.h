@@ -162,7 +162,7 @@ int ea_moe_scratch_init(ea_stream_t stream, ea_moe_scratch* s, void* base, size_
 
 /* out fp32 [R, D] = the R rows' routed experts weighted by wts. Replaces moe.routed (moe.zig:279-293).
  * x: [R, D] rows x_stride apart; pick int32 / wts fp32 [R, slots]. With a scratch of at most 16 rows, widths
- * 2..10, mcg or mul1 and I of 128 or 256, the decode layer's launches (three at one row, five above); with a scratch
+ * 2..10, fp16 or bf16 x and I of 128 or 256, the decode layer's launches (one at one row, five above); with a scratch
  * of 17..128 rows (the reference's decode windows, forward.zig:21), the prefill path's item GEMMs in the scratch's
  * prompt region, the slots added in order (the same bits every run; every pair of a window computed); otherwise the
  * six-launch sequence of moe.zig:279-293. On the decode layer and the sequence, as the reference groups pairs
@@ -279,15 +279,15 @@ int ea_add_f32(ea_stream_t stream, float* a, const float* b, size_t n);
 
 /* ---- the decode layer in one call --------------------------------------------------------------------------- */
 
-/* ffnMain's expert part for a decode window in one call (three launches at one row, five above): pick / wts
+/* ffnMain's expert part for a decode window in one call (one launch at one row, five above): pick / wts
  * [R, 8] = top-8 of logits [R, 256] (as
  * ea_topk8, written out), out [R, D] = moe.routed(x) + the shared expert's mlp(x) (gate and up EXL3 linears with
  * bf16 outputs, swiglu2, the down linear with fp32 output), or the routed part alone when shared is NULL.
  * Replaces the sequence ops.topk -> moe.routed -> forward.mlp -> glue.addF32 of forward.zig:2361-2403 (the
  * reference's decode graph issues those as separate launches). shared: gate, up, down ea_linear (k, n = D, I / I, D;
- * one width in 2..10 and one codebook among the three). Needs s from ea_moe_scratch_init with rows <= 16, R <= rows,
- * E = 256, slots = 8, I of 128 or 256, routed widths 2..10, codebooks mcg / mul1; EA_UNPORTED_GROUPED_VARIANT
- * otherwise. Concurrent calls sharing one scratch race. */
+ * one width in 2..10 and one codebook, mcg or mul1: the codebooks the reference's linear takes). Needs s from
+ * ea_moe_scratch_init with rows <= 16, R <= rows, E = 256, slots = 8, I of 128 or 256, routed widths 2..10, routed
+ * codebook 3inst, mcg or mul1; EA_UNPORTED_GROUPED_VARIANT otherwise. Concurrent calls sharing one scratch race. */
 int ea_ffn_moe_decode(ea_stream_t stream, const void* x, int x_dtype, uint32_t x_stride, const float* logits,
                       const float* bias, float scale, int32_t* pick, float* wts, const ea_routed* ex,
                       const ea_linear* const* shared, const ea_moe_scratch* s, float* out, uint32_t R);

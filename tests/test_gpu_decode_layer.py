@@ -121,6 +121,13 @@ def test_ffn_decode_every_width(ea, k2):
     _case(ea, [1, 4], 1024, 256, k2, 1, k2, 1, 0, 700 + k2)
 
 
+@pytest.mark.parametrize("shared_cb", [1, 2])
+def test_ffn_decode_3inst_routed(ea, shared_cb):
+    """3inst routed experts (the reference's grouped kernel takes every codebook) beside an mcg or a mul1 shared
+    expert (the codebooks its linear takes), one row and then three."""
+    _case(ea, [1, 3], 2048, 256, 8, 0, 8, shared_cb, 0, 800 + shared_cb)
+
+
 def test_ffn_decode_routed_only_i128(ea):
     """No shared expert, I = 128 (a TP=16 shard), mul1 routed experts."""
     _case(ea, [5, 2], 2048, 128, 10, 2, None, None, 0, 400)

@@ -216,6 +216,25 @@ def test_moe_routed_reduced_width(ea, R, x_dtype):
     assert_close_rms(got, want, 2e-3, "moe.routed")
 
 
+@pytest.mark.parametrize("R", [1, 12])
+def test_moe_routed_3inst(ea, R):
+    """3inst routed experts through moe.routed on a scratch of at most 16 rows (the decode layer's launches)."""
+    device, experts, moe, _, synth = ea
+    slots, E, D, I = 8, 64, 1024, 256
+    pick = synth.picks_uniform(70 + R, R, E, slots)
+    wts = synth.routing_weights(71 + R, R, slots)
+    host = synth.HostLayer(72 + R, experts=E, dims=D, width=I, k2=8, cb=0, only=np.unique(pick))
+    x = synth.activations(73 + R, R, D, "f16")
+    want = orc.moe_routed(x, pick, wts, oracle_routed(host), R, slots)
+    ex = moe.Routed(host)
+    sc = moe.Scratch(ex, R, slots)
+    dx, dp, dw = device.upload(x), device.upload(pick), device.upload(wts)
+    out = device.zeros((R, D), torch.float32)
+    moe.routed(device.stream(), dx.data_ptr(), D, dp.data_ptr(), dw.data_ptr(), ex, sc, out.data_ptr(), R, x_dtype=0)
+    assert_close_rms(device.download(out), want, 2e-3, f"moe.routed 3inst R={R}")
+    assert device.device_status() == 0
+
+
 def test_moe_routed_full_shape_r1(ea):
     """BASELINE config 2's routed part at its real shape: D 6144, I 256, 256 experts, 4 bits, batch 1."""
     got, want = _routed_case(ea, 1, 256, 6144, 256, 8, 0, 40)

@@ -51,6 +51,8 @@ def test_unpack_bit_exact(ea, k2, cb):
     (4, 6144, 2048, 8, 1, 2),    # config 1's shape at four rows (the small-row kernel: 32-column groups x 8 splits)
     (7, 2048, 512, 6, 1, 0),     # 3 bits, fp16 out, a ragged row count
     (2, 1024, 384, 4, 1, 2),     # 2 bits
+    (3, 2048, 512, 12, 2, 2),    # 6-bit mul1 (widths above 10: the register-streaming kernel at any row count)
+    (5, 1024, 384, 8, 2, 1),     # 4-bit mul1, bf16 out
 ])
 def test_linear_call(ea, M, K, N, k2, cb, y_dtype):
     device, linear, _, _, synth = ea
