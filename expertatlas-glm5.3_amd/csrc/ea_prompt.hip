@@ -717,8 +717,7 @@ __device__ __forceinline__ void dn_loop(const TileSpan& sp, const uint16_t* xa, 
     constexpr int NL = stage_loads_k<PK, K2>();
     constexpr int TWB = 16 * K2;
     const LaneQuad lq = lane_quad_k<K2>(lane);
-    const int steps = NG * nch;
-    static_assert(NG % 2 == 0, "two steps an iteration");
+    const int steps = NG * nch;  // even (NG even, or nch = 2: the caller's choice): two steps an iteration
     u4v ta[NL], tb[NL];
     f4v acc[MT][2];
     uint32_t sv[4];  // ATOM: svh_d of this thread's epilogue columns, loaded at a column block's first chunk
@@ -763,9 +762,11 @@ __device__ __forceinline__ void dn_loop(const TileSpan& sp, const uint16_t* xa, 
 }
 
 // The down matrix (K = I of 128 or 256: one or two chunks): a block (item of list MT > 2, NG column blocks of 128)
-// loads the item's activations for all of K into LDS once, then its waves run the column blocks independently.
-template <int CB, int MT, int NG, bool ATOM>
-__global__ void __launch_bounds__(PW * 64) __attribute__((amdgpu_waves_per_eu(MT > 2 ? 2 : 4)))
+// loads the item's activations for all of K into LDS once, then its waves run the column blocks independently. WB = 8
+// (the larger items with a pair plane): two groups of four waves, each over NG / 2 of the column blocks, share one copy
+// of the activations, so two blocks fit a CU's LDS at four waves a SIMD (four-wave blocks: three at three).
+template <int CB, int MT, int NG, bool ATOM, int WB = PW>
+__global__ void __launch_bounds__(WB * 64) __attribute__((amdgpu_waves_per_eu(MT > 2 && WB == PW ? 2 : 4)))
 item_dn_kernel(const uint16_t* __restrict__ X, const int64_t* __restrict__ TP, const int* __restrict__ K2T,
                const int* __restrict__ sorted, const int* __restrict__ items, const int* __restrict__ item_count,
                float* __restrict__ Z, int K, int N, int P, int max_items, int* __restrict__ status,
@@ -786,7 +787,8 @@ item_dn_kernel(const uint16_t* __restrict__ X, const int64_t* __restrict__ TP, c
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     __shared__ int pair_sh[MT * 16];
     __shared__ __attribute__((aligned(16))) uint16_t xa[MT * 16 * DXS];
-    __shared__ __attribute__((aligned(16))) uint32_t st[PW][PSTAGE];
+    static_assert(WB == PW || (WB == 2 * PW && !ATOM && NG % 2 == 0), "two wave groups: pair-plane blocks");
+    __shared__ __attribute__((aligned(16))) uint32_t st[WB][PSTAGE];
     constexpr int EWORDS = ATOM ? 2 * 16 * ES : 1;
     constexpr int WWORDS = ATOM ? MT * 16 : 1;
     __shared__ float ebuf[EWORDS];
@@ -800,41 +802,47 @@ item_dn_kernel(const uint16_t* __restrict__ X, const int64_t* __restrict__ TP, c
     DnAtomic at{};
     if constexpr (ATOM) at = DnAtomic{out, svh_d + (size_t)e * N, pair_sh, wts_sh, ebuf, N, slots, half};
     {
+        // 256 threads cover a chunk of a row tile; with eight waves each half of the block loads one chunk
+        constexpr int CPT = WB == PW ? 2 : 1;  // chunks a thread loads
+        const int lt = tid & 255, c0 = WB == PW ? 0 : tid >> 8;
         const __amdgpu_buffer_rsrc_t xrs = buffer_rsrc(X, (uint32_t)((size_t)P * K * 2));
-        u4v av[2][MT];
+        u4v av[CPT][MT];
 #pragma unroll
-        for (int c = 0; c < 2; ++c)
+        for (int q = 0; q < CPT; ++q)
 #pragma unroll
             for (int i = 0; i < MT; ++i) {
-                const int rr = i < mts ? i * 16 + (tid >> 4) : (tid >> 4);
+                const int rr = i < mts ? i * 16 + (lt >> 4) : (lt >> 4);
                 const int p = pair_sh[rr] >= 0 ? pair_sh[rr] : pair_sh[0];
-                const int cc = c < nch ? c : 0;
-                av[c][i] = __builtin_bit_cast(
+                const int cc = c0 + q < nch ? c0 + q : 0;
+                av[q][i] = __builtin_bit_cast(
                     u4v, __builtin_amdgcn_raw_buffer_load_b128(
-                             xrs, ((uint32_t)p * (uint32_t)K + (uint32_t)(cc * PK * 16 + 8 * (tid & 15))) * 2u, 0, 0));
+                             xrs, ((uint32_t)p * (uint32_t)K + (uint32_t)(cc * PK * 16 + 8 * (lt & 15))) * 2u, 0, 0));
             }
 #pragma unroll
-        for (int c = 0; c < 2; ++c)
+        for (int q = 0; q < CPT; ++q)
 #pragma unroll
             for (int i = 0; i < MT; ++i)
-                if (c < nch && i < mts) put_a(xa + (i * 16 + (tid >> 4)) * DXS + c * PK * 16, tid & 15, av[c][i]);
+                if (c0 + q < nch && i < mts)
+                    put_a(xa + (i * 16 + (lt >> 4)) * DXS + (c0 + q) * PK * 16, lt & 15, av[q][i]);
     }
+    constexpr int NGW = WB == PW ? NG : NG / 2;  // column blocks a wave group runs
     const int ns = N >> 4, TWB = 16 * k2;
-    const int nb0 = grp * NG;  // first column block
+    const int w4 = wave & (PW - 1);
+    const int nb0 = grp * NG + (wave / PW) * NGW;  // the wave group's first column block
     TileSpan sp;
     sp.r = buffer_rsrc(T, (uint32_t)((K >> 4) * ns * TWB));
-    sp.off = (nb0 * 8 + 2 * wave) * TWB;
+    sp.off = (nb0 * 8 + 2 * w4) * TWB;
     sp.kstride = ns * TWB;
     __syncthreads();  // the activations are in LDS
     const bool ok = EA_K2_SWITCH(
-        k2, 2, 10, (dn_loop<CB, K2V, MT, NG, ATOM>(sp, xa, st[wave], lane, wave, mts, nch, nb0, pair_sh, Z, N, at)));
+        k2, 2, 10, (dn_loop<CB, K2V, MT, NGW, ATOM>(sp, xa, st[wave], lane, w4, mts, nch, nb0, pair_sh, Z, N, at)));
     if (!ok) {  // no product ran: the item's outputs of the block's column blocks are NaN
         if (lane == 0) record_error(status, DEV_UNSUPPORTED_WIDTH);
-        for (int g = 0; g < NG; ++g)
+        for (int g = 0; g < NGW; ++g)
             for (int i = 0; i < MT * 16; ++i) {
                 const int p = pair_sh[i];
                 if (p < 0) continue;
-                const size_t o = (size_t)(nb0 + g) * 128 + wave * 32 + (lane & 31);
+                const size_t o = (size_t)(nb0 + g) * 128 + w4 * 32 + (lane & 31);
                 if (!ATOM) Z[(size_t)p * N + o] = __builtin_nanf("");
                 else if (!half) static_cast<float*>(out)[(size_t)(p / slots) * N + o] = __builtin_nanf("");
                 else static_cast<uint16_t*>(out)[(size_t)(p / slots) * N + o] = 0x7E00;
@@ -1035,7 +1043,13 @@ static int list_pass(hipStream_t q, const ListPass& a, int big) {
                 d.svh_d, d.out, d.slots, d.half);
     } else if (a.I <= 2 * PK * 16 && (a.D / 128) % DNG == 0) {
         if (big && a.rows > LONG_ROWS && (a.D / 128) % DNG_BIG_LONG == 0)
-            item_dn_kernel<CB, IPM_TILES, DNG_BIG_LONG, false><<<xcd_blocks(a.mi, 1, a.D / 128 / DNG_BIG_LONG), PW * 64, 0, q>>>(
+            item_dn_kernel<CB, IPM_TILES, DNG_BIG_LONG, false, 2 * PW>
+                <<<xcd_blocks(a.mi, 1, a.D / 128 / DNG_BIG_LONG), 2 * PW * 64, 0, q>>>(
+                a.xd, a.tp[2], a.k2[2], a.sorted, a.items, a.count, a.plane, a.I, a.D, a.P, a.mi, a.status, nullptr,
+                nullptr, nullptr, 0, 0);
+        else if (big && a.I == 2 * PK * 16)  // two chunks of K: a wave group's one column block is an even step count
+            item_dn_kernel<CB, IPM_TILES, DNG_BIG, false, 2 * PW>
+                <<<xcd_blocks(a.mi, 1, a.D / 128 / DNG_BIG), 2 * PW * 64, 0, q>>>(
                 a.xd, a.tp[2], a.k2[2], a.sorted, a.items, a.count, a.plane, a.I, a.D, a.P, a.mi, a.status, nullptr,
                 nullptr, nullptr, 0, 0);
         else if (big)
