@@ -7,6 +7,7 @@ build's encoder (ea_exl3/encode.py, pinned to the oracle's decode on the CPU). O
     2e-3 RMS of the oracle's fp32-accumulated decode path;
   - the prefill path (prompt_experts.run) over 64 rows whose top-8 of 8 experts picks them all (items of 48 and 16
     pairs), and over 128 rows at config 4's full shape with Zipf routing: within 2e-3 RMS of the oracle;
+  - the EXL3 linear over config 1's K = 6144 at 1, 4 and 40 rows: within 1e-4 RMS of the oracle;
   - both within the quantization's distance (relative RMS < 0.3) of the same layer computed in fp64 from the
     unquantized bf16 weights: the format carries realistic weights through the whole path."""
 import numpy as np
@@ -199,3 +200,31 @@ def test_prefill_on_quantized_weights(ea, weights):
             dense[r] += float(wts[r, k]) * _dense_expert(xf[r:r + 1], weights[int(pick[r, k])])[0]
     rel = np.sqrt(np.mean((got.astype(np.float64) - dense) ** 2)) / np.sqrt(np.mean(dense ** 2))
     assert rel < 0.3, rel
+
+
+@pytest.mark.parametrize("M", [1, 4, 40])
+def test_linear_full_k_on_quantized_weights(ea, full_weights, M):
+    """linear.call (the small-row kernel up to 16 rows, the split-K kernel above) over config 1's K = 6144 on an
+    encoded realistic gate matrix [6144, 256]: the rotated rows bit for bit and y within 1e-4 RMS of the oracle (the
+    bar of the linear's other tests), and within the beam-2 bound of x @ W on the unquantized weights."""
+    device, encode, linear, moe, pe, synth = ea
+    W, T, suh, svh = full_weights[0][0]
+    K, N = DF, IF
+    lin = linear.Linear(T, suh, svh, K, N, K2, CB)
+    x = synth.activations(2500 + M, M, K, "f16")
+    xh_w = orc.exl3_rot_in(x, suh, M, K)
+    tw = 4 * K2
+    y_w = orc.exl3_linear(xh_w, linear.strips(T, K, N, K2), 8 * tw, (K // 16) * 8 * tw, svh, M, K, N, K2, CB, lin.sk,
+                          lin.wk, y_dtype=2)
+    sc = linear.Scratch(M, K, lin.sk * M * N)
+    dx = device.upload(x)
+    y = device.zeros((M, N), torch.float32)
+    linear.call(device.stream(), sc, [lin], dx.data_ptr(), 0, M, [y.data_ptr()], [2])
+    np.testing.assert_array_equal(device.download(sc.xh[0][: M * K].view(torch.int16)).reshape(M, K), xh_w)
+    got = device.download(y)
+    assert_close_rms(got, y_w, 1e-4, f"linear M={M} on quantized weights")
+    assert int(device.download(lin.counters).sum()) == 0
+    assert device.device_status() == 0
+    dense = x.view(np.float16).astype(np.float64) @ W.astype(np.float64)
+    rel = np.sqrt(np.mean((got.astype(np.float64) - dense) ** 2)) / np.sqrt(np.mean(dense ** 2))
+    assert rel < 0.45, rel
