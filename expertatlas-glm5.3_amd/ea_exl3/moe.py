@@ -88,9 +88,8 @@ def routed(stream: int, x: int, x_stride: int, pick: int, wts: int, ex: Routed, 
 def ffn_decode(stream: int, x: int, x_stride: int, logits: int, bias: int, scale: float, pick: int, wts: int,
                ex: Routed, shared, s: Scratch, out: int, R: int, x_dtype: int = 1) -> None:
     """ffnMain's expert part in one call (forward.zig:2361-2403; one launch at one row, five above): top-8 of logits
-    into pick / wts, then out fp32
-    [R, D] = moe.routed(x) + the shared expert's mlp(x). shared: (gate, up, down) ctypes ea_linear structs, or None
-    for the routed part alone."""
+    into pick / wts, then out fp32 [R, D] = moe.routed(x) + the shared expert's mlp(x). shared: (gate, up, down)
+    ctypes ea_linear structs, or None for the routed part alone."""
     arr = None
     if shared is not None:
         from ._lib import Linear as _Linear
