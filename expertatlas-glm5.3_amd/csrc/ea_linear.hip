@@ -231,19 +231,30 @@ __global__ void __launch_bounds__(1024) lin_small_kernel(ea_jobs jobs, ea_rot_jo
     stage_issue_k<NKT, K2>(sp, lane, v);
 
     // then the activation rows (and suh), 16 bytes a load, every load issued (a thread past the end reads the last
-    // chunk again)
+    // chunk again). XL = 0 (rotating, and no more (row, Hadamard block) items than waves): wave w loads item w's two
+    // values a lane and their suh itself, rotates them in registers while the other waves decode, and only the barrier
+    // before the products is left (the block-level form stages the rows, waits, rotates, waits again)
+    constexpr bool PWR = ROT && XL == 0;
     const uint16_t* xsrc = ROT ? static_cast<const uint16_t*>(x) : dptr<const uint16_t>(J.xh);
     const int cpr = span >> 3, chunks = M * cpr;  // 16-byte chunks a row, in all
-    u4v xv[XL];
-#pragma unroll
-    for (int i = 0; i < XL; ++i) {
-        const int c = min(i * NT + (int)threadIdx.x, chunks - 1), m = c / cpr, cc = c - m * cpr;
-        xv[i] = *reinterpret_cast<const u4v*>(xsrc + (size_t)m * K + k_first + 8 * cc);
-    }
+    const int nhb = span >> 7;
+    u4v xv[XL > 0 ? XL : 1];
     u4v sv = u4v{0u, 0u, 0u, 0u};
-    if constexpr (ROT)
-        sv = *reinterpret_cast<const u4v*>(dptr<const uint16_t>(rj.suh[ji]) + k_first +
-                                           8 * min((int)threadIdx.x, cpr - 1));
+    uint32_t rxw = 0u, rsw = 0u;
+    if constexpr (PWR) {
+        const int it = wave < M * nhb ? wave : 0, m = it / nhb, hb = it - m * nhb;  // past the items: item 0 again
+        rxw = *reinterpret_cast<const uint32_t*>(xsrc + (size_t)m * K + k_first + hb * 128 + 2 * lane);
+        rsw = *reinterpret_cast<const uint32_t*>(dptr<const uint16_t>(rj.suh[ji]) + k_first + hb * 128 + 2 * lane);
+    } else {
+#pragma unroll
+        for (int i = 0; i < XL; ++i) {
+            const int c = min(i * NT + (int)threadIdx.x, chunks - 1), m = c / cpr, cc = c - m * cpr;
+            xv[i] = *reinterpret_cast<const u4v*>(xsrc + (size_t)m * K + k_first + 8 * cc);
+        }
+        if constexpr (ROT)
+            sv = *reinterpret_cast<const u4v*>(dptr<const uint16_t>(rj.suh[ji]) + k_first +
+                                               8 * min((int)threadIdx.x, cpr - 1));
+    }
     // the svh and bias of the lane's two columns of the 128-column block, for whichever block finishes it (loaded by
     // every block, unconditionally: a load in a branch would make the compiler wait for all loads before the first use)
     const bool finisher = (g & 3) == 3 && split == SK - 1;  // the highest-index block of the 4 SK
@@ -259,6 +270,22 @@ __global__ void __launch_bounds__(1024) lin_small_kernel(ea_jobs jobs, ea_rot_jo
 #pragma unroll
     for (int i = 0; i < XL; ++i) hold(xv[i]);
     hold(sv);
+    hold(rxw);
+    hold(rsw);
+    if constexpr (PWR) {
+        // this wave's item, rotated into the staged rows (exl3_linear.cu:152-173 per (row, Hadamard block))
+        if (wave < M * nhb) {
+            const int m = wave / nhb, hb = wave - m * nhb;
+            const uint16_t x0 = (uint16_t)(rxw & 0xffffu), x1 = (uint16_t)(rxw >> 16);
+            float v0 = (x_bf16 ? bf2f(x0) : h2f(x0)) * h2f((uint16_t)(rsw & 0xffffu));
+            float v1 = (x_bf16 ? bf2f(x1) : h2f(x1)) * h2f((uint16_t)(rsw >> 16));
+            fwht128_w64(v0, v1, lane);
+            const uint32_t h = (uint32_t)f2h(v0 * HAD_SCALE) | ((uint32_t)f2h(v1 * HAD_SCALE) << 16);
+            *reinterpret_cast<uint32_t*>(xs + m * XS + hb * 128 + 2 * lane) = h;
+            uint16_t* xh = dptr<uint16_t>(rj.xh[ji]);
+            if (g == 0 && xh) *reinterpret_cast<uint32_t*>(xh + (size_t)m * K + (hb0 + hb) * 128 + 2 * lane) = h;
+        }
+    }
     // the trellis into the wave's LDS region (it waits only for the trellis loads), then every tile decoded into its
     // MFMA operand
     stage_store_k<NKT, K2>(st, lane, v);
@@ -291,13 +318,12 @@ __global__ void __launch_bounds__(1024) lin_small_kernel(ea_jobs jobs, ea_rot_jo
             *reinterpret_cast<u4v*>(xs + m * XS + 8 * cc) = xv[i];
         }
     }
-    if (ROT && (int)threadIdx.x < cpr) *reinterpret_cast<u4v*>(suh_s + 8 * threadIdx.x) = sv;
+    if (ROT && !PWR && (int)threadIdx.x < cpr) *reinterpret_cast<u4v*>(suh_s + 8 * threadIdx.x) = sv;
     __syncthreads();
-    EA_STAMP(3, threadIdx.x == 0);  // the activations in LDS, every wave's tiles decoded
-    if constexpr (ROT) {
+    EA_STAMP(3, threadIdx.x == 0);  // the activations in LDS (rotated with PWR), every wave's tiles decoded
+    if constexpr (ROT && !PWR) {
         // rotate in place: a wave a (row, Hadamard block), two values a lane (exl3_linear.cu:152-173)
         uint16_t* xh = dptr<uint16_t>(rj.xh[ji]);
-        const int nhb = span >> 7;
         for (int item = wave; item < M * nhb; item += WK) {
             const int m = item / nhb, hb = item - m * nhb;
             uint32_t* p = reinterpret_cast<uint32_t*>(xs + m * XS + hb * 128 + 2 * lane);
@@ -496,6 +522,13 @@ static bool launch_small_k2(const ea_jobs& jobs, const ea_rot_jobs& rj, int bloc
     // 16-byte activation loads a thread: the rows' span over the block's threads
     const int kh = nkt * wk * 16, span_max = ROT ? kh + 256 : kh;
     const int xl = (M * (span_max / 8) + wk * 64 - 1) / (wk * 64);
+    // rotating with at most one (row, Hadamard block) a wave (the blocks' k ranges then start on Hadamard blocks)
+    if constexpr (ROT) {
+        if (kh % 128 == 0 && M * (kh / 128) <= wk) {
+            launch_small_xl<CB, K2, ROT, 0, TAG>(jobs, rj, blocks, s, M, K, wk, nkt, x, x_bf16, lds, status);
+            return true;
+        }
+    }
     if (xl <= 1) launch_small_xl<CB, K2, ROT, 1, TAG>(jobs, rj, blocks, s, M, K, wk, nkt, x, x_bf16, lds, status);
     else if (xl <= 2) launch_small_xl<CB, K2, ROT, 2, TAG>(jobs, rj, blocks, s, M, K, wk, nkt, x, x_bf16, lds, status);
     else if (xl <= 4) launch_small_xl<CB, K2, ROT, 4, TAG>(jobs, rj, blocks, s, M, K, wk, nkt, x, x_bf16, lds, status);
