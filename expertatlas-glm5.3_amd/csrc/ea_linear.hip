@@ -353,10 +353,12 @@ __global__ void __launch_bounds__(1024) lin_small_kernel(ea_jobs jobs, ea_rot_jo
     }
     __syncthreads();  // every wave is done with the staged trellis: the wave sums take its place
     EA_STAMP(5, threadIdx.x == 0);  // every wave's MFMAs done
+    // the rows the call has (lane group lane >> 4 holds rows 4 (lane >> 4) .. + 3); the others are never read
 #pragma unroll
     for (int j = 0; j < 2; ++j)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) red[(wave * 16 + 4 * (lane >> 4) + i) * 32 + j * 16 + row] = acc[j][i];
+        for (int i = 0; i < 4; ++i)
+            if (4 * (lane >> 4) + i < M) red[(wave * 16 + 4 * (lane >> 4) + i) * 32 + j * 16 + row] = acc[j][i];
     __syncthreads();
     if constexpr (TAG) {
         // the block's sums into its tagged slots; the finisher keeps its own in red's first rows (its slots are
