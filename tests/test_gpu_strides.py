@@ -2,7 +2,8 @@
 takes x_stride gives the same bits as on the same rows packed. The gap between rows holds fp16 NaNs, so a read past a
 row's D values would poison the outputs. Covered: moe.routed on a scratch of at most 16 rows (the decode layer), of
 17..128 rows (the prefill path in the scratch's prompt region) and of more (the six-launch sequence);
-ea_ffn_moe_decode with the shared expert (one row and four); prompt_experts.run with and without the pair plane."""
+ea_ffn_moe_decode with the shared expert (one row and four), and fed by the router GEMV; prompt_experts.run with and
+without the pair plane."""
 import numpy as np
 import pytest
 
@@ -104,4 +105,34 @@ def test_prompt_experts_strided_rows(ea, planes):
         np.testing.assert_array_equal(outs[1], outs[0])
     else:  # atomics in arrival order: the same values to fp32 rounding of the order
         np.testing.assert_allclose(outs[1], outs[0], rtol=0, atol=1e-5 * float(np.abs(outs[0]).max()))
+    assert device.device_status() == 0
+
+
+@pytest.mark.parametrize("R", [1, 3])
+def test_ffn_decode_router_strided_rows(ea, R):
+    """ea_ffn_moe_decode_router: the router GEMV reads the rows x_stride apart too; logits, picks and out the same
+    bits as from packed rows."""
+    device, linear, moe, pe, synth = ea
+    E, D, I = 256, 2048, 256
+    rng = np.random.default_rng(3300 + R)
+    rw = synth.bf16_bits((0.02 * rng.standard_normal((E, D))).astype(np.float32))
+    x = synth.activations(3301 + R, R, D, "f16")
+    _, bias = synth.logits(3302, 1)
+    picks = orc.topk8(orc.router(x, rw, 0), bias)[0]
+    host = synth.HostLayer(3303 + R, experts=E, dims=D, width=I, k2=8, only=np.unique(picks))
+    ex = moe.Routed(host)
+    sc = moe.Scratch(ex, 16, 8)
+    drw, db = device.upload(rw), device.upload(bias)
+    got = []
+    for xb, stride in ((x, D), (_strided(x, D), D + PAD)):
+        dx = device.upload(np.ascontiguousarray(xb))
+        dl = device.zeros((R, E), torch.float32)
+        dp, dw = device.zeros((R, 8), torch.int32), device.zeros((R, 8), torch.float32)
+        out = device.zeros((R, D), torch.float32)
+        moe.ffn_decode_router(device.stream(), dx.data_ptr(), stride, drw.data_ptr(), dl.data_ptr(), db.data_ptr(), 2.5,
+                              dp.data_ptr(), dw.data_ptr(), ex, None, sc, out.data_ptr(), R, x_dtype=0)
+        got.append([device.download(t) for t in (dl, dp, dw, out)])
+    for a, b in zip(got[0], got[1]):
+        np.testing.assert_array_equal(b, a)
+    np.testing.assert_array_equal(got[0][1], picks)
     assert device.device_status() == 0
