@@ -1,10 +1,14 @@
 """HIP graph capture of the library's calls through torch.cuda.CUDAGraph: a prefill pass (its two item lists fork
-onto the library's second stream and join back with events, so the capture follows the fork) and a decode layer
-(three launches on the caller's stream). Each is captured once after an eager warm-up and replayed several times,
+onto the library's second stream and join back with events, so the capture follows the fork), the decode layer (one
+launch at one row, five at four), moe.routed on a 40-row window (the prefill path in the scratch's prompt region) and
+the EXL3 linear at one row (the tagged split-K slots, zeroed by each call's finisher) and at 40 rows (the per-pass
+counters, reset by each call's last block). Each is captured once after an eager warm-up and replayed several times,
 with eager work and synchronizations between the replays; every replay must give the eager result bit for bit (both
 paths are deterministic: splits and slots are summed in a fixed order)."""
 import numpy as np
 import pytest
+
+import oracle as orc
 
 pytestmark = pytest.mark.gpu
 torch = pytest.importorskip("torch")
@@ -57,12 +61,11 @@ def test_prefill_graph_replays(ea):
                                                  out.data_ptr(), R, do_round=False), out)
 
 
-def test_decode_layer_graph_replays(ea):
+@pytest.mark.parametrize("R", [1, 4])
+def test_decode_layer_graph_replays(ea, R):
     device, linear, moe, pe, synth = ea
-    R, E, D, I = 1, 256, 2048, 256
-    logits, bias = synth.logits(910, R)
-    import oracle as orc
-
+    E, D, I = 256, 2048, 256
+    logits, bias = synth.logits(910 + R, R)
     pick, _ = orc.topk8(logits, bias)
     host = synth.HostLayer(911, experts=E, dims=D, width=I, k2=8, only=np.unique(pick))
     shapes = [(D, I), (D, I), (I, D)]
@@ -77,3 +80,33 @@ def test_decode_layer_graph_replays(ea):
     _capture_and_replay(device, lambda s: moe.ffn_decode(s, dx.data_ptr(), D, dl.data_ptr(), db.data_ptr(), 2.5,
                                                          dp.data_ptr(), dw.data_ptr(), ex, [l.c for l in lin], sc,
                                                          out.data_ptr(), R, x_dtype=0), out)
+
+
+def test_window_graph_replays(ea):
+    device, linear, moe, pe, synth = ea
+    R, E, D, I, slots = 40, 64, 1024, 256, 8
+    pick = synth.picks_uniform(930, R, E, slots)
+    wts = synth.routing_weights(931, R, slots)
+    host = synth.HostLayer(932, experts=E, dims=D, width=I, k2=8, only=np.unique(pick))
+    ex = moe.Routed(host)
+    sc = moe.Scratch(ex, 64, slots)
+    assert sc.c.fused != 0  # the prompt region
+    x = synth.activations(933, R, D, "f16")
+    dx, dp, dw = device.upload(x), device.upload(pick), device.upload(wts)
+    out = device.zeros((R, D), torch.float32)
+    _capture_and_replay(device, lambda s: moe.routed(s, dx.data_ptr(), D, dp.data_ptr(), dw.data_ptr(), ex, sc,
+                                                     out.data_ptr(), R, x_dtype=0), out)
+
+
+@pytest.mark.parametrize("M", [1, 40])
+def test_linear_graph_replays(ea, M):
+    device, linear, moe, pe, synth = ea
+    K, N = 6144, 256
+    lin = linear.Linear(synth.trellis(940, 0, 0, 0, K, N, 8), synth.scales(941, K, 1.0), synth.scales(942, N, 0.02),
+                        K, N, 8, 1)
+    sc = linear.Scratch(M, K, lin.sk * M * N)
+    x = synth.activations(943 + M, M, K, "f16")
+    dx = device.upload(x)
+    y = device.zeros((M, N), torch.float32)
+    _capture_and_replay(device, lambda s: linear.call(s, sc, [lin], dx.data_ptr(), 0, M, [y.data_ptr()], [2]), y)
+    assert int(device.download(lin.counters).sum()) == 0
