@@ -189,15 +189,20 @@ constexpr int LS_MAXR = 16;
 constexpr int LS_MAXNKT = 16;
 constexpr int LS_FLAGS = 32;  // flag bytes a 128-column block has in the counters (int32 [8 N / 128], zero between calls)
 constexpr int LS_MAXTS = 8;   // tagged splits the finisher polls at once (two slots a lane each)
+constexpr int LS_PASS = 8;    // rows a pass of the tagged form (passes side by side up to 128 rows)
 constexpr uint32_t LS_TAG = 0x7FB5EA1Du;
 constexpr int LS_POLLS = 1 << 20;  // polls before the finisher gives up (tens of milliseconds)
 
 template <int CB, int K2, int NKT, bool ROT, int XL, bool TAG>
-__global__ void __launch_bounds__(1024) lin_small_kernel(ea_jobs jobs, ea_rot_jobs rj, int M, int K, const void* x,
-                                                        int x_bf16, int* status) {
+__global__ void __launch_bounds__(1024) lin_small_kernel(ea_jobs jobs, ea_rot_jobs rj, int M_all, int K,
+                                                        const void* x, int x_bf16, int* status) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     constexpr int TW = 4 * K2;
     EA_STAMP(0, threadIdx.x == 0);  // the block's start
+    // the tagged form takes the call's rows in passes of LS_PASS side by side (blockIdx.y): rows m0 .. m0 + M - 1 of
+    // M_all; the flag form all of them (at most LS_MAXR) in one
+    const int m0 = TAG ? (int)blockIdx.y * LS_PASS : 0;
+    const int M = TAG ? min(LS_PASS, M_all - m0) : M_all;
     int ji = 0;
 #pragma unroll
     for (int q = 1; q < EA_MAX_JOBS; ++q)
@@ -243,13 +248,13 @@ __global__ void __launch_bounds__(1024) lin_small_kernel(ea_jobs jobs, ea_rot_jo
     uint32_t rxw = 0u, rsw = 0u;
     if constexpr (PWR) {
         const int it = wave < M * nhb ? wave : 0, m = it / nhb, hb = it - m * nhb;  // past the items: item 0 again
-        rxw = *reinterpret_cast<const uint32_t*>(xsrc + (size_t)m * K + k_first + hb * 128 + 2 * lane);
+        rxw = *reinterpret_cast<const uint32_t*>(xsrc + (size_t)(m0 + m) * K + k_first + hb * 128 + 2 * lane);
         rsw = *reinterpret_cast<const uint32_t*>(dptr<const uint16_t>(rj.suh[ji]) + k_first + hb * 128 + 2 * lane);
     } else {
 #pragma unroll
         for (int i = 0; i < XL; ++i) {
             const int c = min(i * NT + (int)threadIdx.x, chunks - 1), m = c / cpr, cc = c - m * cpr;
-            xv[i] = *reinterpret_cast<const u4v*>(xsrc + (size_t)m * K + k_first + 8 * cc);
+            xv[i] = *reinterpret_cast<const u4v*>(xsrc + (size_t)(m0 + m) * K + k_first + 8 * cc);
         }
         if constexpr (ROT)
             sv = *reinterpret_cast<const u4v*>(dptr<const uint16_t>(rj.suh[ji]) + k_first +
@@ -283,7 +288,8 @@ __global__ void __launch_bounds__(1024) lin_small_kernel(ea_jobs jobs, ea_rot_jo
             const uint32_t h = (uint32_t)f2h(v0 * HAD_SCALE) | ((uint32_t)f2h(v1 * HAD_SCALE) << 16);
             *reinterpret_cast<uint32_t*>(xs + m * XS + hb * 128 + 2 * lane) = h;
             uint16_t* xh = dptr<uint16_t>(rj.xh[ji]);
-            if (g == 0 && xh) *reinterpret_cast<uint32_t*>(xh + (size_t)m * K + (hb0 + hb) * 128 + 2 * lane) = h;
+            if (g == 0 && xh)
+                *reinterpret_cast<uint32_t*>(xh + (size_t)(m0 + m) * K + (hb0 + hb) * 128 + 2 * lane) = h;
         }
     }
     // the trellis into the wave's LDS region (it waits only for the trellis loads), then every tile decoded into its
@@ -334,7 +340,8 @@ __global__ void __launch_bounds__(1024) lin_small_kernel(ea_jobs jobs, ea_rot_jo
             fwht128_w64(v0, v1, lane);
             const uint32_t h = (uint32_t)f2h(v0 * HAD_SCALE) | ((uint32_t)f2h(v1 * HAD_SCALE) << 16);
             *p = h;
-            if (g == 0 && xh) *reinterpret_cast<uint32_t*>(xh + (size_t)m * K + (hb0 + hb) * 128 + 2 * lane) = h;
+            if (g == 0 && xh)
+                *reinterpret_cast<uint32_t*>(xh + (size_t)(m0 + m) * K + (hb0 + hb) * 128 + 2 * lane) = h;
         }
         __syncthreads();
         EA_STAMP(4, threadIdx.x == 0);  // rotated
@@ -370,7 +377,7 @@ __global__ void __launch_bounds__(1024) lin_small_kernel(ea_jobs jobs, ea_rot_jo
             for (int w = 1; w < WK; ++w) sum += red[(w * 16 + m) * 32 + c];
             red[m * 32 + c] = sum;
             if (!finisher)
-                __hip_atomic_store(Zt + ((size_t)split * M + m) * N + g * 32 + c,
+                __hip_atomic_store(Zt + ((size_t)split * M_all + m0 + m) * N + g * 32 + c,
                                    ((uint64_t)LS_TAG << 32) | __float_as_uint(sum), __ATOMIC_RELAXED,
                                    __HIP_MEMORY_SCOPE_AGENT);
         }
@@ -388,7 +395,7 @@ __global__ void __launch_bounds__(1024) lin_small_kernel(ea_jobs jobs, ea_rot_jo
 #pragma unroll
                 for (int q = 0; q < LS_MAXTS; ++q)
                     if (q < SK && !(own && q == SK - 1)) {
-                        const uint64_t* at = Zt + ((size_t)q * M + m) * N + col;
+                        const uint64_t* at = Zt + ((size_t)q * M_all + m0 + m) * N + col;
                         p[q][0] = __hip_atomic_load(at, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                         p[q][1] = __hip_atomic_load(at + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                         ok &= (uint32_t)(p[q][0] >> 32) == LS_TAG && (uint32_t)(p[q][1] >> 32) == LS_TAG;
@@ -420,13 +427,13 @@ __global__ void __launch_bounds__(1024) lin_small_kernel(ea_jobs jobs, ea_rot_jo
             if (!timed_out)
                 for (int q = 0; q < SK; ++q)
                     if (!(own && q == SK - 1)) {
-                        uint64_t* at = Zt + ((size_t)q * M + m) * N + col;
+                        uint64_t* at = Zt + ((size_t)q * M_all + m0 + m) * N + col;
                         __hip_atomic_store(at, (uint64_t)0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                         __hip_atomic_store(at + 1, (uint64_t)0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                     }
             if (timed_out) acc2 = float2{__builtin_nanf(""), __builtin_nanf("")};  // a writer never arrived
             finish_store_pre(acc2.x, acc2.y, lane, svw, bias != nullptr, bw, dptr<void>(J.y), J.y_dtype,
-                             (size_t)m * N + col);
+                             (size_t)(m0 + m) * N + col);
         }
         EA_STAMP(8, threadIdx.x == 0);  // wave 0's rows finished
         return;
@@ -507,10 +514,11 @@ static size_t lin_small_lds(int M, int K2, int NKT, int WK, bool rot) {
 template <int CB, int K2, bool ROT, int XL, bool TAG>
 static void launch_small_xl(const ea_jobs& jobs, const ea_rot_jobs& rj, int blocks, hipStream_t s, int M, int K, int wk,
                             int nkt, const void* x, int x_bf16, size_t lds, int* status) {
-#define EA_LS(NKT_)                                                                                                   \
-    if (nkt == NKT_) {                                                                                                \
-        lin_small_kernel<CB, K2, NKT_, ROT, XL, TAG><<<blocks, wk * 64, lds, s>>>(jobs, rj, M, K, x, x_bf16, status); \
-        return;                                                                                                       \
+    const dim3 grid((unsigned)blocks, TAG ? (unsigned)((M + LS_PASS - 1) / LS_PASS) : 1u);  // the tagged form's passes
+#define EA_LS(NKT_)                                                                                                 \
+    if (nkt == NKT_) {                                                                                              \
+        lin_small_kernel<CB, K2, NKT_, ROT, XL, TAG><<<grid, wk * 64, lds, s>>>(jobs, rj, M, K, x, x_bf16, status); \
+        return;                                                                                                     \
     }
     EA_LS(2) EA_LS(4) EA_LS(6) EA_LS(8) EA_LS(10) EA_LS(12) EA_LS(14) EA_LS(16)
 #undef EA_LS
@@ -519,14 +527,15 @@ static void launch_small_xl(const ea_jobs& jobs, const ea_rot_jobs& rj, int bloc
 template <int CB, int K2, bool ROT, bool TAG>
 static bool launch_small_k2(const ea_jobs& jobs, const ea_rot_jobs& rj, int blocks, hipStream_t s, int M, int K,
                             int wk, int nkt, const void* x, int x_bf16, int* status) {
-    const size_t lds = lin_small_lds(M, K2, nkt, wk, ROT);
+    const int mp = TAG && M > LS_PASS ? LS_PASS : M;  // the rows a block takes
+    const size_t lds = lin_small_lds(mp, K2, nkt, wk, ROT);
     if (lds > 64 * 1024) return false;
     // 16-byte activation loads a thread: the rows' span over the block's threads
     const int kh = nkt * wk * 16, span_max = ROT ? kh + 256 : kh;
-    const int xl = (M * (span_max / 8) + wk * 64 - 1) / (wk * 64);
+    const int xl = (mp * (span_max / 8) + wk * 64 - 1) / (wk * 64);
     // rotating with at most one (row, Hadamard block) a wave (the blocks' k ranges then start on Hadamard blocks)
     if constexpr (ROT) {
-        if (kh % 128 == 0 && M * (kh / 128) <= wk) {
+        if (kh % 128 == 0 && mp * (kh / 128) <= wk) {
             launch_small_xl<CB, K2, ROT, 0, TAG>(jobs, rj, blocks, s, M, K, wk, nkt, x, x_bf16, lds, status);
             return true;
         }
@@ -553,7 +562,7 @@ static int small_grid(ea_jobs& sj) {
 // 16, a width the staged decode takes, 16-bit activations when rotating); false otherwise, and nothing is launched.
 static bool launch_small(const ea_jobs& jobs, const ea_rot_jobs* rj, hipStream_t s, int M, int K, uint32_t k2,
                          uint32_t cb, int wk, const void* x, int x_dtype, int* status) {
-    if (M > LS_MAXR || k2 > (uint32_t)STAGE_MAXK2) return false;
+    if (M > 128 || k2 > (uint32_t)STAGE_MAXK2) return false;
     if (rj && x_dtype != F16 && x_dtype != BF16) return false;
     const uintptr_t align = rj ? reinterpret_cast<uintptr_t>(x) | (uintptr_t)K * 2 : (uintptr_t)K * 2;
     if (align & 15) return false;  // 16-byte activation loads
@@ -582,11 +591,18 @@ static bool launch_small(const ea_jobs& jobs, const ea_rot_jobs* rj, hipStream_t
         tw *= 2;
         tn /= 2;
     }
+    // the tagged form on sixteen waves; above LS_MAXR rows, when its block's LDS is too large for a pass's rows, on
+    // eight; the flag form up to LS_MAXR rows; otherwise not this kernel
 #define EA_SV(K2_, CB_)                                                                                            \
     if (k2 == K2_ && cb == CB_) {                                                                                  \
         if (tag && (rj ? launch_small_k2<CB_, K2_, true, true>(tj, r, tb, s, M, K, tw, tn, x, bf, status)          \
                        : launch_small_k2<CB_, K2_, false, true>(tj, r, tb, s, M, K, tw, tn, x, bf, status)))       \
             return true;                                                                                           \
+        if (tag && M > LS_MAXR && tw != 2 * wk &&                                                                  \
+            (rj ? launch_small_k2<CB_, K2_, true, true>(tj, r, tb, s, M, K, 2 * wk, nkt, x, bf, status)            \
+                : launch_small_k2<CB_, K2_, false, true>(tj, r, tb, s, M, K, 2 * wk, nkt, x, bf, status)))         \
+            return true;                                                                                           \
+        if (M > LS_MAXR) return false;                                                                             \
         return rj ? launch_small_k2<CB_, K2_, true, false>(sj, r, nb, s, M, K, wk, nkt, x, bf, status)             \
                   : launch_small_k2<CB_, K2_, false, false>(sj, r, nb, s, M, K, wk, nkt, x, bf, status);           \
     }
