@@ -235,8 +235,9 @@ typedef struct ea_linear {
     uint32_t k, n, k2, cb, sk, wk;
 } ea_linear;
 /* linear.zig:142-154 Scratch: xh fp16 [M, K] and z fp32 [SK, M, N] a layer. z must not hold the small-row kernel's
- * tag when first used (zero it once at allocation, as the counters are): calls of up to about 8 rows with an even
- * split count hand their partial sums over in z as tagged 8-byte slots and leave every slot they used zero. Two calls
+ * tag when first used (zero it once at allocation, as the counters are): calls of up to about 8 rows, and of 17 to 128
+ * rows (in passes of 8), with an even split count hand their partial sums over in z as tagged 8-byte slots and leave
+ * every slot they used zero. Two calls
  * that run at once on one z race, as in the reference. A call whose status word then reads EA_SYNC_TIMEOUT (a
  * split's block never stored its slot) leaves its slots as they are: zero z again before the next call on it. */
 typedef struct ea_linear_scratch {
