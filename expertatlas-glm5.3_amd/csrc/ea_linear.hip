@@ -193,6 +193,18 @@ constexpr int LS_PASS = 8;    // rows a pass of the tagged form (passes side by 
 constexpr uint32_t LS_TAG = 0x7FB5EA1Du;
 constexpr int LS_POLLS = 1 << 20;  // polls before the finisher gives up (tens of milliseconds)
 
+// A small-row block's sum of (row m, column c) over its WK (at most 16) waves' sums in red, added in wave order, with
+// every LDS read issued before the first add (a loop over the run-time wave count waited for its reads in turn).
+__device__ __forceinline__ float ls_wave_sum(const float* red, int WK, int m, int c) {
+    float v[16];
+#pragma unroll
+    for (int w = 0; w < 16; ++w) v[w] = red[(min(w, WK - 1) * 16 + m) * 32 + c];
+    float sum = v[0];
+#pragma unroll
+    for (int w = 1; w < 16; ++w) sum = w < WK ? sum + v[w] : sum;
+    return sum;
+}
+
 template <int CB, int K2, int NKT, bool ROT, int XL, bool TAG>
 __global__ void __launch_bounds__(1024) lin_small_kernel(ea_jobs jobs, ea_rot_jobs rj, int M_all, int K,
                                                         const void* x, int x_bf16, int* status) {
@@ -373,8 +385,7 @@ __global__ void __launch_bounds__(1024) lin_small_kernel(ea_jobs jobs, ea_rot_jo
         uint64_t* Zt = dptr<uint64_t>(J.Z);
         for (int idx = threadIdx.x; idx < M * 32; idx += WK * 64) {
             const int m = idx >> 5, c = idx & 31;
-            float sum = red[m * 32 + c];
-            for (int w = 1; w < WK; ++w) sum += red[(w * 16 + m) * 32 + c];
+            const float sum = ls_wave_sum(red, WK, m, c);
             red[m * 32 + c] = sum;
             if (!finisher)
                 __hip_atomic_store(Zt + ((size_t)split * M_all + m0 + m) * N + g * 32 + c,
@@ -441,8 +452,7 @@ __global__ void __launch_bounds__(1024) lin_small_kernel(ea_jobs jobs, ea_rot_jo
     float* Z = dptr<float>(J.Z);
     for (int idx = threadIdx.x; idx < M * 32; idx += WK * 64) {
         const int m = idx >> 5, c = idx & 31;
-        float sum = red[m * 32 + c];
-        for (int w = 1; w < WK; ++w) sum += red[(w * 16 + m) * 32 + c];
+        const float sum = ls_wave_sum(red, WK, m, c);
         st_coh(Z + ((size_t)split * M + m) * N + g * 32 + c, sum);
     }
     stores_done();
