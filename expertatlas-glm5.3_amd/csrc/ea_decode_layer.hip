@@ -1169,13 +1169,13 @@ __device__ __forceinline__ void l1_advance(const DLArgs& a, uint32_t tag, int la
     const int others = (int)gridDim.x - 1;
     const uint32_t* chk = l1_checkin(a);
     for (int n = 0;; ++n) {
+        // every word loaded before any is checked (a check beside each load made each load wait for the one before)
+        uint32_t v[PER];
+#pragma unroll
+        for (int k = 0; k < PER; ++k) v[k] = ld_coh(chk + lane + 64 * k);  // inside the sync words for every k
         bool ok = true;
 #pragma unroll
-        for (int k = 0; k < PER; ++k) {
-            const int i = lane + 64 * k;
-            const uint32_t v = ld_coh(chk + i);  // inside the sync words for every i
-            ok &= i >= others || v == tag;
-        }
+        for (int k = 0; k < PER; ++k) ok &= lane + 64 * k >= others || v[k] == tag;
         if (wave_all(ok)) break;
         if (n >= L1_POLLS) {
             if (lane == 0) record_error(a.status, DEV_SYNC_TIMEOUT);

@@ -205,6 +205,69 @@ __device__ __forceinline__ float ls_wave_sum(const float* red, int WK, int m, in
     return sum;
 }
 
+// The tagged form's finisher (the highest-index block of a 128-column block's blocks): a wave a row of its pass, two
+// columns a lane. Its own split's slots of its own 32 columns (lanes 48..63) come from red, the others are polled;
+// every read slot is set back to zero. TS >= SK splits are loaded each poll, every one before any is checked (loads
+// under a lane condition, or under the split count, made the compiler wait for each split's loads in turn): splits
+// past SK read the last split's slots again, and a lane's own split (never written) is read but not checked.
+template <int TS>
+__device__ __forceinline__ void ls_finish_rows(const ea_job& J, uint64_t* Zt, const float* red, int M_all, int m0,
+                                               int M, int N, int col, int SK, int wave, int WK, int lane, uint32_t svw,
+                                               uint32_t bw, int* status) {
+    const bool own = lane >= 48;
+    for (int m = wave; m < M; m += WK) {
+        uint64_t p[TS][2];
+        bool timed_out = false;
+        for (int n = 0;; ++n) {
+#pragma unroll
+            for (int q = 0; q < TS; ++q) {
+                const uint64_t* at = Zt + ((size_t)min(q, SK - 1) * M_all + m0 + m) * N + col;
+                p[q][0] = __hip_atomic_load(at, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                p[q][1] = __hip_atomic_load(at + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+            bool ok = true;
+#pragma unroll
+            for (int q = 0; q < TS; ++q)
+                ok &= q >= SK || (own && q == SK - 1) ||
+                      ((uint32_t)(p[q][0] >> 32) == LS_TAG && (uint32_t)(p[q][1] >> 32) == LS_TAG);
+            if (__builtin_amdgcn_ballot_w64(!ok) == 0) break;
+            if (n >= LS_POLLS) {
+                timed_out = true;
+                if (lane == 0) record_error(status, DEV_SYNC_TIMEOUT);
+                break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+        }
+        EA_STAMP(7, threadIdx.x == 0);  // wave 0's polls done
+        // the lane's own split (lanes 48..63, the last split) from red: every lane reads red, in bounds
+        const int c = own ? 2 * lane - 96 : 0;
+        const float r0 = red[m * 32 + c], r1 = red[m * 32 + c + 1];
+        const bool own0 = own && SK == 1;
+        float2 acc2 = float2{own0 ? r0 : __uint_as_float((uint32_t)p[0][0]),
+                             own0 ? r1 : __uint_as_float((uint32_t)p[0][1])};
+#pragma unroll
+        for (int q = 1; q < TS; ++q)
+            if (q < SK) {
+                const bool mine = own && q == SK - 1;
+                acc2.x += mine ? r0 : __uint_as_float((uint32_t)p[q][0]);
+                acc2.y += mine ? r1 : __uint_as_float((uint32_t)p[q][1]);
+            }
+        // the slots read go back to zero for the next call. After a give-up they are left as they are: a writer that
+        // arrives late would tag a slot just cleared, and the next call's finisher would take that stale sum for its
+        // own; the status word says EA_SYNC_TIMEOUT instead, and z must be zeroed again before reuse
+        if (!timed_out)
+            for (int q = 0; q < SK; ++q)
+                if (!(own && q == SK - 1)) {
+                    uint64_t* at = Zt + ((size_t)q * M_all + m0 + m) * N + col;
+                    __hip_atomic_store(at, (uint64_t)0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    __hip_atomic_store(at + 1, (uint64_t)0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
+        if (timed_out) acc2 = float2{__builtin_nanf(""), __builtin_nanf("")};  // a writer never arrived
+        finish_store_pre(acc2.x, acc2.y, lane, svw, J.bias != 0, bw, dptr<void>(J.y), J.y_dtype,
+                         (size_t)(m0 + m) * N + col);
+    }
+}
+
 template <int CB, int K2, int NKT, bool ROT, int XL, bool TAG>
 __global__ void __launch_bounds__(1024) lin_small_kernel(ea_jobs jobs, ea_rot_jobs rj, int M_all, int K,
                                                         const void* x, int x_bf16, int* status) {
@@ -395,57 +458,16 @@ __global__ void __launch_bounds__(1024) lin_small_kernel(ea_jobs jobs, ea_rot_jo
         EA_STAMP(6, threadIdx.x == 0);  // thread 0's sums stored (the finisher: kept)
         if (!finisher) return;
         __syncthreads();
-        // the finisher: a wave a row, two columns a lane; its own split's slots of its own 32 columns (lanes 48..63)
-        // come from red, the others are polled; every read slot is set back to zero
-        const bool own = lane >= 48;
-        for (int m = wave; m < M; m += WK) {
-            uint64_t p[LS_MAXTS][2];
-            bool timed_out = false;
-            for (int n = 0;; ++n) {
-                bool ok = true;
-#pragma unroll
-                for (int q = 0; q < LS_MAXTS; ++q)
-                    if (q < SK && !(own && q == SK - 1)) {
-                        const uint64_t* at = Zt + ((size_t)q * M_all + m0 + m) * N + col;
-                        p[q][0] = __hip_atomic_load(at, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                        p[q][1] = __hip_atomic_load(at + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                        ok &= (uint32_t)(p[q][0] >> 32) == LS_TAG && (uint32_t)(p[q][1] >> 32) == LS_TAG;
-                    }
-                if (__builtin_amdgcn_ballot_w64(!ok) == 0) break;
-                if (n >= LS_POLLS) {
-                    timed_out = true;
-                    if (lane == 0) record_error(status, DEV_SYNC_TIMEOUT);
-                    break;
-                }
-                __builtin_amdgcn_s_sleep(1);
-            }
-            EA_STAMP(7, threadIdx.x == 0);  // wave 0's polls done
-            if (own) {
-                const int c = 2 * lane - 96;
-                p[SK - 1][0] = __float_as_uint(red[m * 32 + c]);
-                p[SK - 1][1] = __float_as_uint(red[m * 32 + c + 1]);
-            }
-            float2 acc2 = float2{__uint_as_float((uint32_t)p[0][0]), __uint_as_float((uint32_t)p[0][1])};
-#pragma unroll
-            for (int q = 1; q < LS_MAXTS; ++q)
-                if (q < SK) {
-                    acc2.x += __uint_as_float((uint32_t)p[q][0]);
-                    acc2.y += __uint_as_float((uint32_t)p[q][1]);
-                }
-            // the slots read go back to zero for the next call. After a give-up they are left as they are: a writer
-            // that arrives late would tag a slot just cleared, and the next call's finisher would take that stale sum
-            // for its own; the status word says EA_SYNC_TIMEOUT instead, and z must be zeroed again before reuse
-            if (!timed_out)
-                for (int q = 0; q < SK; ++q)
-                    if (!(own && q == SK - 1)) {
-                        uint64_t* at = Zt + ((size_t)q * M_all + m0 + m) * N + col;
-                        __hip_atomic_store(at, (uint64_t)0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                        __hip_atomic_store(at + 1, (uint64_t)0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    }
-            if (timed_out) acc2 = float2{__builtin_nanf(""), __builtin_nanf("")};  // a writer never arrived
-            finish_store_pre(acc2.x, acc2.y, lane, svw, bias != nullptr, bw, dptr<void>(J.y), J.y_dtype,
-                             (size_t)(m0 + m) * N + col);
-        }
+        // the finisher: a wave a row, two columns a lane (ls_finish_rows), its poll built for the split count rounded
+        // up to a power of two
+        if (SK <= 1)
+            ls_finish_rows<1>(J, Zt, red, M_all, m0, M, N, col, SK, wave, WK, lane, svw, bw, status);
+        else if (SK <= 2)
+            ls_finish_rows<2>(J, Zt, red, M_all, m0, M, N, col, SK, wave, WK, lane, svw, bw, status);
+        else if (SK <= 4)
+            ls_finish_rows<4>(J, Zt, red, M_all, m0, M, N, col, SK, wave, WK, lane, svw, bw, status);
+        else
+            ls_finish_rows<LS_MAXTS>(J, Zt, red, M_all, m0, M, N, col, SK, wave, WK, lane, svw, bw, status);
         EA_STAMP(8, threadIdx.x == 0);  // wave 0's rows finished
         return;
     }
