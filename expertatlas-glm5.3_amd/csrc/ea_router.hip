@@ -38,7 +38,10 @@ __device__ __forceinline__ void act4(uint2 u, bool bf, float (&v)[4]) {
 }
 
 // Block (expert group of EB, row group of RT_ROWS): wave s computes slice s of every (row, expert) of the block.
-template <int EB>
+// ONE (m = 1): the lane's chunks four at a time, every weight and activation load of the four issued before the
+// first product (a chunk past the slice re-reads the slice's last chunk and is not added); the same sums in the same
+// order as the general form, whose loads of a row under `r < rows` wait chunk by chunk.
+template <int EB, bool ONE>
 __global__ void __launch_bounds__(64 * RT_SLICES) router_kernel(const uint16_t* __restrict__ x, int x_bf16,
                                                                 int x_stride, const uint16_t* __restrict__ w,
                                                                 float* __restrict__ part, float* __restrict__ out,
@@ -54,6 +57,29 @@ __global__ void __launch_bounds__(64 * RT_SLICES) router_kernel(const uint16_t* 
 #pragma unroll
         for (int j = 0; j < EB; ++j) acc[r][j] = 0.0f;
     const size_t k_lo = (size_t)s * kw;
+    if constexpr (ONE) {
+        static_assert(EB == 1, "one row: one expert a block");
+        const uint16_t* wr = w + (size_t)e0 * d + k_lo;  // e0 < ne: a block per expert
+        const uint16_t* xr = x + (size_t)m0 * x_stride + k_lo;
+        for (int c0 = 0; c0 < nc; c0 += 4 * 64) {
+            uint2 wu[4], xu[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int c = min(c0 + i * 64 + lane, nc - 1);
+                wu[i] = *reinterpret_cast<const uint2*>(wr + 4 * (size_t)c);
+                xu[i] = *reinterpret_cast<const uint2*>(xr + 4 * (size_t)c);
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                float wv[4], xv[4];
+                act4(wu[i], true, wv);
+                act4(xu[i], bf, xv);
+                if (c0 + i * 64 + lane < nc)
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) acc[0][0] = __builtin_fmaf(xv[q], wv[q], acc[0][0]);
+            }
+        }
+    } else {
 #pragma unroll 3
     for (int c = lane; c < nc; c += 64) {
         const size_t k = k_lo + 4 * (size_t)c;
@@ -75,6 +101,7 @@ __global__ void __launch_bounds__(64 * RT_SLICES) router_kernel(const uint16_t* 
                     for (int i = 0; i < 4; ++i) acc[r][j] = __builtin_fmaf(xv[i], wv[j][i], acc[r][j]);
             }
         }
+    }
     }
 #pragma unroll
     for (int r = 0; r < RT_ROWS; ++r) {
@@ -117,11 +144,14 @@ int launch_router(hipStream_t s, const void* x, int x_dtype, uint32_t x_stride, 
     const unsigned gy = (m + RT_ROWS - 1) / RT_ROWS;
     const auto* xs = static_cast<const uint16_t*>(x);
     const auto* ws = static_cast<const uint16_t*>(w);
-    if (m <= RT_ROWS)
-        router_kernel<1><<<dim3(ne, gy), 64 * RT_SLICES, 0, s>>>(xs, x_dtype == BF16, (int)x_stride, ws, part, out,
-                                                                  (int)m, (int)d, (int)ne);
+    if (m == 1)
+        router_kernel<1, true><<<dim3(ne, gy), 64 * RT_SLICES, 0, s>>>(xs, x_dtype == BF16, (int)x_stride, ws, part,
+                                                                        out, (int)m, (int)d, (int)ne);
+    else if (m <= RT_ROWS)
+        router_kernel<1, false><<<dim3(ne, gy), 64 * RT_SLICES, 0, s>>>(xs, x_dtype == BF16, (int)x_stride, ws, part,
+                                                                         out, (int)m, (int)d, (int)ne);
     else
-        router_kernel<4><<<dim3((ne + 3) / 4, gy), 64 * RT_SLICES, 0, s>>>(xs, x_dtype == BF16, (int)x_stride, ws,
+        router_kernel<4, false><<<dim3((ne + 3) / 4, gy), 64 * RT_SLICES, 0, s>>>(xs, x_dtype == BF16, (int)x_stride, ws,
                                                                             part, out, (int)m, (int)d, (int)ne);
     return launched();
 }
