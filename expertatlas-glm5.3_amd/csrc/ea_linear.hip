@@ -422,19 +422,29 @@ __global__ void __launch_bounds__(1024) lin_small_kernel(ea_jobs jobs, ea_rot_jo
         EA_STAMP(4, threadIdx.x == 0);  // rotated
     }
 
-    // the product: A rows are the activation rows (zero past M), B the decoded tiles
+    // the product: A rows are the activation rows (zero past M), B the decoded tiles. The lanes of the call's rows
+    // read every k step's operand in one branch before the first product (one LDS round trip, not one a step);
+    // the other lanes' operands stay zero.
     const int row = lane & 15;
-    const uint16_t* xr = row < M ? xs + row * XS + xoff + wave * NKT * 16 : nullptr;
+    h8v a[NKT / 2];
+#pragma unroll
+    for (int t = 0; t < NKT / 2; ++t) a[t] = h8v{0, 0, 0, 0, 0, 0, 0, 0};
+    if (row < M) {
+        const uint16_t* xr = xs + row * XS + xoff + wave * NKT * 16;
+#pragma unroll
+        for (int t = 0; t < NKT / 2; ++t) a[t] = load_a8(xr, 2 * t * 16, lane);
+    }
     f4v acc[2] = {f4v{0.f, 0.f, 0.f, 0.f}, f4v{0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
     for (int t = 0; t < NKT; t += 2) {
-        const h8v a = load_a8(xr, t * 16, lane);
 #pragma unroll
         for (int j = 0; j < 2; ++j)
-            acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, __builtin_bit_cast(h8v, bq[t >> 1][j]), acc[j], 0, 0, 0);
+            acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[t >> 1], __builtin_bit_cast(h8v, bq[t >> 1][j]), acc[j],
+                                                            0, 0, 0);
     }
-    __syncthreads();  // every wave is done with the staged trellis: the wave sums take its place
-    EA_STAMP(5, threadIdx.x == 0);  // every wave's MFMAs done
+    // the wave sums take the staged trellis' place in LDS with no barrier first: each wave read only its own staged
+    // tiles, and every wave had decoded them before the barrier above
+    EA_STAMP(5, threadIdx.x == 0);  // this wave's MFMAs done
     // the rows the call has (lane group lane >> 4 holds rows 4 (lane >> 4) .. + 3); the others are never read
 #pragma unroll
     for (int j = 0; j < 2; ++j)
