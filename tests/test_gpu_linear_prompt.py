@@ -53,6 +53,8 @@ def test_unpack_bit_exact(ea, k2, cb):
     (2, 1024, 384, 4, 1, 2),     # 2 bits
     (3, 2048, 512, 12, 2, 2),    # 6-bit mul1 (widths above 10: the register-streaming kernel at any row count)
     (5, 1024, 384, 8, 2, 1),     # 4-bit mul1, bf16 out
+    (1, 8192, 256, 8, 1, 2),     # SK 16: the tagged finisher polls eight splits
+    (3, 8192, 512, 6, 1, 1),     # the same at three rows, 3 bits, bf16 out
 ])
 def test_linear_call(ea, M, K, N, k2, cb, y_dtype):
     device, linear, _, _, synth = ea
