@@ -360,7 +360,7 @@ def test_unsupported_width_poisons_output(ea):
     assert device.device_status() == 0
 
 
-@pytest.mark.parametrize("rows_seq,x_dtype", [([1, 1], 0), ([16, 4], 1)])
+@pytest.mark.parametrize("rows_seq,x_dtype", [([1, 1], 0), ([16, 4], 1), ([1], 1)])
 def test_ffn_decode_from_router(ea, rows_seq, x_dtype):
     """ea_ffn_moe_decode_router: the router's logits (bf16 router weight [256, D], ops.router's ordered slices) written
     to the caller's buffer and then routed, as forward.zig:2350-2403 does. The logits must be the oracle router's bits,
