@@ -81,27 +81,27 @@ __global__ void __launch_bounds__(64 * RT_SLICES) router_kernel(const uint16_t* 
         }
     } else {
 #pragma unroll 3
-    for (int c = lane; c < nc; c += 64) {
-        const size_t k = k_lo + 4 * (size_t)c;
-        uint2 wu[EB];
+        for (int c = lane; c < nc; c += 64) {
+            const size_t k = k_lo + 4 * (size_t)c;
+            uint2 wu[EB];
 #pragma unroll
-        for (int j = 0; j < EB; ++j)
-            wu[j] = e0 + j < ne ? *reinterpret_cast<const uint2*>(w + (size_t)(e0 + j) * d + k) : uint2{0u, 0u};
-        float wv[EB][4];
+            for (int j = 0; j < EB; ++j)
+                wu[j] = e0 + j < ne ? *reinterpret_cast<const uint2*>(w + (size_t)(e0 + j) * d + k) : uint2{0u, 0u};
+            float wv[EB][4];
 #pragma unroll
-        for (int j = 0; j < EB; ++j) act4(wu[j], true, wv[j]);
+            for (int j = 0; j < EB; ++j) act4(wu[j], true, wv[j]);
 #pragma unroll
-        for (int r = 0; r < RT_ROWS; ++r) {
-            if (r < rows) {
-                float xv[4];
-                act4(*reinterpret_cast<const uint2*>(x + (size_t)(m0 + r) * x_stride + k), bf, xv);
+            for (int r = 0; r < RT_ROWS; ++r) {
+                if (r < rows) {
+                    float xv[4];
+                    act4(*reinterpret_cast<const uint2*>(x + (size_t)(m0 + r) * x_stride + k), bf, xv);
 #pragma unroll
-                for (int j = 0; j < EB; ++j)
+                    for (int j = 0; j < EB; ++j)
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) acc[r][j] = __builtin_fmaf(xv[i], wv[j][i], acc[r][j]);
+                        for (int i = 0; i < 4; ++i) acc[r][j] = __builtin_fmaf(xv[i], wv[j][i], acc[r][j]);
+                }
             }
         }
-    }
     }
 #pragma unroll
     for (int r = 0; r < RT_ROWS; ++r) {
@@ -151,8 +151,9 @@ int launch_router(hipStream_t s, const void* x, int x_dtype, uint32_t x_stride, 
         router_kernel<1, false><<<dim3(ne, gy), 64 * RT_SLICES, 0, s>>>(xs, x_dtype == BF16, (int)x_stride, ws, part,
                                                                          out, (int)m, (int)d, (int)ne);
     else
-        router_kernel<4, false><<<dim3((ne + 3) / 4, gy), 64 * RT_SLICES, 0, s>>>(xs, x_dtype == BF16, (int)x_stride, ws,
-                                                                            part, out, (int)m, (int)d, (int)ne);
+        router_kernel<4, false><<<dim3((ne + 3) / 4, gy), 64 * RT_SLICES, 0, s>>>(xs, x_dtype == BF16, (int)x_stride,
+                                                                                   ws, part, out, (int)m, (int)d,
+                                                                                   (int)ne);
     return launched();
 }
 
