@@ -199,14 +199,31 @@ __device__ __forceinline__ void topk8_wave(const float* logits, const float* bia
 // The trellis addresses and widths of every routed unit, into LDS (one round trip for the block, instead of one an
 // item): gate and up, and down for the block that publishes them. Routed from logits, every expert's tables are in
 // LDS already (loaded with the logits) and no round trip is left.
+// Every entry of the three matrices is read (all three tables are always set), before any is stored: reads chosen
+// between LDS and memory by one expression became flat loads that waited one by one.
 __device__ __forceinline__ void route_tables(const DLArgs& a, RouteSh& sh, int mats) {
     for (int u = threadIdx.x; u < sh.ucount; u += DL_THREADS) {
         const int e = sh.uids[u];
+        uint64_t p[3];
+        int k[3];
+        if (a.logits) {
+#pragma unroll
+            for (int m = 0; m < 3; ++m) {
+                p[m] = sh.r.tptr[m][e];
+                k[m] = sh.r.tk2[m][e];
+            }
+        } else {
+#pragma unroll
+            for (int m = 0; m < 3; ++m) {
+                p[m] = (uint64_t)a.ptr[m][e];
+                k[m] = a.k2t[m][e];
+            }
+        }
 #pragma unroll
         for (int m = 0; m < 3; ++m)
             if (m < mats) {
-                sh.uptr[u][m] = a.logits ? sh.r.tptr[m][e] : (uint64_t)a.ptr[m][e];
-                sh.uk2[u][m] = a.logits ? sh.r.tk2[m][e] : a.k2t[m][e];
+                sh.uptr[u][m] = p[m];
+                sh.uk2[u][m] = k[m];
             }
     }
     __syncthreads();
